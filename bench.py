@@ -1,0 +1,232 @@
+#!/usr/bin/env python3
+"""Benchmark of the decode-time fused MoE layer on one MI355X.
+
+Workload: one Mixtral-8x7B-shape MoE layer at batch
+1 -- h=4096, I=14336, E=8, top-2 with renormalised weights, fp16 expert
+weights, fp32 gating and accumulation, x ~ N(0,1) fp32.  A "step" is one call
+of the fused layer (warp_route.functional.fused_moe) on inputs already
+resident in HBM.  Layers rotate over --layers independent random layers
+(default 4, 11.3 GB) so that the 256 MB Infinity Cache holds no reuse between
+calls.
+
+Prints one JSON line: value = microseconds per layer (lower is better),
+roofline = selected-expert weight bytes / layer time against 8 TB/s HBM3E,
+cpu_baseline = the reference's pure-torch MoE (fp32, host cores) timed on a
+bounded sample of the same layer.
+
+  python bench.py [--steps K] [--warmup W] [--layers L] [--config mixtral]
+  python bench.py --copy-probe     # plain device copy, for counter calibration
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "warp-route_amd")]
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = ("µs per MoE layer at batch=1 (Mixtral shape); "
+          "achieved HBM GB/s as % of peak")
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(x, gw, buf, cfg, seconds: float):
+    """The reference's pure-torch MoE (tests/test_python.py:15-37, plus
+    renormalisation) in fp32 on the host, on the same layer: router, softmax,
+    top-k and the selected experts' FFN.  Only the selected experts are
+    materialised as fp32 host tensors (upcast from the same fp16 weights)."""
+    import torch
+    from oracle import moe_oracle as O
+
+    n = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+    xc, gwc = x.float().cpu(), gw.float().cpu()
+    logits = gwc @ xc
+    sel = torch.topk(torch.softmax(logits, 0), k).indices.tolist()
+    es = buf.element_size()
+    stride = O.layout_offsets(E, h, I, es)["expert_stride"] // es
+    nel = I * h
+    gp, up, dp = [None] * E, [None] * E, [None] * E
+    for e in sel:
+        base = e * stride
+        gp[e] = buf[base:base + nel].view(I, h).float().cpu()
+        up[e] = buf[base + nel:base + 2 * nel].view(I, h).float().cpu()
+        dp[e] = buf[base + 2 * nel:base + 3 * nel].view(h, I).float().cpu()
+    for _ in range(2):
+        O.torch_moe_reference_cpu(xc, gwc, gp, up, dp, k, cfg.renormalize)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 1000):
+        t0 = time.perf_counter()
+        O.torch_moe_reference_cpu(xc, gwc, gp, up, dp, k, cfg.renormalize)
+        times.append(time.perf_counter() - t0)
+    med_us = statistics.median(times) * 1e6
+    fp32_bytes = k * 3 * h * I * 4
+    return {
+        "value": round(med_us, 1),
+        "unit": "us/layer",
+        "cores": n,
+        "kind": "port",
+        "sample": (f"{len(times)} calls of one {cfg.name} layer (batch 1, fp32 torch on the host, "
+                   f"median), after 2 warm-ups; {fp32_bytes / med_us / 1e3:.1f} GB/s on the "
+                   f"{fp32_bytes / 1e6:.0f} MB of fp32 selected weights; CPU: {cpu_model()}"),
+    }
+
+
+def copy_probe(nbytes: int, iters: int) -> dict:
+    """Device-to-device copy of nbytes (torch's copy kernel): the achievable
+    streaming ceiling, and the calibration run for FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    src = torch.empty(nbytes // 2, dtype=torch.float16, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(iters):
+        dst.copy_(src)
+    e.record()
+    torch.cuda.synchronize()
+    us = s.elapsed_time(e) * 1e3 / iters
+    return {"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "us_per_copy": round(us, 2),
+            "copy_GBps_read_plus_write": round(2 * nbytes / us / 1e3, 1)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--config", default="mixtral", choices=["mixtral", "deepseek", "dbrx"])
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): the MoE layer is "
+              "benchmarked on a single MI355X; multi-GPU sharding is a design note, not a "
+              "measured configuration.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+
+    if args.copy_probe:
+        print(json.dumps(copy_probe(1 << 30, 50)), flush=True)
+        return 0
+
+    from warp_route import functional as F
+    from warp_route.synthetic import CONFIGS, make_config_layer
+
+    cfg = CONFIGS[args.config]
+    E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+    dev = torch.device("cuda:0")
+    log(f"[bench] generating {args.layers} {cfg.name} layers on the GPU")
+    layers = [make_config_layer(cfg, seed=s, device=dev, gen_device=dev)
+              for s in range(args.layers)]
+    torch.cuda.synchronize()
+
+    # Distinct selected experts per call (always k at batch 1).
+    sel_bytes = cfg.selected_bytes
+    for x, gw, _ in layers:
+        ids, _ = F.gate_topk(x, gw, E, h, k, cfg.renormalize)
+        assert len(set(ids.tolist())) == k
+
+    def step(i):
+        x, gw, buf = layers[i % len(layers)]
+        return F.fused_moe(x, gw, buf, E, h, I, k, cfg.renormalize)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # Whole timed region: K back-to-back calls between two events on the
+    # stream the kernels run on (the current HIP stream).
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(args.steps):
+        step(i)
+    stop.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(stop)
+    us = total_ms * 1e3 / args.steps
+
+    # Per-call distribution (separate pass, events around each call).
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        step(i)
+        b.record()
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+    p10, p50, p90 = (per[int(q * (len(per) - 1))] for q in (0.1, 0.5, 0.9))
+
+    achieved = sel_bytes / (us * 1e-6) / 1e9
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{cfg.name}.json")
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get("hbm_bytes_per_call")
+
+    result = {
+        "metric": METRIC,
+        "value": round(us, 2),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us / 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 weights, f32 accumulate",
+        "data": "synthetic (seeded random-init layers drawn on the GPU)",
+        "config": {"workload": f"{cfg.name} MoE layer, decode batch 1", "hidden": h,
+                   "intermediate": I, "experts": E, "top_k": k,
+                   "renormalize": cfg.renormalize, "weight_dtype": "fp16",
+                   "x_dtype": "fp32", "layers_rotated": args.layers,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic},
+        "per_call_us": {"p10": round(p10, 2), "p50": round(p50, 2), "p90": round(p90, 2)},
+        "selected_bytes_per_call": sel_bytes,
+    }
+    if not args.no_cpu_baseline:
+        x, gw, buf = layers[0]
+        log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s sample)")
+        result["cpu_baseline"] = cpu_baseline(x, gw, buf, cfg, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

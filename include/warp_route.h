@@ -1,0 +1,159 @@
+/*
+ * warp_route.h -- C-ABI of the MI355X (gfx950) decode-time MoE library
+ * (libwarp_route_hip.so).
+ *
+ * This is the drop-in boundary beneath the PyTorch extension `warp_route._C`.
+ * Every entry point takes plain pointers and sizes; there are no C++ or torch
+ * types in the signatures, no exceptions, and no process exit.  Every
+ * argument is validated before any HIP call, so argument errors are
+ * reported as status codes even on a machine without a GPU.
+ *
+ * Semantics shared by all MoE entry points (reference citations are into
+ * anishesg/warp-route):
+ *   logits[e] = sum_i gate_w[e, i] * x[i]                (src/fused_moe.cu:100-112)
+ *   p         = softmax(logits) over all E experts       (src/naive_moe.cu:156-162)
+ *   ids       = k rounds of argmax over unused experts, strict '>', so ties go
+ *               to the lower expert index                (src/naive_moe.cu:164-174)
+ *   w[kk]     = p[ids[kk]], divided by sum_kk p[ids[kk]] when renormalize != 0
+ *               (the reference never renormalises; renormalize = 0 is its
+ *               behaviour)
+ *   out       = sum_kk w[kk] * Wd_e (silu(Wg_e x) * (Wu_e x)),  e = ids[kk]
+ *                                                        (src/fused_moe.cu:167-224)
+ * Gating and accumulation are fp32.  Expert weights are fp32 or fp16 in the
+ * packed expert layout (src/expert_layout.cuh:5-18): per expert
+ * [gate I x h][up I x h][down h x I], row-major, expert stride rounded up to
+ * 128 bytes.
+ *
+ * Streams: work is enqueued asynchronously on `stream` (a hipStream_t passed
+ * as void*, NULL = the null stream).  The reference launched on the legacy
+ * default stream and called cudaDeviceSynchronize (src/bindings.cpp:54-55,
+ * 93-94, 137-140); this library never synchronises the device.  The naive
+ * entry point synchronises `stream` once, for its host-side top-K, as the
+ * reference does (src/naive_moe.cu:197-199).
+ */
+#ifndef WARP_ROUTE_H
+#define WARP_ROUTE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define WR_API __attribute__((visibility("default")))
+#else
+#define WR_API
+#endif
+
+/* Router limits: src/gate.cuh:5 (GATE_MAX_EXPERTS) and src/gate.cuh:7
+ * (GATE_MAX_TOPK).  The reference's fused and batched launchers accept only
+ * top_k in {1, 2} (src/fused_moe.cu:239-242, src/fused_moe_batched.cu:192-195);
+ * here every entry point accepts 1 <= top_k <= min(WR_MAX_TOPK, num_experts). */
+#define WR_MAX_EXPERTS 64
+#define WR_MAX_TOPK 6
+/* Expert stride alignment in bytes: src/expert_layout.cuh:43-45. */
+#define WR_EXPERT_ALIGN 128
+
+typedef enum wr_status {
+  WR_OK = 0,
+  WR_EINVAL_NULL = 1,         /* a required pointer is NULL                    */
+  WR_EINVAL_SHAPE = 2,        /* num_experts, hidden_dim or intermediate_dim < 1 */
+  WR_EINVAL_TOPK = 3,         /* top_k outside [1, min(WR_MAX_TOPK, E)]        */
+  WR_EINVAL_EXPERTS = 4,      /* num_experts > WR_MAX_EXPERTS                  */
+  WR_EINVAL_DTYPE = 5,        /* unknown weight or activation dtype tag        */
+  WR_EINVAL_WEIGHT_SIZE = 6,  /* weight_bytes < total packed layout bytes      */
+  WR_EINVAL_WORKSPACE = 7,    /* workspace NULL or smaller than required       */
+  WR_EINVAL_BATCH = 8,        /* batch_size < 0, or != 1 for a single-token op */
+  WR_EINVAL_KIND = 9,         /* unknown wr_kind                               */
+  WR_EHIP = 100               /* a HIP runtime call failed                     */
+} wr_status;
+
+/* Element type tags. */
+typedef enum wr_dtype { WR_F32 = 0, WR_F16 = 1 } wr_dtype;
+
+/* Which entry point a workspace is sized for. */
+typedef enum wr_kind { WR_KIND_FUSED = 0, WR_KIND_BATCHED = 1, WR_KIND_NAIVE = 2 } wr_kind;
+
+/* Byte offsets within one expert block.  Replaces `ExpertOffsets`
+ * (src/expert_layout.cuh:27-32). */
+typedef struct wr_offsets {
+  int64_t gate_proj_offset;
+  int64_t up_proj_offset;
+  int64_t down_proj_offset;
+  int64_t expert_stride;
+} wr_offsets;
+
+/* Arguments of one MoE call.  Replaces `FusedMoEParams`
+ * (src/fused_moe.cuh:17-22), `BatchedFusedMoEParams`
+ * (src/fused_moe_batched.cuh:18-24) and `NaiveMoEParams`
+ * (src/naive_moe.cuh:17-22) plus their d_hidden/d_output arguments.  All
+ * pointers are device pointers. */
+typedef struct wr_moe_args {
+  const float *gate_w;     /* [E, h] fp32 router, row-major                      */
+  const void *weight_buf;  /* packed experts, element type weight_dtype          */
+  int64_t weight_bytes;    /* bytes readable at weight_buf                       */
+  int32_t weight_dtype;    /* wr_dtype                                           */
+  int32_t num_experts;     /* E                                                  */
+  int32_t hidden_dim;      /* h                                                  */
+  int32_t intermediate_dim;/* I                                                  */
+  int32_t top_k;           /* k                                                  */
+  int32_t renormalize;     /* 0: weights are the softmax probabilities (reference) */
+  int32_t batch_size;      /* B tokens in x and out (1 for fused and naive)      */
+  int32_t act_dtype;       /* wr_dtype of x and out                              */
+  const void *x;           /* [B, h]                                             */
+  void *out;               /* [B, h], fully overwritten                          */
+  int32_t *topk_ids;       /* optional [B, k]: selected experts, descending weight */
+  float *topk_weights;     /* optional [B, k]: their gate weights                */
+  void *workspace;         /* device scratch, >= wr_workspace_bytes(...) bytes   */
+  size_t workspace_bytes;
+} wr_moe_args;
+
+/* Human-readable name of a status code (never NULL). */
+WR_API const char *wr_status_str(int status);
+
+/* Expert block offsets for element size elem_bytes (4 = fp32, 2 = fp16).
+ * Replaces compute_offsets (src/expert_layout.cuh:34-47), which fixed the
+ * element size at sizeof(float). */
+WR_API int wr_layout(int num_experts, int hidden_dim, int intermediate_dim,
+                     int elem_bytes, wr_offsets *out);
+
+/* Total packed bytes of all experts, or -1 for invalid arguments.
+ * Replaces total_weight_bytes (src/expert_layout.cuh:74-77). */
+WR_API int64_t wr_total_weight_bytes(int num_experts, int hidden_dim,
+                                     int intermediate_dim, int elem_bytes);
+
+/* Device workspace an entry point of `kind` needs, or 0 for invalid
+ * arguments.  The reference allocated naive scratch with cudaMalloc on every
+ * call (src/bindings.cpp:53-56, src/naive_moe.cu:24-42); here the caller
+ * provides it (the torch extension takes it from the caching allocator). */
+WR_API size_t wr_workspace_bytes(int kind, int num_experts, int hidden_dim,
+                                 int intermediate_dim, int top_k, int batch_size);
+
+/* Router logits, softmax and top-K for B tokens; writes args->topk_ids and
+ * args->topk_weights (both required here) and nothing else.  The device gate
+ * shared by the fused and batched entry points.  Replaces warp_gate_topk
+ * (src/gate.cu:103-116, declared at src/gate.cuh:21-27). */
+WR_API int wr_gate_topk(const wr_moe_args *args, void *stream);
+
+/* Single-token fused MoE (batch_size must be 1).  Replaces fused_moe_forward
+ * (src/fused_moe.cu:233-263, declared at src/fused_moe.cuh:29-32). */
+WR_API int wr_fused_moe(const wr_moe_args *args, void *stream);
+
+/* B-token fused MoE (batch_size >= 0; 0 is a no-op as in
+ * src/fused_moe_batched.cu:201).  Tokens that share an expert share its weight
+ * reads.  Replaces batched_fused_moe_forward (src/fused_moe_batched.cu:186-214,
+ * declared at src/fused_moe_batched.cuh:30-33). */
+WR_API int wr_batched_fused_moe(const wr_moe_args *args, void *stream);
+
+/* Single-token multi-kernel baseline with host softmax/top-K (batch_size must
+ * be 1).  Synchronises `stream` once.  Replaces naive_moe_forward
+ * (src/naive_moe.cu:181-241, declared at src/naive_moe.cuh:40-44). */
+WR_API int wr_naive_moe(const wr_moe_args *args, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WARP_ROUTE_H */

@@ -1,0 +1,64 @@
+"""Shared helpers for the GPU parity tests: run the oracle on exactly the
+inputs the GPU saw, and compare to the parity bar (ids bit-exact under the
+margin guard; outputs within rtol = atol = 1e-2, plus a tighter relative
+bound where fp32 accumulation allows it)."""
+import numpy as np
+import torch
+
+from oracle import moe_oracle as O
+
+
+def f64(t: torch.Tensor) -> np.ndarray:
+    return t.detach().to("cpu", torch.float64).numpy()
+
+
+def expert_mats(buf: torch.Tensor, e: int, E: int, h: int, I: int):
+    """(gate, up, down) of expert e from a packed buffer on any device, as fp64
+    numpy arrays (expert_views on the flat layout, src/expert_layout.cuh:50-71)."""
+    es = buf.element_size()
+    off = O.layout_offsets(E, h, I, es)
+    base = e * off["expert_stride"] // es
+    n = I * h
+    g = buf[base:base + n].view(I, h)
+    u = buf[base + n:base + 2 * n].view(I, h)
+    d = buf[base + 2 * n:base + 3 * n].view(h, I)
+    return f64(g), f64(u), f64(d)
+
+
+def oracle_token(x: torch.Tensor, gate_w: torch.Tensor, buf: torch.Tensor, E: int, h: int,
+                 I: int, k: int, renorm: bool):
+    """Oracle for one token, fetching only the selected experts."""
+    xn = f64(x)
+    gw = f64(gate_w)
+    logits64 = O.router_logits(gw, xn)
+    probs, ids, ws = O.softmax_topk(logits64.astype(np.float32), k, renorm)
+    m = logits64.max()
+    p64 = np.exp(logits64 - m)
+    p64 /= p64.sum()
+    w64 = p64[ids]
+    if renorm:
+        w64 = w64 / w64.sum()
+    out = np.zeros(h)
+    for kk in range(k):
+        g, u, d = expert_mats(buf, int(ids[kk]), E, h, I)
+        out += w64[kk] * O.expert_ffn(xn, g, u, d)
+    robust = O.selection_is_robust(gw, xn, k)
+    return {"out": out, "ids": ids, "weights": ws, "robust": robust}
+
+
+def assert_parity(got_out, got_ids, got_w, ref, rel_tol=1e-4, w_rtol=1e-5, label=""):
+    """The parity bar: ids bit-exact (the case must pass the margin guard),
+    weights within w_rtol, output within rtol = atol = 1e-2 and within
+    rel_tol of max|ref| (max-abs error, tests/test_correctness.cu:121-130)."""
+    assert ref["robust"], f"{label}: selection not robust to fp32 rounding; pick another seed"
+    if got_ids is not None:
+        np.testing.assert_array_equal(got_ids.cpu().numpy().reshape(-1), ref["ids"],
+                                      err_msg=f"{label}: expert ids")
+    if got_w is not None:
+        np.testing.assert_allclose(got_w.cpu().numpy().reshape(-1), ref["weights"], rtol=w_rtol,
+                                   atol=1e-7, err_msg=f"{label}: gate weights")
+    g = f64(got_out).reshape(-1)
+    np.testing.assert_allclose(g, ref["out"], rtol=1e-2, atol=1e-2, err_msg=f"{label}: output")
+    err = O.relative_error(g, ref["out"])
+    assert err < rel_tol, f"{label}: relative error {err:.3e} >= {rel_tol:.1e}"
+    return err

@@ -1,0 +1,169 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+include/warp_route.h declares, and rejects invalid arguments with the right
+status before any HIP call (each case below has at least one invalid
+argument, so no kernel is ever launched from this file)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from warp_route import capi
+from warp_route import functional as F
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "warp_route.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return re.findall(r"WR_API\s+[\w\s\*]+?\b(wr_\w+)\s*\(", text)
+
+
+def test_header_declares_the_expected_entry_points():
+    assert sorted(declared_symbols()) == sorted([
+        "wr_status_str", "wr_layout", "wr_total_weight_bytes", "wr_workspace_bytes",
+        "wr_gate_topk", "wr_fused_moe", "wr_batched_fused_moe", "wr_naive_moe"])
+
+
+def test_library_exports_every_declared_symbol():
+    lib = capi.lib()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_header_constants_match_binding():
+    text = open(HEADER).read()
+    for name in ("WR_MAX_EXPERTS", "WR_MAX_TOPK", "WR_EXPERT_ALIGN"):
+        m = re.search(rf"#define {name} (\d+)", text)
+        assert int(m.group(1)) == getattr(capi, name)
+    for name in ("WR_OK", "WR_EINVAL_NULL", "WR_EINVAL_SHAPE", "WR_EINVAL_TOPK",
+                 "WR_EINVAL_EXPERTS", "WR_EINVAL_DTYPE", "WR_EINVAL_WEIGHT_SIZE",
+                 "WR_EINVAL_WORKSPACE", "WR_EINVAL_BATCH", "WR_EINVAL_KIND", "WR_EHIP",
+                 "WR_F32", "WR_F16", "WR_KIND_FUSED", "WR_KIND_BATCHED", "WR_KIND_NAIVE"):
+        m = re.search(rf"\b{name} = (\d+)", text)
+        assert m and int(m.group(1)) == getattr(capi, name), name
+
+
+def test_struct_layout_matches_header_order():
+    # 3 pointer-sized fields, 8 int32, 6 pointer-sized: 104 bytes, no padding.
+    assert ctypes.sizeof(capi.WrMoeArgs) == 104
+    assert capi.WrMoeArgs.x.offset == 56
+    assert ctypes.sizeof(capi.WrOffsets) == 32
+
+
+@pytest.mark.parametrize("E,h,I,es", [(8, 4096, 14336, 2), (64, 2048, 1408, 2),
+                                      (16, 6144, 10752, 2), (8, 256, 512, 4), (2, 3, 5, 4),
+                                      (2, 3, 5, 2)])
+def test_layout_agrees_with_python_and_oracle(E, h, I, es):
+    from oracle import moe_oracle as O
+    assert capi.layout(E, h, I, es) == O.layout_offsets(E, h, I, es)
+    assert F.expert_layout(E, h, I, es) == O.layout_offsets(E, h, I, es)
+    assert capi.lib().wr_total_weight_bytes(E, h, I, es) == O.total_weight_bytes(E, h, I, es)
+
+
+def test_layout_rejects_bad_arguments():
+    o = capi.WrOffsets()
+    lib = capi.lib()
+    assert lib.wr_layout(0, 4, 4, 2, ctypes.byref(o)) == capi.WR_EINVAL_SHAPE
+    assert lib.wr_layout(1, 4, 4, 3, ctypes.byref(o)) == capi.WR_EINVAL_DTYPE
+    assert lib.wr_layout(1, 4, 4, 2, None) == capi.WR_EINVAL_NULL
+    assert lib.wr_total_weight_bytes(1, 0, 4, 2) == -1
+
+
+def test_workspace_bytes():
+    lib = capi.lib()
+    # fused: E fp32 logits + k*I fp32 activations, each rounded to 256 bytes
+    assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 4096, 14336, 2, 1) == 256 + 2 * 14336 * 4
+    assert lib.wr_workspace_bytes(capi.WR_KIND_BATCHED, 8, 4096, 14336, 2, 4) == 256 + 8 * 14336 * 4
+    assert lib.wr_workspace_bytes(capi.WR_KIND_NAIVE, 8, 100, 10, 1, 1) == 256 + 3 * 256 + 2 * 512
+    assert lib.wr_workspace_bytes(7, 8, 64, 64, 2, 1) == 0
+    assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 65, 64, 64, 2, 1) == 0
+    assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 64, 64, 0, 1) == 0
+    assert lib.wr_workspace_bytes(capi.WR_KIND_BATCHED, 8, 64, 64, 2, -1) == 0
+
+
+def test_status_strings():
+    for s in range(0, 12):
+        assert capi.status_str(s)
+    assert capi.status_str(capi.WR_EHIP) == "HIP runtime error"
+
+
+FAKE = 0x1000  # never dereferenced: every case below fails validation first
+
+
+def valid_args(B=1):
+    E, h, I, k = 8, 64, 32, 2
+    a = capi.WrMoeArgs()
+    a.gate_w = FAKE
+    a.weight_buf = FAKE
+    a.weight_bytes = capi.lib().wr_total_weight_bytes(E, h, I, 2)
+    a.weight_dtype = capi.WR_F16
+    a.num_experts, a.hidden_dim, a.intermediate_dim, a.top_k = E, h, I, k
+    a.renormalize = 0
+    a.batch_size = B
+    a.act_dtype = capi.WR_F32
+    a.x = FAKE
+    a.out = FAKE
+    a.topk_ids = FAKE
+    a.topk_weights = FAKE
+    a.workspace = FAKE
+    a.workspace_bytes = 1 << 30
+    return a
+
+
+CASES = [
+    ("num_experts", 0, capi.WR_EINVAL_SHAPE),
+    ("hidden_dim", 0, capi.WR_EINVAL_SHAPE),
+    ("intermediate_dim", -3, capi.WR_EINVAL_SHAPE),
+    ("num_experts", 65, capi.WR_EINVAL_EXPERTS),
+    ("top_k", 0, capi.WR_EINVAL_TOPK),
+    ("top_k", 7, capi.WR_EINVAL_TOPK),
+    ("weight_dtype", 2, capi.WR_EINVAL_DTYPE),
+    ("act_dtype", -1, capi.WR_EINVAL_DTYPE),
+    ("gate_w", None, capi.WR_EINVAL_NULL),
+    ("x", None, capi.WR_EINVAL_NULL),
+    ("out", None, capi.WR_EINVAL_NULL),
+    ("weight_buf", None, capi.WR_EINVAL_NULL),
+    ("weight_bytes", 1000, capi.WR_EINVAL_WEIGHT_SIZE),
+    ("workspace", None, capi.WR_EINVAL_WORKSPACE),
+    ("workspace_bytes", 16, capi.WR_EINVAL_WORKSPACE),
+]
+
+
+@pytest.mark.parametrize("entry", ["wr_fused_moe", "wr_batched_fused_moe", "wr_naive_moe"])
+@pytest.mark.parametrize("field,value,want", CASES)
+def test_validation_codes(entry, field, value, want):
+    a = valid_args()
+    setattr(a, field, value)
+    assert capi.call(entry, a) == want
+
+
+def test_top_k_above_num_experts_is_rejected():
+    a = valid_args()
+    a.num_experts, a.top_k = 2, 3
+    a.weight_bytes = 1 << 40
+    assert capi.call("wr_fused_moe", a) == capi.WR_EINVAL_TOPK
+
+
+def test_batch_rules():
+    a = valid_args(B=2)
+    a.weight_bytes = 10  # would fail later; batch is checked first
+    assert capi.call("wr_fused_moe", a) == capi.WR_EINVAL_BATCH
+    assert capi.call("wr_naive_moe", a) == capi.WR_EINVAL_BATCH
+    a.batch_size = -1
+    assert capi.call("wr_batched_fused_moe", a) == capi.WR_EINVAL_BATCH
+    # B == 0 is a no-op, as in src/fused_moe_batched.cu:201 (returns before HIP)
+    a.batch_size = 0
+    assert capi.call("wr_batched_fused_moe", a) == capi.WR_OK
+    assert capi.call("wr_gate_topk", a) == capi.WR_OK
+
+
+def test_gate_topk_requires_outputs():
+    a = valid_args()
+    a.topk_ids = None
+    assert capi.call("wr_gate_topk", a) == capi.WR_EINVAL_NULL
+    a = valid_args()
+    a.topk_weights = None
+    assert capi.call("wr_gate_topk", a) == capi.WR_EINVAL_NULL
+    assert capi.lib().wr_fused_moe(None, None) == capi.WR_EINVAL_NULL

@@ -1,0 +1,290 @@
+"""GPU parity: the HIP kernels (through warp_route._C and the C-ABI) against
+the CPU oracle on the same seeded inputs.
+
+Bar: selected expert ids bit-exact (fp32 gating, ties to
+the lower index; every randomly drawn case must pass the oracle's margin
+guard), gate weights within 1e-5, outputs within rtol = atol = 1e-2, and
+within 1e-4 of max|ref| (max-abs error) where the output is fp32.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+from tests._helpers import assert_parity, f64, oracle_token
+
+import warp_route
+from warp_route import capi
+from warp_route import functional as F
+from warp_route.synthetic import CONFIGS, clustered_batch, make_config_layer, make_layer
+
+pytestmark = pytest.mark.gpu
+
+F32, F16 = torch.float32, torch.float16
+
+# (E, h, I, k, weight dtype, renormalize)
+SMALL = [
+    (8, 256, 512, 1, F32, False),
+    (8, 256, 512, 2, F32, False),
+    (8, 512, 1024, 2, F16, True),
+    (16, 256, 512, 2, F32, True),
+    (8, 1024, 2048, 2, F16, False),
+    (64, 256, 512, 6, F16, False),
+    (16, 512, 256, 4, F32, True),
+    (8, 256, 1408, 6, F16, True),
+    (5, 100, 36, 2, F32, False),   # h % 4 != 0: scalar weight path
+    (5, 100, 36, 2, F16, True),
+    (3, 33, 17, 3, F16, False),    # odd shapes, k == E
+    (1, 64, 64, 1, F16, False),    # single expert
+]
+
+
+def ids_of(c):
+    E, h, I, k, wd, rn = c
+    return f"E{E}-h{h}-I{I}-k{k}-{'f16' if wd == F16 else 'f32'}{'-renorm' if rn else ''}"
+
+
+def robust_layer(E, h, I, wd, k, device, x_dtype=F32, batch=None, seed0=0):
+    """First seed >= seed0 whose selection passes the oracle's margin guard
+    for every token (decided on the CPU before anything runs on the GPU)."""
+    for seed in range(seed0, seed0 + 50):
+        x, gw, buf = make_layer(E, h, I, wd, router_std=h ** -0.5, expert_std=0.05, seed=seed,
+                                batch=batch, device=device, x_dtype=x_dtype)
+        xs = x.float().cpu().double().numpy().reshape(-1, h)
+        gws = gw.cpu().double().numpy()
+        if all(O.selection_is_robust(gws, xs[b], k) for b in range(xs.shape[0])):
+            return x, gw, buf, seed
+    raise AssertionError("no robust seed found")
+
+
+def out_tol(x_dtype):
+    return 2e-3 if x_dtype == F16 else 1e-4
+
+
+@pytest.mark.parametrize("x_dtype", [F32, F16], ids=["xf32", "xf16"])
+@pytest.mark.parametrize("cfg", SMALL, ids=ids_of)
+@pytest.mark.parametrize("op", ["fused", "naive"])
+def test_single_token_parity(cuda, op, cfg, x_dtype):
+    E, h, I, k, wd, rn = cfg
+    x, gw, buf, seed = robust_layer(E, h, I, wd, k, cuda, x_dtype)
+    ids = torch.empty(k, dtype=torch.int32, device=cuda)
+    ws = torch.empty(k, dtype=torch.float32, device=cuda)
+    fn = F.fused_moe if op == "fused" else F.naive_moe
+    print(f"[gpu] {op} {ids_of(cfg)} x={x_dtype} seed={seed}", flush=True)
+    out = fn(x, gw, buf, E, h, I, k, rn, ids, ws)
+    torch.cuda.synchronize()
+    assert out.dtype == x_dtype and out.shape == (h,)
+    ref = oracle_token(x, gw, buf, E, h, I, k, rn)
+    assert_parity(out, ids, ws, ref, rel_tol=out_tol(x_dtype), label=f"{op} {ids_of(cfg)}")
+
+
+@pytest.mark.parametrize("cfg", SMALL, ids=ids_of)
+def test_gate_topk_parity(cuda, cfg):
+    E, h, I, k, wd, rn = cfg
+    x, gw, _, seed = robust_layer(E, h, 8, wd, k, cuda, batch=5)
+    print(f"[gpu] gate_topk {ids_of(cfg)} seed={seed}", flush=True)
+    ids, ws = F.gate_topk(x, gw, E, h, k, rn)
+    torch.cuda.synchronize()
+    for b in range(5):
+        l64 = O.router_logits(f64(gw), f64(x[b]))
+        _, rid, rw = O.softmax_topk(l64.astype(np.float32), k, rn)
+        np.testing.assert_array_equal(ids[b].cpu().numpy(), rid)
+        np.testing.assert_allclose(ws[b].cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("op", ["fused", "naive", "gate"])
+def test_exact_tie_known_answers(cuda, op):
+    """Ties constructed so that GPU and oracle see bit-identical logits."""
+    E, h, I, k = 8, 128, 64, 3
+    _, gw, buf = make_layer(E, h, I, F16, router_std=0.1, seed=1, device=cuda)
+
+    def run(x, g):
+        if op == "gate":
+            return F.gate_topk(x, g, E, h, k)
+        ids = torch.empty(k, dtype=torch.int32, device=cuda)
+        ws = torch.empty(k, dtype=torch.float32, device=cuda)
+        fn = F.fused_moe if op == "fused" else F.naive_moe
+        out = fn(x, g, buf, E, h, I, k, False, ids, ws)
+        return ids, ws, out
+
+    # 1. hidden == 0: all logits exactly 0 -> ids 0..k-1, weights 1/E, output 0.
+    r = run(torch.zeros(h, device=cuda), gw)
+    assert r[0].tolist() == [0, 1, 2]
+    assert torch.all(r[1] == 0.125)
+    if op != "gate":
+        assert torch.all(r[2] == 0)
+    # 2. all router rows identical -> ids 0..k-1 for any x.
+    x = torch.randn(h, device=cuda)
+    same = gw[0:1].expand(E, h).contiguous()
+    assert run(x, same)[0].tolist() == [0, 1, 2]
+    # 3. duplicate rows 2 and 6 forced to the top: 2 must come first.
+    g3 = gw.clone()
+    g3[2] = x / x.norm() * 4.0
+    g3[6] = g3[2]
+    ids3 = run(x, g3)[0].tolist()
+    assert ids3[:2] == [2, 6]
+
+
+@pytest.mark.parametrize("B", [1, 4, 16, 64])
+@pytest.mark.parametrize("cfg", [(8, 256, 512, 1, F32, False), (8, 256, 512, 2, F32, False),
+                                 (16, 512, 1024, 2, F16, True), (64, 256, 512, 6, F16, False)],
+                         ids=ids_of)
+def test_batched_parity(cuda, cfg, B):
+    """Every row equals the oracle and, bit for bit, the single-token op
+    (tests/test_batched.py:33-59)."""
+    E, h, I, k, wd, rn = cfg
+    x, gw, buf, seed = robust_layer(E, h, I, wd, k, cuda, batch=B)
+    ids = torch.empty(B, k, dtype=torch.int32, device=cuda)
+    ws = torch.empty(B, k, dtype=torch.float32, device=cuda)
+    print(f"[gpu] batched {ids_of(cfg)} B={B} seed={seed}", flush=True)
+    out = F.batched_fused_moe(x, gw, buf, E, h, I, k, rn, ids, ws)
+    torch.cuda.synchronize()
+    assert out.shape == (B, h)
+    for b in range(B):
+        ref = oracle_token(x[b], gw, buf, E, h, I, k, rn)
+        assert_parity(out[b], ids[b], ws[b], ref, label=f"batched b={b}")
+        single = F.fused_moe(x[b].contiguous(), gw, buf, E, h, I, k, rn)
+        assert torch.equal(single, out[b]), f"row {b} differs from the single-token op"
+
+
+def test_batched_empty_batch(cuda):
+    E, h, I, k = 8, 64, 64, 2
+    _, gw, buf = make_layer(E, h, I, F16, seed=0, device=cuda)
+    out = F.batched_fused_moe(torch.empty(0, h, device=cuda), gw, buf, E, h, I, k)
+    assert out.shape == (0, h)
+
+
+def test_errors_are_python_exceptions(cuda):
+    E, h, I, k = 8, 64, 64, 2
+    x, gw, buf = make_layer(E, h, I, F16, seed=0, device=cuda)
+    with pytest.raises(RuntimeError, match="weight_buf too small"):
+        F.fused_moe(x, gw, buf[:-1], E, h, I, k)
+    with pytest.raises(RuntimeError, match="top_k"):
+        F.fused_moe(x, gw, buf, E, h, I, 7)
+    with pytest.raises(RuntimeError, match="num_experts"):
+        F.naive_moe(x, torch.randn(65, h, device=cuda), buf, 65, h, I, k)
+    with pytest.raises(RuntimeError, match="gate_w must have shape"):
+        F.fused_moe(x, gw[:4], buf, E, h, I, k)
+    with pytest.raises(RuntimeError, match="float32"):
+        F.fused_moe(x, gw.double(), buf, E, h, I, k)
+    with pytest.raises(ValueError):
+        F.batched_fused_moe(x, gw, buf, E, h, I, k)
+
+
+def test_deterministic(cuda):
+    cfg = CONFIGS["toy"]
+    x, gw, buf = make_config_layer(cfg, seed=0, device=cuda)
+    a = F.fused_moe(x, gw, buf, cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k)
+    b = F.fused_moe(x, gw, buf, cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k)
+    assert torch.equal(a, b)
+
+
+def test_c_abi_direct_call_matches_extension(cuda):
+    """wr_fused_moe through ctypes on torch-owned device memory."""
+    E, h, I, k = 16, 512, 256, 4
+    x, gw, buf, _ = robust_layer(E, h, I, F16, k, cuda)
+    want = F.fused_moe(x, gw, buf, E, h, I, k, True)
+    out = torch.empty_like(x)
+    ids = torch.empty(k, dtype=torch.int32, device=cuda)
+    ws = torch.empty(k, dtype=torch.float32, device=cuda)
+    nws = capi.lib().wr_workspace_bytes(capi.WR_KIND_FUSED, E, h, I, k, 1)
+    work = torch.empty(nws, dtype=torch.uint8, device=cuda)
+    a = capi.WrMoeArgs()
+    a.gate_w, a.weight_buf = gw.data_ptr(), buf.data_ptr()
+    a.weight_bytes = buf.numel() * buf.element_size()
+    a.weight_dtype, a.act_dtype = capi.WR_F16, capi.WR_F32
+    a.num_experts, a.hidden_dim, a.intermediate_dim, a.top_k = E, h, I, k
+    a.renormalize, a.batch_size = 1, 1
+    a.x, a.out = x.data_ptr(), out.data_ptr()
+    a.topk_ids, a.topk_weights = ids.data_ptr(), ws.data_ptr()
+    a.workspace, a.workspace_bytes = work.data_ptr(), nws
+    st = capi.call("wr_fused_moe", a, torch.cuda.current_stream().cuda_stream)
+    assert st == capi.WR_OK, capi.status_str(st)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+
+
+def test_golden_toy_fixture(cuda):
+    """The toy config (seed 0) against the committed fixture."""
+    import json
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "toy_golden.json")
+    gold = json.load(open(path))
+    cfg = CONFIGS["toy"]
+    x, gw, buf = make_config_layer(cfg, seed=0, device=cuda)
+    ids = torch.empty(cfg.top_k, dtype=torch.int32, device=cuda)
+    ws = torch.empty(cfg.top_k, dtype=torch.float32, device=cuda)
+    for fn in (F.fused_moe, F.naive_moe):
+        out = fn(x, gw, buf, cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k,
+                 cfg.renormalize, ids, ws)
+        torch.cuda.synchronize()
+        assert ids.tolist() == gold["ids"]
+        np.testing.assert_allclose(ws.cpu().numpy(), gold["weights"], rtol=1e-5)
+        assert O.relative_error(f64(out), np.array(gold["out"])) < 1e-4
+
+
+def test_moelayer(cuda):
+    torch.manual_seed(0)
+    layer = warp_route.MoELayer(8, 128, 96, top_k=2, renormalize=True,
+                                weight_dtype=torch.float16).to(cuda)
+    x = torch.randn(128, device=cuda)
+    y1 = layer(x)
+    yb = layer(torch.stack([x, -x]))
+    assert torch.equal(yb[0], y1)
+    buf = layer._pack_weights()
+    ref = oracle_token(x, layer.router.data, buf, 8, 128, 96, 2, True)
+    np.testing.assert_allclose(f64(y1), ref["out"], rtol=1e-2, atol=1e-2)
+    with torch.no_grad():
+        layer.down_proj[int(ref["ids"][0])].mul_(2.0)
+    assert layer._pack_weights() is not buf  # in-place change invalidates the pack
+    y2 = layer(x)
+    assert not torch.equal(y2, y1)
+
+
+FULL = ["mixtral", "deepseek", "dbrx"]
+
+
+@pytest.mark.parametrize("name", FULL)
+@pytest.mark.parametrize("op", ["fused", "naive"])
+def test_full_size_configs(cuda, name, op):
+    """BASELINE configs at full size (weights drawn on the GPU), parity on the
+    selected experts."""
+    cfg = CONFIGS[name]
+    E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+    for seed in range(20):
+        x, gw, buf = make_config_layer(cfg, seed=seed, device=cuda, gen_device=cuda)
+        if O.selection_is_robust(f64(gw), f64(x), k):
+            break
+        del buf
+    print(f"[gpu] full {name} {op} seed={seed}", flush=True)
+    ids = torch.empty(k, dtype=torch.int32, device=cuda)
+    ws = torch.empty(k, dtype=torch.float32, device=cuda)
+    fn = F.fused_moe if op == "fused" else F.naive_moe
+    out = fn(x, gw, buf, E, h, I, k, cfg.renormalize, ids, ws)
+    torch.cuda.synchronize()
+    ref = oracle_token(x, gw, buf, E, h, I, k, cfg.renormalize)
+    assert_parity(out, ids, ws, ref, label=f"{name} {op}")
+    del buf
+    torch.cuda.empty_cache()
+
+
+def test_full_size_batched_clustered(cuda):
+    """Batched decode at Mixtral shape with tokens clustered on one expert pair."""
+    cfg = CONFIGS["mixtral"]
+    E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+    _, gw, buf = make_config_layer(cfg, seed=0, device=cuda, gen_device=cuda)
+    B = 16
+    x = clustered_batch(gw, B, pair=(3, 5), alpha=4.0, seed=1, device=cuda)
+    print(f"[gpu] full batched mixtral B={B}", flush=True)
+    ids = torch.empty(B, k, dtype=torch.int32, device=cuda)
+    out = F.batched_fused_moe(x, gw, buf, E, h, I, k, True, ids)
+    torch.cuda.synchronize()
+    pairs = {tuple(sorted(r)) for r in ids.cpu().tolist()}
+    assert (3, 5) in pairs
+    for b in (0, 7, 15):
+        ref = oracle_token(x[b], gw, buf, E, h, I, k, True)
+        assert_parity(out[b], ids[b], None, ref, label=f"clustered b={b}")
+    del buf
+    torch.cuda.empty_cache()

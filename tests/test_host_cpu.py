@@ -1,0 +1,134 @@
+"""Host-side checks without a GPU: the golden fixture still regenerates, the
+Python layer packs exactly like the oracle, and argument errors surface as
+Python exceptions before anything reaches a device."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+
+import warp_route
+from warp_route import functional as F
+from warp_route.synthetic import CONFIGS, make_layer
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def test_golden_fixture_regenerates():
+    from tests.golden import make_golden
+    gold = json.load(open(os.path.join(HERE, "golden", "toy_golden.json")))
+    now = make_golden.compute()
+    assert now["sha256"] == gold["sha256"], "synthetic generator changed"
+    assert now["ids"] == gold["ids"]
+    np.testing.assert_array_equal(now["weights"], gold["weights"])
+    np.testing.assert_allclose(now["out"], gold["out"], rtol=1e-12, atol=0)
+
+
+def test_golden_fixture_agrees_with_reference_test_formula():
+    """The fixture against the reference's pure-torch MoE (tests/test_python.py:15-37)."""
+    gold = json.load(open(os.path.join(HERE, "golden", "toy_golden.json")))
+    c = CONFIGS["toy"]
+    x, gw, buf = make_layer(c.num_experts, c.hidden_dim, c.intermediate_dim, torch.float32,
+                            c.router_std, c.expert_std, seed=0)
+    g, u, d = [], [], []
+    for e in range(c.num_experts):
+        ge, ue, de = O.expert_views(buf.numpy(), e, c.num_experts, c.hidden_dim,
+                                    c.intermediate_dim)
+        g.append(torch.from_numpy(ge.copy()))
+        u.append(torch.from_numpy(ue.copy()))
+        d.append(torch.from_numpy(de.copy()))
+    out, ids, ws = O.torch_moe_reference_cpu(x, gw, g, u, d, c.top_k, c.renormalize)
+    assert ids.tolist() == gold["ids"]
+    assert O.relative_error(out.numpy(), np.array(gold["out"])) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_pack_matches_oracle(dtype):
+    E, h, I = 3, 12, 20
+    g = torch.Generator().manual_seed(0)
+    gp = [torch.randn(I, h, generator=g) for _ in range(E)]
+    up = [torch.randn(I, h, generator=g) for _ in range(E)]
+    dp = [torch.randn(h, I, generator=g) for _ in range(E)]
+    buf = F._pack_expert_weights(gp, up, dp, E, h, I, dtype=dtype)
+    npd = np.float32 if dtype == torch.float32 else np.float16
+    want = O.pack_expert_weights([t.numpy() for t in gp], [t.numpy() for t in up],
+                                 [t.numpy() for t in dp], E, h, I, npd)
+    np.testing.assert_array_equal(buf.numpy(), want)
+    assert buf.dtype == dtype
+
+
+def test_pack_default_is_the_reference_fp32_layout():
+    E, h, I = 2, 4, 6
+    t = [torch.ones(I, h), torch.ones(I, h)]
+    buf = F._pack_expert_weights(t, t, [torch.ones(h, I)] * 2, E, h, I)
+    assert buf.dtype == torch.float32
+    assert buf.numel() * 4 == O.total_weight_bytes(E, h, I, 4)
+
+
+def test_synthetic_generator_draw_order():
+    """x, router, then per expert gate/up/down, all from one generator."""
+    E, h, I = 2, 8, 4
+    x, gw, buf = make_layer(E, h, I, torch.float32, router_std=0.5, expert_std=0.1, seed=3)
+    g = torch.Generator().manual_seed(3)
+    assert torch.equal(x, torch.randn(h, generator=g))
+    assert torch.equal(gw, torch.randn(E, h, generator=g) * 0.5)
+    for e in range(E):
+        ge, ue, de = O.expert_views(buf.numpy(), e, E, h, I)
+        np.testing.assert_array_equal(ge, (torch.randn(I, h, generator=g) * 0.1).numpy())
+        np.testing.assert_array_equal(ue, (torch.randn(I, h, generator=g) * 0.1).numpy())
+        np.testing.assert_array_equal(de, (torch.randn(h, I, generator=g) * 0.1).numpy())
+
+
+def test_config_selected_bytes():
+    assert CONFIGS["mixtral"].selected_bytes == 704_643_072
+    assert CONFIGS["deepseek"].selected_bytes == 103_809_024
+    assert CONFIGS["dbrx"].selected_bytes == 1_585_446_912
+    assert CONFIGS["toy"].selected_bytes == 3_145_728
+
+
+def test_cpu_tensors_are_rejected_before_any_launch():
+    E, h, I, k = 4, 16, 8, 2
+    x, gw, buf = make_layer(E, h, I, torch.float16, seed=0)
+    for fn in (F.fused_moe, F.naive_moe):
+        with pytest.raises(RuntimeError, match="CUDA"):
+            fn(x, gw, buf, E, h, I, k)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        F.batched_fused_moe(x.view(1, h), gw, buf, E, h, I, k)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        F.gate_topk(x, gw, E, h, k)
+
+
+def test_batched_shape_errors_are_value_errors():
+    E, h, I, k = 4, 16, 8, 2
+    x, gw, buf = make_layer(E, h, I, torch.float16, seed=0)
+    with pytest.raises(ValueError, match="2D"):
+        F.batched_fused_moe(x, gw, buf, E, h, I, k)
+    with pytest.raises(ValueError, match="does not match"):
+        F.batched_fused_moe(x.view(2, 8), gw, buf, E, h, I, k)
+
+
+def test_moelayer_argument_checks():
+    with pytest.raises(ValueError):
+        warp_route.MoELayer(8, 16, 16, top_k=7)
+    with pytest.raises(ValueError):
+        warp_route.MoELayer(65, 16, 16, top_k=2)
+    with pytest.raises(ValueError):
+        warp_route.MoELayer(2, 16, 16, top_k=3)
+    layer = warp_route.MoELayer(4, 16, 8, top_k=2)
+    with pytest.raises(ValueError, match="1D or 2D"):
+        layer(torch.zeros(1, 1, 16))
+
+
+def test_moelayer_pack_cache():
+    layer = warp_route.MoELayer(3, 8, 4, top_k=2, weight_dtype=torch.float16)
+    a = layer._pack_weights()
+    assert layer._pack_weights() is a
+    with torch.no_grad():
+        layer.up_proj[1].add_(1.0)
+    b = layer._pack_weights()
+    assert b is not a
+    ge, ue, de = O.expert_views(b.numpy(), 1, 3, 8, 4)
+    np.testing.assert_array_equal(ue, layer.up_proj[1].data.half().numpy())

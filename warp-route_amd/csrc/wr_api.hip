@@ -1,0 +1,191 @@
+// extern "C" boundary of libwarp_route_hip.so (declared in include/warp_route.h).
+//
+// Every entry point validates all arguments before the first HIP call and
+// reports problems as wr_status codes; nothing here exits the process (the
+// reference printed and called exit(1), src/fused_moe.cu:9-15, 239-247).
+// The argument checks mirror the reference's TORCH_CHECKs
+// (src/bindings.cpp:9-23, 35-43, 71-83, 110-125).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "warp_route.h"
+#include "wr_internal.h"
+
+namespace {
+
+using wr::Problem;
+
+int64_t stride_bytes(int64_t E, int64_t h, int64_t I, int64_t es, int64_t* up, int64_t* down) {
+  (void)E;
+  const int64_t gateup = I * h, dn = h * I;
+  const int64_t up_off = gateup * es;
+  const int64_t down_off = up_off + gateup * es;
+  const int64_t raw = down_off + dn * es;
+  if (up) *up = up_off;
+  if (down) *down = down_off;
+  return (raw + WR_EXPERT_ALIGN - 1) / WR_EXPERT_ALIGN * WR_EXPERT_ALIGN;
+}
+
+int check_dims(int E, int h, int I, int k) {
+  if (E < 1 || h < 1 || I < 1) return WR_EINVAL_SHAPE;
+  if (E > WR_MAX_EXPERTS) return WR_EINVAL_EXPERTS;
+  if (k < 1 || k > WR_MAX_TOPK || k > E) return WR_EINVAL_TOPK;
+  return WR_OK;
+}
+
+bool dtype_ok(int d) { return d == WR_F32 || d == WR_F16; }
+
+size_t ws_bytes(int kind, int E, int h, int I, int k, int B) {
+  switch (kind) {
+    case WR_KIND_FUSED:
+      return wr::FusedWs::bytes(E, I, k, 1);
+    case WR_KIND_BATCHED:
+      return wr::FusedWs::bytes(E, I, k, B > 0 ? B : 1);
+    case WR_KIND_NAIVE:
+      return wr::NaiveWs::bytes(E, h, I);
+    default:
+      return 0;
+  }
+}
+
+// Elements per lane per weight access.  The 128-bit path needs every row and
+// every expert block 16-byte aligned (h and I multiples of the vector width,
+// 16-byte aligned weight and activation pointers); anything else takes the
+// scalar path.
+int choose_vec(const wr_moe_args* a) {
+  const int v = a->weight_dtype == WR_F16 ? 8 : 4;
+  if (a->hidden_dim % v != 0 || a->intermediate_dim % v != 0) return 1;
+  if (reinterpret_cast<uintptr_t>(a->weight_buf) % 16 != 0) return 1;
+  if (reinterpret_cast<uintptr_t>(a->x) % 16 != 0) return 1;
+  return v;
+}
+
+// kind: WR_KIND_* or -1 for the gate-only entry point.
+int validate(const wr_moe_args* a, int kind, Problem* p) {
+  if (a == nullptr) return WR_EINVAL_NULL;
+  int st = check_dims(a->num_experts, a->hidden_dim, a->intermediate_dim, a->top_k);
+  if (st != WR_OK) return st;
+  if (!dtype_ok(a->weight_dtype) || !dtype_ok(a->act_dtype)) return WR_EINVAL_DTYPE;
+  const bool single = kind == WR_KIND_FUSED || kind == WR_KIND_NAIVE;
+  if (single ? a->batch_size != 1 : a->batch_size < 0) return WR_EINVAL_BATCH;
+  if (a->batch_size == 0) {
+    p->B = 0;
+    return WR_OK;
+  }
+  if (a->gate_w == nullptr || a->x == nullptr) return WR_EINVAL_NULL;
+  if (kind < 0) {
+    if (a->topk_ids == nullptr || a->topk_weights == nullptr) return WR_EINVAL_NULL;
+  } else {
+    if (a->weight_buf == nullptr || a->out == nullptr) return WR_EINVAL_NULL;
+    const int es = a->weight_dtype == WR_F16 ? 2 : 4;
+    int64_t up = 0, down = 0;
+    const int64_t stride =
+        stride_bytes(a->num_experts, a->hidden_dim, a->intermediate_dim, es, &up, &down);
+    if (a->weight_bytes < stride * a->num_experts) return WR_EINVAL_WEIGHT_SIZE;
+    const size_t need = ws_bytes(kind, a->num_experts, a->hidden_dim, a->intermediate_dim,
+                                 a->top_k, a->batch_size);
+    if (a->workspace == nullptr || a->workspace_bytes < need) return WR_EINVAL_WORKSPACE;
+    p->stride_b = stride;
+    p->off_up_b = up;
+    p->off_down_b = down;
+  }
+  p->gate_w = a->gate_w;
+  p->wbuf = a->weight_buf;
+  p->wdt = a->weight_dtype;
+  p->adt = a->act_dtype;
+  p->E = a->num_experts;
+  p->h = a->hidden_dim;
+  p->I = a->intermediate_dim;
+  p->k = a->top_k;
+  p->renorm = a->renormalize ? 1 : 0;
+  p->B = a->batch_size;
+  p->x = a->x;
+  p->out = a->out;
+  p->topk_ids = a->topk_ids;
+  p->topk_w = a->topk_weights;
+  p->ws = static_cast<char*>(a->workspace);
+  p->ws_bytes = a->workspace_bytes;
+  p->vec = kind < 0 ? 1 : choose_vec(a);
+  return WR_OK;
+}
+
+int hip_status(hipError_t e) { return e == hipSuccess ? WR_OK : WR_EHIP; }
+
+}  // namespace
+
+extern "C" {
+
+WR_API const char* wr_status_str(int status) {
+  switch (status) {
+    case WR_OK: return "ok";
+    case WR_EINVAL_NULL: return "a required pointer is NULL";
+    case WR_EINVAL_SHAPE: return "num_experts, hidden_dim and intermediate_dim must be >= 1";
+    case WR_EINVAL_TOPK: return "top_k must be in [1, min(6, num_experts)]";
+    case WR_EINVAL_EXPERTS: return "num_experts exceeds WR_MAX_EXPERTS (64)";
+    case WR_EINVAL_DTYPE: return "unsupported dtype (weights and activations must be fp32 or fp16)";
+    case WR_EINVAL_WEIGHT_SIZE: return "weight_buf is smaller than the packed expert layout";
+    case WR_EINVAL_WORKSPACE: return "workspace is NULL or smaller than wr_workspace_bytes()";
+    case WR_EINVAL_BATCH: return "invalid batch_size";
+    case WR_EINVAL_KIND: return "unknown workspace kind";
+    case WR_EHIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+WR_API int wr_layout(int num_experts, int hidden_dim, int intermediate_dim, int elem_bytes,
+                     wr_offsets* out) {
+  if (out == nullptr) return WR_EINVAL_NULL;
+  if (num_experts < 1 || hidden_dim < 1 || intermediate_dim < 1) return WR_EINVAL_SHAPE;
+  if (elem_bytes != 2 && elem_bytes != 4) return WR_EINVAL_DTYPE;
+  int64_t up = 0, down = 0;
+  out->expert_stride = stride_bytes(num_experts, hidden_dim, intermediate_dim, elem_bytes, &up, &down);
+  out->gate_proj_offset = 0;
+  out->up_proj_offset = up;
+  out->down_proj_offset = down;
+  return WR_OK;
+}
+
+WR_API int64_t wr_total_weight_bytes(int num_experts, int hidden_dim, int intermediate_dim,
+                                     int elem_bytes) {
+  wr_offsets o;
+  if (wr_layout(num_experts, hidden_dim, intermediate_dim, elem_bytes, &o) != WR_OK) return -1;
+  return (int64_t)num_experts * o.expert_stride;
+}
+
+WR_API size_t wr_workspace_bytes(int kind, int num_experts, int hidden_dim, int intermediate_dim,
+                                 int top_k, int batch_size) {
+  if (check_dims(num_experts, hidden_dim, intermediate_dim, top_k) != WR_OK) return 0;
+  if (batch_size < 0) return 0;
+  return ws_bytes(kind, num_experts, hidden_dim, intermediate_dim, top_k, batch_size);
+}
+
+WR_API int wr_gate_topk(const wr_moe_args* args, void* stream) {
+  Problem p{};
+  const int st = validate(args, -1, &p);
+  if (st != WR_OK || p.B == 0) return st;
+  return hip_status(wr::launch_gate_topk(p, static_cast<hipStream_t>(stream)));
+}
+
+WR_API int wr_fused_moe(const wr_moe_args* args, void* stream) {
+  Problem p{};
+  const int st = validate(args, WR_KIND_FUSED, &p);
+  if (st != WR_OK) return st;
+  return hip_status(wr::launch_fused(p, static_cast<hipStream_t>(stream)));
+}
+
+WR_API int wr_batched_fused_moe(const wr_moe_args* args, void* stream) {
+  Problem p{};
+  const int st = validate(args, WR_KIND_BATCHED, &p);
+  if (st != WR_OK || p.B == 0) return st;
+  return hip_status(wr::launch_batched(p, static_cast<hipStream_t>(stream)));
+}
+
+WR_API int wr_naive_moe(const wr_moe_args* args, void* stream) {
+  Problem p{};
+  const int st = validate(args, WR_KIND_NAIVE, &p);
+  if (st != WR_OK) return st;
+  return hip_status(wr::run_naive(p, static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

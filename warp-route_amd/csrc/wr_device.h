@@ -1,0 +1,208 @@
+// Device-side building blocks shared by the gfx950 MoE kernels: wave64
+// reductions over DPP, the ballot-based top-K gate, 128-bit weight loads and
+// the SwiGLU activation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "warp_route.h"
+
+namespace wr {
+
+constexpr int kWave = 64;
+
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Shape and layout of one MoE problem, passed to kernels by value.  Offsets
+// and the expert stride are in elements of the weight type: the stride is a
+// multiple of 128 bytes (src/expert_layout.cuh:43-45), so it divides evenly.
+struct Geom {
+  int E, h, I, k, renorm, B;
+  int64_t stride, off_up, off_down;
+};
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions.  All 64 lanes must be active.  The in-row steps use
+// quad_perm / row_half_mirror / row_mirror DPP moves; the cross-row steps use
+// row_bcast:15 and row_bcast:31, after which lane 63 holds the total.
+// ---------------------------------------------------------------------------
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_mov(float old, float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                         CTRL, ROW_MASK, 0xf, false));
+}
+
+__device__ __forceinline__ float lane_bcast(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over the wave; the result is returned uniformly to every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_mov<0xb1>(0.0f, v);        // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4e>(0.0f, v);        // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(0.0f, v);       // row_half_mirror
+  v += dpp_mov<0x140>(0.0f, v);       // row_mirror: every lane holds its row sum
+  v += dpp_mov<0x142, 0xa>(0.0f, v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_mov<0x143, 0xc>(0.0f, v);  // row_bcast:31 into rows 2 and 3
+  return lane_bcast(v, 63);
+}
+
+// Max over the wave (IEEE maxNum: a NaN lane never wins), uniform result.
+__device__ __forceinline__ float wave_max(float v) {
+  const float ninf = -__builtin_inff();
+  v = fmaxf(v, dpp_mov<0xb1>(ninf, v));
+  v = fmaxf(v, dpp_mov<0x4e>(ninf, v));
+  v = fmaxf(v, dpp_mov<0x141>(ninf, v));
+  v = fmaxf(v, dpp_mov<0x140>(ninf, v));
+  v = fmaxf(v, dpp_mov<0x142, 0xa>(ninf, v));
+  v = fmaxf(v, dpp_mov<0x143, 0xc>(ninf, v));
+  return lane_bcast(v, 63);
+}
+
+// SiLU(g) = g / (1 + exp(-g)) (src/fused_moe.cu:30-32), with the accurate
+// OCML expf and IEEE division.
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// ---------------------------------------------------------------------------
+// Gate: softmax over E <= 64 logits and top-K, one wave.  Lane e owns expert
+// e.  Each round takes the wave max of the still-available probabilities and
+// the lowest lane holding it (first set bit of a 64-bit ballot), which is the
+// reference's iterative argmax with a strict '>' (src/naive_moe.cu:164-174):
+// ties go to the lower index and a NaN probability is never picked.  If no
+// expert is pickable the round yields expert 0 with weight -FLT_MAX, as the
+// reference loop does.
+// ---------------------------------------------------------------------------
+struct TopK {
+  int id[WR_MAX_TOPK];
+  float w[WR_MAX_TOPK];
+};
+
+__device__ __forceinline__ void wave_select_topk(const float* __restrict__ logits, int E, int k,
+                                                 int renorm, TopK& t) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const bool valid = lane < E;
+  const float l = valid ? logits[lane] : -__builtin_inff();
+  const float m = wave_max(l);
+  const float ex = valid ? expf(l - m) : 0.0f;
+  const float s = wave_sum(ex);
+  const float p = ex / s;
+  bool avail = valid;
+  float tot = 0.0f;
+#pragma unroll
+  for (int kk = 0; kk < WR_MAX_TOPK; ++kk) {
+    t.id[kk] = 0;
+    t.w[kk] = 0.0f;
+    if (kk < k) {
+      const bool cand = avail && (p > -3.402823466e38f);
+      const float best = wave_max(cand ? p : -__builtin_inff());
+      const uint64_t mask = __ballot(cand && p == best);
+      const int id = mask ? (__ffsll((unsigned long long)mask) - 1) : 0;
+      const float wv = mask ? best : -3.402823466e38f;
+      t.id[kk] = __builtin_amdgcn_readfirstlane(id);
+      t.w[kk] = wv;
+      tot += wv;
+      if (lane == id) avail = false;
+    }
+  }
+  if (renorm) {
+#pragma unroll
+    for (int kk = 0; kk < WR_MAX_TOPK; ++kk)
+      if (kk < k) t.w[kk] = t.w[kk] / tot;
+  }
+}
+
+// Runtime-index read of a TopK field without a scratch-memory array.
+__device__ __forceinline__ int topk_id(const TopK& t, int kk) {
+  int r = t.id[0];
+#pragma unroll
+  for (int i = 1; i < WR_MAX_TOPK; ++i) r = (kk == i) ? t.id[i] : r;
+  return r;
+}
+__device__ __forceinline__ float topk_w(const TopK& t, int kk) {
+  float r = t.w[0];
+#pragma unroll
+  for (int i = 1; i < WR_MAX_TOPK; ++i) r = (kk == i) ? t.w[i] : r;
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// Vector loads.  VEC elements per lane: 8 x fp16 or 4 x fp32 is one 128-bit
+// access; VEC = 1 is the scalar path for unaligned shapes.
+// ---------------------------------------------------------------------------
+template <typename T, int VEC>
+struct WVec;
+template <>
+struct WVec<f16, 8> { typedef f16x8 type; };
+template <>
+struct WVec<f16, 1> { typedef f16 type; };
+template <>
+struct WVec<float, 4> { typedef f32x4 type; };
+template <>
+struct WVec<float, 1> { typedef float type; };
+
+// Streaming weight load: read once per call, so mark it non-temporal.
+template <typename T, int VEC>
+__device__ __forceinline__ typename WVec<T, VEC>::type load_w(const T* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const typename WVec<T, VEC>::type*>(p));
+}
+
+template <typename V>
+__device__ __forceinline__ float velem(const V& v, int i) {
+  if constexpr (std::is_same<V, f16>::value || std::is_same<V, float>::value) {
+    return (float)v;
+  } else {
+    return (float)v[i];
+  }
+}
+
+template <typename V>
+__device__ __forceinline__ V vzero() {
+  if constexpr (std::is_same<V, f16>::value || std::is_same<V, float>::value) {
+    return V(0);
+  } else {
+    V z;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(V) / sizeof(z[0])); ++i) z[i] = 0;
+    return z;
+  }
+}
+
+// VEC activation values as fp32 (cached load: reused across rows).
+template <typename XT, int VEC>
+__device__ __forceinline__ void load_x(const XT* __restrict__ p, float (&v)[VEC]) {
+  if constexpr (std::is_same<XT, float>::value && VEC % 4 == 0) {
+#pragma unroll
+    for (int q = 0; q < VEC / 4; ++q) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(p + 4 * q);
+      v[4 * q + 0] = t[0];
+      v[4 * q + 1] = t[1];
+      v[4 * q + 2] = t[2];
+      v[4 * q + 3] = t[3];
+    }
+  } else if constexpr (std::is_same<XT, f16>::value && VEC == 8) {
+    const f16x8 t = *reinterpret_cast<const f16x8*>(p);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (float)t[i];
+  } else if constexpr (std::is_same<XT, f16>::value && VEC == 4) {
+    const f16x4 t = *reinterpret_cast<const f16x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (float)t[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) v[i] = (float)p[i];
+  }
+}
+
+template <typename OT>
+__device__ __forceinline__ OT to_out(float v) {
+  return (OT)v;
+}
+
+}  // namespace wr
