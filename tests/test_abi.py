@@ -73,9 +73,17 @@ def test_layout_rejects_bad_arguments():
 
 def test_workspace_bytes():
     lib = capi.lib()
-    # fused: E fp32 logits + k*I fp32 activations, each rounded to 256 bytes
-    assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 4096, 14336, 2, 1) == 256 + 2 * 14336 * 4
-    assert lib.wr_workspace_bytes(capi.WR_KIND_BATCHED, 8, 4096, 14336, 2, 4) == 256 + 8 * 14336 * 4
+    # fused: control block (64 arrival counters, a timeout flag and an XCD
+    # flag, one 256-byte line each) + 64 fp32 logits per token (E padded to
+    # 64) + act: single token k rows of I rounded up to 8 columns, B > 1
+    # B*k*I; fp32, rounded up to 256 bytes.
+    ctrl = 66 * 256
+    assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 4096, 14336, 2, 1) == (
+        ctrl + 256 + 2 * 14336 * 4)
+    assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 64, 100, 3, 1) == (
+        ctrl + 256 + 1280)  # 3 * 104 * 4 = 1248 -> 1280
+    assert lib.wr_workspace_bytes(capi.WR_KIND_BATCHED, 8, 4096, 14336, 2, 4) == (
+        ctrl + 4 * 256 + 8 * 14336 * 4)
     assert lib.wr_workspace_bytes(capi.WR_KIND_NAIVE, 8, 100, 10, 1, 1) == 256 + 3 * 256 + 2 * 512
     assert lib.wr_workspace_bytes(7, 8, 64, 64, 2, 1) == 0
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 65, 64, 64, 2, 1) == 0

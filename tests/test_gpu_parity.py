@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import moe_oracle as O
-from tests._helpers import assert_parity, f64, oracle_token
+from tests._helpers import assert_parity, assert_same_up_to_order, f64, oracle_token
 
 import warp_route
 from warp_route import capi
@@ -132,8 +132,8 @@ def test_exact_tie_known_answers(cuda, op):
                                  (16, 512, 1024, 2, F16, True), (64, 256, 512, 6, F16, False)],
                          ids=ids_of)
 def test_batched_parity(cuda, cfg, B):
-    """Every row equals the oracle and, bit for bit, the single-token op
-    (tests/test_batched.py:33-59)."""
+    """Every row equals the oracle and the single-token op up to summation
+    order, with identical ids and weights (tests/test_batched.py:33-59)."""
     E, h, I, k, wd, rn = cfg
     x, gw, buf, seed = robust_layer(E, h, I, wd, k, cuda, batch=B)
     ids = torch.empty(B, k, dtype=torch.int32, device=cuda)
@@ -145,8 +145,11 @@ def test_batched_parity(cuda, cfg, B):
     for b in range(B):
         ref = oracle_token(x[b], gw, buf, E, h, I, k, rn)
         assert_parity(out[b], ids[b], ws[b], ref, label=f"batched b={b}")
-        single = F.fused_moe(x[b].contiguous(), gw, buf, E, h, I, k, rn)
-        assert torch.equal(single, out[b]), f"row {b} differs from the single-token op"
+        s_ids = torch.empty(k, dtype=torch.int32, device=cuda)
+        s_ws = torch.empty(k, dtype=torch.float32, device=cuda)
+        single = F.fused_moe(x[b].contiguous(), gw, buf, E, h, I, k, rn, s_ids, s_ws)
+        assert torch.equal(s_ids, ids[b]) and torch.equal(s_ws, ws[b]), f"row {b} selection"
+        assert_same_up_to_order(out[b], single, label=f"row {b} vs single-token op")
 
 
 def test_batched_empty_batch(cuda):
@@ -206,6 +209,83 @@ def test_c_abi_direct_call_matches_extension(cuda):
     assert torch.equal(out, want)
 
 
+def _fused_args(x, gw, buf, E, h, I, k, out, work, renorm=0):
+    a = capi.WrMoeArgs()
+    a.gate_w, a.weight_buf = gw.data_ptr(), buf.data_ptr()
+    a.weight_bytes = buf.numel() * buf.element_size()
+    a.weight_dtype = capi.WR_F16
+    a.act_dtype = capi.WR_F16 if x.dtype == torch.float16 else capi.WR_F32
+    a.num_experts, a.hidden_dim, a.intermediate_dim, a.top_k = E, h, I, k
+    a.renormalize, a.batch_size = renorm, 1
+    a.x, a.out = x.data_ptr(), out.data_ptr()
+    a.workspace, a.workspace_bytes = work.data_ptr(), work.numel()
+    return a
+
+
+@pytest.mark.parametrize("shape", [(16, 512, 256, 4), (8, 4096, 14336, 2), (64, 2048, 1408, 6),
+                                   (8, 192, 100, 3)],
+                         ids=["small", "mixtral", "deepseek", "ragged"])
+def test_fused_handoff_never_times_out(cuda, shape):
+    """Single-token fused kernel: every gate/up block incremented its arrival
+    counter (64 counters, 256 bytes apart; gate/up blocks = act chunks
+    k * ceil(ceil(I / 2) / 4) rounded up to a multiple of 32) and no down
+    block's bounded wait expired (timeout word after the counters).  The
+    workspace starts as junk: the router kernel must zero the control block on
+    every call.  The XCD flag (next word) says whether blocks ran on the XCDs
+    the act layout expects; either value gives correct results."""
+    E, h, I, k = shape
+    x, gw, buf = make_layer(E, h, I, F16, router_std=h ** -0.5, seed=2, device=cuda,
+                            gen_device=cuda)
+    nws = capi.lib().wr_workspace_bytes(capi.WR_KIND_FUSED, E, h, I, k, 1)
+    work = torch.full((nws,), 0xAB, dtype=torch.uint8, device=cuda)
+    out = torch.empty_like(x)
+    a = _fused_args(x, gw, buf, E, h, I, k, out, work)
+    n1 = (k * (((I + 1) // 2 + 3) // 4) + 31) // 32 * 32
+    for _ in range(3):
+        assert capi.call("wr_fused_moe", a, torch.cuda.current_stream().cuda_stream) == 0
+        torch.cuda.synchronize()
+        words = work[:66 * 256].view(torch.int32).cpu()
+        counters = words[0:64 * 64:64]
+        assert int(words[64 * 64]) == 0, "a down block's wait expired"
+        assert int(words[65 * 64]) in (0, 1)
+        assert counters.tolist() == [(n1 - c + 63) // 64 for c in range(64)]
+    print(f"[gpu] handoff {shape}: gate/up blocks {n1}, xcd flag {int(words[65 * 64])}")
+    ref = oracle_token(x, gw, buf, E, h, I, k, False)
+    np.testing.assert_allclose(f64(out), ref["out"], rtol=1e-2, atol=1e-2)
+    del buf
+    torch.cuda.empty_cache()
+
+
+def test_fused_workspace_reused_across_layers(cuda):
+    """Two different layers called alternately through ONE workspace (the act
+    lines sit at the same addresses every call) give, call after call, exactly
+    the outputs each layer gives through a fresh workspace.  A down block that
+    read act values left by the previous call would break the equality."""
+    E, h, I, k = 8, 1024, 2048, 2
+    layers = [make_layer(E, h, I, F16, router_std=h ** -0.5, seed=s, device=cuda,
+                         gen_device=cuda) for s in (11, 12)]
+    want = []
+    for x, gw, buf in layers:
+        fresh = torch.zeros(capi.lib().wr_workspace_bytes(capi.WR_KIND_FUSED, E, h, I, k, 1),
+                            dtype=torch.uint8, device=cuda)
+        o = torch.empty_like(x)
+        assert capi.call("wr_fused_moe", _fused_args(x, gw, buf, E, h, I, k, o, fresh),
+                         torch.cuda.current_stream().cuda_stream) == 0
+        want.append(o)
+    torch.cuda.synchronize()
+    assert not torch.equal(want[0], want[1])
+    shared = torch.empty_like(fresh)
+    outs = [torch.empty_like(layers[0][0]) for _ in range(40)]
+    stream = torch.cuda.current_stream().cuda_stream
+    for i, o in enumerate(outs):
+        x, gw, buf = layers[i % 2]
+        assert capi.call("wr_fused_moe", _fused_args(x, gw, buf, E, h, I, k, o, shared),
+                         stream) == 0
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        assert torch.equal(o, want[i % 2]), f"call {i}"
+
+
 def test_golden_toy_fixture(cuda):
     """The toy config (seed 0) against the committed fixture."""
     import json
@@ -232,7 +312,7 @@ def test_moelayer(cuda):
     x = torch.randn(128, device=cuda)
     y1 = layer(x)
     yb = layer(torch.stack([x, -x]))
-    assert torch.equal(yb[0], y1)
+    assert_same_up_to_order(yb[0], y1, label="batched row vs single token")
     buf = layer._pack_weights()
     ref = oracle_token(x, layer.router.data, buf, 8, 128, 96, 2, True)
     np.testing.assert_allclose(f64(y1), ref["out"], rtol=1e-2, atol=1e-2)

@@ -84,11 +84,12 @@ struct TopK {
   float w[WR_MAX_TOPK];
 };
 
-__device__ __forceinline__ void wave_select_topk(const float* __restrict__ logits, int E, int k,
-                                                 int renorm, TopK& t) {
+// `l` is this lane's logit (lane e holds expert e; lanes >= E are ignored).
+__device__ __forceinline__ void wave_select_topk_reg(float l_in, int E, int k, int renorm,
+                                                     TopK& t) {
   const int lane = threadIdx.x & (kWave - 1);
   const bool valid = lane < E;
-  const float l = valid ? logits[lane] : -__builtin_inff();
+  const float l = valid ? l_in : -__builtin_inff();
   const float m = wave_max(l);
   const float ex = valid ? expf(l - m) : 0.0f;
   const float s = wave_sum(ex);
@@ -116,6 +117,45 @@ __device__ __forceinline__ void wave_select_topk(const float* __restrict__ logit
     for (int kk = 0; kk < WR_MAX_TOPK; ++kk)
       if (kk < k) t.w[kk] = t.w[kk] / tot;
   }
+}
+
+// Same, reading the E logits of one token from memory.  The reads are
+// wave-uniform scalar loads: every wave of a persistent grid reads the same
+// line at kernel start, and through the scalar cache that costs one L2
+// request per CU instead of one per wave (which serialises on one L2 channel).
+// `logits` must have WR_MAX_EXPERTS readable floats (entries >= E are ignored).
+__device__ __forceinline__ void wave_select_topk(const float* __restrict__ logits, int E, int k,
+                                                 int renorm, TopK& t) {
+  const int lane = threadIdx.x & (kWave - 1);
+  float l = 0.0f;
+#pragma unroll
+  for (int e = 0; e < WR_MAX_EXPERTS; ++e) {
+    const float v = __builtin_bit_cast(
+        float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, logits[e])));
+    l = (lane == e) ? v : l;
+  }
+  wave_select_topk_reg(l, E, k, renorm, t);
+}
+
+// Contiguous share [begin, end) of `total` items for worker w of n; shares
+// differ in size by at most one item.
+__device__ __forceinline__ void share(int total, int w, int n, int& begin, int& end) {
+  begin = (int)((int64_t)total * w / n);
+  end = (int)((int64_t)total * (w + 1) / n);
+}
+
+// Hardware id of the XCD (accelerator complex die) this wave runs on
+// (HW_REG_XCC_ID bits [3:0]).  Each XCD has its own L2.
+__device__ __forceinline__ unsigned xcc_id() {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 15u;
+}
+
+// Invalidate this CU's vector L1 and wait for it.  The CU's later loads then
+// fetch from L2.
+__device__ __forceinline__ void invalidate_l1() {
+  asm volatile("buffer_inv sc0\n\ts_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Runtime-index read of a TopK field without a scratch-memory array.

@@ -32,15 +32,40 @@ constexpr size_t kWsAlign = 256;
 
 // Workspace carving.  Every region starts on a 256-byte boundary.
 struct FusedWs {
-  float* logits;  // [B][E]
-  float* act;     // [B][k][I], already scaled by the gate weight
+  // Single-token hand-off, one 256-byte line per word: kCounters arrival
+  // counters, the wait-timeout flag, and the flag "a gate/up block ran on an
+  // unexpected XCD".  The router kernel of each single-token call zeroes them.
+  static constexpr int kCounters = 64;
+  static constexpr int kCounterStride = 64;  // words (256 bytes)
+  static constexpr int kTimeoutWord = kCounters * kCounterStride;
+  static constexpr int kXccFlagWord = kTimeoutWord + kCounterStride;
+  static constexpr int kCtrlWords = kCounters + 2;  // zeroed words, kCounterStride apart
+  static constexpr size_t kCtrlBytes = (size_t)kCtrlWords * kCounterStride * 4;
+  // act rows are I rounded up to whole 8-column chunks.
+  static constexpr int kActCols = 8;
+
+  unsigned* ctrl;  // kCtrlBytes
+  float* logits;   // [B][WR_MAX_EXPERTS]: token b's E logits, padded to 64
+  float* act;      // B == 1: [k][act_row(I)]; B > 1: [B][k][I].
+                   // Values are already scaled by the gate weight.
+
+  __host__ __device__ static int64_t act_row(int I) {
+    return (int64_t)((I + kActCols - 1) / kActCols) * kActCols;
+  }
+  static size_t act_floats(int I, int k, int B) {
+    return B == 1 ? (size_t)k * act_row(I) : (size_t)B * k * I;
+  }
   static size_t bytes(int E, int I, int k, int B) {
-    return align_up((size_t)B * E * 4, kWsAlign) + align_up((size_t)B * k * I * 4, kWsAlign);
+    (void)E;
+    return kCtrlBytes + (size_t)B * WR_MAX_EXPERTS * 4 +
+           align_up(act_floats(I, k, B) * 4, kWsAlign);
   }
   static FusedWs carve(char* ws, int E, int I, int k, int B) {
     FusedWs w;
-    w.logits = reinterpret_cast<float*>(ws);
-    w.act = reinterpret_cast<float*>(ws + align_up((size_t)B * E * 4, kWsAlign));
+    w.ctrl = reinterpret_cast<unsigned*>(ws);
+    w.logits = reinterpret_cast<float*>(ws + kCtrlBytes);
+    w.act = reinterpret_cast<float*>(ws + kCtrlBytes + (size_t)B * WR_MAX_EXPERTS * 4);
+    (void)E;
     (void)I;
     (void)k;
     return w;

@@ -1,98 +1,144 @@
 // Fused decode-time MoE kernels for gfx950 (wave64).
 //
-// The layer is three streaming passes over HBM-resident data:
-//   1. k_router_logits: one wave per (expert, token) computes the router dot
-//      product (src/fused_moe.cu:100-112) into the workspace.
-//   2. k_gateup: every wave re-derives the top-K selection from the logits
-//      (wave_select_topk; a few dozen instructions), then streams RPW rows of
-//      the selected expert's gate and up matrices with 128-bit non-temporal
-//      loads, reduces each row across the wave and writes
+// The layer is three streaming passes:
+//   1. k_router_logits: one 4-wave workgroup per (expert, token) computes the
+//      router dot product (src/fused_moe.cu:100-112); each wave covers a
+//      quarter of the row, so one memory round trip covers it.
+//   2. k_gateup: a persistent grid of waves.  Each wave derives the top-K
+//      selection from the logits once (wave_select_topk: DPP max/sum and a
+//      64-bit ballot), then streams a contiguous share of the selected
+//      experts' gate/up rows with 128-bit non-temporal loads, RPW rows of
+//      each matrix at a time, reduces every row across the wave and writes
 //      act = w_kk * silu(gate . x) * (up . x) in fp32
 //      (src/fused_moe.cu:192-201, silu at :30-32).
-//   3. k_down: a workgroup owns RPD output rows; its four waves split the
-//      concatenated k*I columns of the selected down matrices, accumulate in
-//      fp32 registers, combine through LDS and write each output row once
-//      (src/fused_moe.cu:203-224, without the reference's repeated global
-//      read-modify-write of the output).
-// Bytes that matter are the selected expert weights; x, logits and act are
-// small and served from L2.  The batched entry point runs the same kernels
-// with one grid row (blockIdx.y) per token.
+//   3. k_down: a persistent grid of waves; each wave owns whole output rows,
+//      streams those rows of every selected down matrix (contiguous I-long
+//      spans), accumulates sum_kk Wd_kk[r,:] . act_kk in fp32 registers and
+//      writes the row once (src/fused_moe.cu:203-224, without the reference's
+//      repeated global read-modify-write of the output).
+// The selected expert weights are the only large traffic; x, logits and act
+// are small and served from cache.  Work shares are contiguous row ranges
+// that differ by at most one item, and the grid is sized so that no wave
+// gets more items than necessary (balanced tail).
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdlib>
 
 #include "wr_device.h"
 #include "wr_internal.h"
+
+#ifndef WR_GU_RPW
+#define WR_GU_RPW 2  // gate/up rows per matrix in flight per wave
+#endif
+#ifndef WR_GU_U
+#define WR_GU_U 4    // 64*VEC-element chunks per row per iteration
+#endif
+#ifndef WR_DN_RPD
+#define WR_DN_RPD 2  // down rows per wave item
+#endif
+#ifndef WR_DN_U
+#define WR_DN_U 4
+#endif
+#ifndef WR_FU_RPD
+#define WR_FU_RPD 4  // single-token fused kernel: output rows per down block
+#endif
+#ifndef WR_FU_U
+#define WR_FU_U 4    // single-token fused kernel: column chunks per down tile
+#endif
+#ifndef WR_WAVES_PER_CU
+#define WR_WAVES_PER_CU 8  // persistent waves per CU (upper bound)
+#endif
 
 namespace wr {
 
 constexpr int kBlock = 256;  // 4 waves
 constexpr int kWavesPerBlock = kBlock / kWave;
 
-// One wave's fp32 dot product of a router row with x.  Shared by every
-// kernel that produces logits so that all of them produce identical bits.
+// ---------------------------------------------------------------------------
+// Router
+// ---------------------------------------------------------------------------
+// Wave q (0..3) of a 4-wave group: fp32 partial dot over quarter q of the row
+// (quarters are whole 64*VEC-element chunks).  Every producer of logits uses
+// this and the same combine order, so all of them produce identical bits.
 template <typename XT, int VEC>
-__device__ __forceinline__ float wave_router_dot(const float* __restrict__ row,
-                                                 const XT* __restrict__ x, int h) {
+__device__ __forceinline__ float router_partial(const float* __restrict__ row,
+                                                const XT* __restrict__ x, int h, int q) {
   const int lane = threadIdx.x & (kWave - 1);
-  float acc0 = 0.0f, acc1 = 0.0f;
-  int c = lane * VEC;
-  for (; c + kWave * VEC < h; c += 2 * kWave * VEC) {
-    float w0[VEC], x0[VEC], w1[VEC], x1[VEC];
-    load_x<float, VEC>(row + c, w0);
-    load_x<XT, VEC>(x + c, x0);
-    load_x<float, VEC>(row + c + kWave * VEC, w1);
-    load_x<XT, VEC>(x + c + kWave * VEC, x1);
+  constexpr int CH = kWave * VEC;
+  const int span = (h + 4 * CH - 1) / (4 * CH) * CH;
+  const int beg = q * span;
+  const int end = min(h, beg + span);
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = beg + lane * VEC; c0 < end; c0 += 8 * CH) {
+    float w[8][VEC], xv[8][VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      acc0 = fmaf(w0[i], x0[i], acc0);
-      acc1 = fmaf(w1[i], x1[i], acc1);
+    for (int u = 0; u < 8; ++u) {
+      const int c = c0 + u * CH;
+      if (c < end) {
+        load_x<float, VEC>(row + c, w[u]);
+        load_x<XT, VEC>(x + c, xv[u]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) w[u][i] = xv[u][i] = 0.0f;
+      }
     }
-  }
-  if (c < h) {
-    float w0[VEC], x0[VEC];
-    load_x<float, VEC>(row + c, w0);
-    load_x<XT, VEC>(x + c, x0);
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) acc0 = fmaf(w0[i], x0[i], acc0);
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[u & 3] = fmaf(w[u][i], xv[u][i], acc[u & 3]);
   }
-  return wave_sum(acc0 + acc1);
+  return wave_sum((acc[0] + acc[1]) + (acc[2] + acc[3]));
 }
 
-// grid (ceil(E / 4), B), block 256: wave w of block bx computes expert
-// 4*bx + w for token blockIdx.y.
+__device__ __forceinline__ float router_combine(const float* p) {
+  return (p[0] + p[1]) + (p[2] + p[3]);
+}
+
+// grid (E, B), block 256.  Token b's logits go to logits[b * 64 + e] (padded
+// so that consumers can read all 64 with scalar loads).  Block (0, 0) also
+// zeroes the words zero[i * zstride], i < nzero (the fused kernel's arrival
+// counters and timeout flag), which the next kernel on the stream reads.
 template <typename XT, int VEC>
 __global__ __launch_bounds__(kBlock) void k_router_logits(const float* __restrict__ gate_w,
                                                           const XT* __restrict__ x,
                                                           float* __restrict__ logits, int E,
-                                                          int h) {
-  const int wave = threadIdx.x / kWave;
-  const int e = blockIdx.x * kWavesPerBlock + wave;
-  const int b = blockIdx.y;
-  if (e >= E) return;  // wave-uniform
-  const float v = wave_router_dot<XT, VEC>(gate_w + (int64_t)e * h, x + (int64_t)b * h, h);
-  if ((threadIdx.x & (kWave - 1)) == 0) logits[(int64_t)b * E + e] = v;
+                                                          int h, unsigned* __restrict__ zero,
+                                                          int nzero, int zstride) {
+  __shared__ float part[4];
+  const int q = threadIdx.x / kWave;
+  const int e = blockIdx.x, b = blockIdx.y;
+  if (zero != nullptr && e == 0 && b == 0 && (int)threadIdx.x < nzero)
+    zero[(int64_t)threadIdx.x * zstride] = 0u;
+  const float p = router_partial<XT, VEC>(gate_w + (int64_t)e * h, x + (int64_t)b * h, h, q);
+  if ((threadIdx.x & (kWave - 1)) == 0) part[q] = p;
+  __syncthreads();
+  if (threadIdx.x == 0) logits[(int64_t)b * WR_MAX_EXPERTS + e] = router_combine(part);
 }
 
-// Standalone gate: grid B, block 1024.  Logits go through LDS; wave 0 selects
-// and writes ids/weights.  Same per-expert dot as k_router_logits.
+// Standalone gate: grid B, block 1024 (four 4-wave groups).  Group g handles
+// experts g, g+4, ...; wave 0 then selects and writes ids and weights.
 template <typename XT, int VEC>
 __global__ __launch_bounds__(1024) void k_gate_topk(const float* __restrict__ gate_w,
                                                     const XT* __restrict__ x, int E, int h,
                                                     int k, int renorm,
                                                     int32_t* __restrict__ ids_out,
                                                     float* __restrict__ w_out) {
-  __shared__ float lg[WR_MAX_EXPERTS];
+  __shared__ float part[WR_MAX_EXPERTS][4];
   const int wave = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int g = wave / 4, q = wave % 4;
   const int b = blockIdx.x;
-  for (int e = wave; e < E; e += nw) {
-    const float v = wave_router_dot<XT, VEC>(gate_w + (int64_t)e * h, x + (int64_t)b * h, h);
-    if ((threadIdx.x & (kWave - 1)) == 0) lg[e] = v;
+  for (int e = g; e < E; e += 4) {
+    const float p = router_partial<XT, VEC>(gate_w + (int64_t)e * h, x + (int64_t)b * h, h, q);
+    if (lane == 0) part[e][q] = p;
   }
   __syncthreads();
   if (wave == 0) {
+    const float l = lane < E ? router_combine(part[lane]) : 0.0f;
     TopK t;
-    wave_select_topk(lg, E, k, renorm, t);
-    const int lane = threadIdx.x;
+    wave_select_topk_reg(l, E, k, renorm, t);
 #pragma unroll
     for (int kk = 0; kk < WR_MAX_TOPK; ++kk) {
       if (kk < k && lane == kk) {
@@ -103,25 +149,31 @@ __global__ __launch_bounds__(1024) void k_gate_topk(const float* __restrict__ ga
   }
 }
 
-// grid (ceil(k * ceil(I / RPW) / 4), B), block 256.  Global wave gw handles
-// rows [r0, r0 + RPW) of selected expert kk.
+// ---------------------------------------------------------------------------
+// Gate/up: grid (ceil(nw / 4), B).  Wave w of token b owns items
+// share(k * ceil(I / RPW), w, nw); item it covers rows [r0, r0 + RPW) of
+// selected expert kk = it / ceil(I / RPW).
+// ---------------------------------------------------------------------------
 template <typename WT, typename XT, int VEC, int RPW, int U>
 __global__ __launch_bounds__(kBlock) void k_gateup(const WT* __restrict__ wbuf,
                                                    const XT* __restrict__ x,
                                                    const float* __restrict__ logits,
                                                    float* __restrict__ act,
                                                    int32_t* __restrict__ ids_out,
-                                                   float* __restrict__ w_out, Geom g) {
+                                                   float* __restrict__ w_out, Geom g, int nw) {
   typedef typename WVec<WT, VEC>::type V;
+  constexpr int CH = kWave * VEC;
   const int lane = threadIdx.x & (kWave - 1);
   const int b = blockIdx.y;
-  const int gw = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  const int w = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  if (w >= nw) return;  // wave-uniform
   const int items = (g.I + RPW - 1) / RPW;
-  if (gw >= g.k * items) return;  // wave-uniform
+  int ib, ie;
+  share(g.k * items, w, nw, ib, ie);
 
   TopK t;
-  wave_select_topk(logits + (int64_t)b * g.E, g.E, g.k, g.renorm, t);
-  if (gw == 0) {
+  wave_select_topk(logits + (int64_t)b * WR_MAX_EXPERTS, g.E, g.k, g.renorm, t);
+  if (w == 0) {
 #pragma unroll
     for (int kk = 0; kk < WR_MAX_TOPK; ++kk) {
       if (kk < g.k && lane == kk) {
@@ -130,26 +182,206 @@ __global__ __launch_bounds__(kBlock) void k_gateup(const WT* __restrict__ wbuf,
       }
     }
   }
-
-  const int kk = gw / items;
-  const int r0 = (gw - kk * items) * RPW;
-  const int e = topk_id(t, kk);
-  const float wk = topk_w(t, kk);
-  const WT* G = wbuf + (int64_t)e * g.stride + (int64_t)r0 * g.h;
-  const WT* Up = G + g.off_up;
   const XT* xb = x + (int64_t)b * g.h;
-  const int nrows = min(RPW, g.I - r0);
 
+  for (int it = ib; it < ie; ++it) {
+    const int kk = it / items;
+    const int r0 = (it - kk * items) * RPW;
+    const int e = topk_id(t, kk);
+    const WT* G = wbuf + (int64_t)e * g.stride + (int64_t)r0 * g.h;
+    const WT* Up = G + g.off_up;
+    const int nrows = min(RPW, g.I - r0);
+
+    float ag[RPW], au[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) ag[j] = au[j] = 0.0f;
+
+    for (int c0 = lane * VEC; c0 < g.h; c0 += U * CH) {
+      V wg[U][RPW], wu[U][RPW];
+      float xv[U][VEC];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * CH;
+        const bool ok = c < g.h;
+#pragma unroll
+        for (int j = 0; j < RPW; ++j) {
+          const bool okj = ok && j < nrows;
+          wg[u][j] = okj ? load_w<WT, VEC>(G + (int64_t)j * g.h + c) : vzero<V>();
+          wu[u][j] = okj ? load_w<WT, VEC>(Up + (int64_t)j * g.h + c) : vzero<V>();
+        }
+        if (ok) {
+          load_x<XT, VEC>(xb + c, xv[u]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) xv[u][i] = 0.0f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int j = 0; j < RPW; ++j)
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            ag[j] = fmaf(velem(wg[u][j], i), xv[u][i], ag[j]);
+            au[j] = fmaf(velem(wu[u][j], i), xv[u][i], au[j]);
+          }
+    }
+
+    const float wk = topk_w(t, kk);
+    float* a = act + ((int64_t)b * g.k + kk) * g.I + r0;
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+      const float gs = wave_sum(ag[j]);
+      const float us = wave_sum(au[j]);
+      if (lane == 0 && j < nrows) a[j] = wk * (silu(gs) * us);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Down: grid (ceil(nw / 4), B).  Wave w of token b owns output-row items
+// share(ceil(h / RPD), w, nw); for each it streams rows [r0, r0 + RPD) of
+// every selected down matrix against that expert's act vector.
+// ---------------------------------------------------------------------------
+template <typename WT, typename OT, int VEC, int RPD, int U>
+__global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
+                                                 const float* __restrict__ logits,
+                                                 const float* __restrict__ act,
+                                                 OT* __restrict__ out, Geom g, int nw) {
+  typedef typename WVec<WT, VEC>::type V;
+  constexpr int CH = kWave * VEC;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int b = blockIdx.y;
+  const int w = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  if (w >= nw) return;  // wave-uniform
+  int ib, ie;
+  share((g.h + RPD - 1) / RPD, w, nw, ib, ie);
+
+  TopK t;
+  wave_select_topk(logits + (int64_t)b * WR_MAX_EXPERTS, g.E, g.k, g.renorm, t);
+  const float* ab = act + (int64_t)b * g.k * g.I;
+
+  for (int it = ib; it < ie; ++it) {
+    const int r0 = it * RPD;
+    const int nrows = min(RPD, g.h - r0);
+    float acc[RPD];
+#pragma unroll
+    for (int j = 0; j < RPD; ++j) acc[j] = 0.0f;
+
+    for (int kk = 0; kk < g.k; ++kk) {
+      const WT* D = wbuf + (int64_t)topk_id(t, kk) * g.stride + g.off_down + (int64_t)r0 * g.I;
+      const float* a = ab + (int64_t)kk * g.I;
+      for (int c0 = lane * VEC; c0 < g.I; c0 += U * CH) {
+        V wv[U][RPD];
+        float av[U][VEC];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int c = c0 + u * CH;
+          const bool ok = c < g.I;
+#pragma unroll
+          for (int j = 0; j < RPD; ++j)
+            wv[u][j] = (ok && j < nrows) ? load_w<WT, VEC>(D + (int64_t)j * g.I + c) : vzero<V>();
+          if (ok) {
+            load_x<float, VEC>(a + c, av[u]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) av[u][i] = 0.0f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int j = 0; j < RPD; ++j)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) acc[j] = fmaf(velem(wv[u][j], i), av[u][i], acc[j]);
+      }
+    }
+
+#pragma unroll
+    for (int j = 0; j < RPD; ++j) {
+      const float s = wave_sum(acc[j]);
+      if (lane == 0 && j < nrows) out[(int64_t)b * g.h + r0 + j] = to_out<OT>(s);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Single-token fused FFN: ONE launch, grid = [n1 gate/up blocks][n2 down
+// blocks], 4 waves per block.
+//
+// act is [k][act_row] fp32, in 8-column chunks; chunk G = kk * bpk + j holds
+// columns [8 j, 8 j + 8) of selected expert kk (bpk = chunks per expert).
+// Gate/up block b computes chunk G = chunk_of_block(b): its wave w computes
+// rows 8 j + 2 w and 8 j + 2 w + 1 of expert kk's gate and up matrices and
+// stores w_kk * silu(gate . x) * (up . x) with agent-scope stores, which are
+// written through to memory.  When all of them have completed, the block
+// increments arrival counter b mod 64 (the counters sit 256 bytes apart so
+// that their atomics do not serialise on one address).
+//
+// Down block: owns RPD output rows.  It issues the loads of its first tile of
+// down weights (they do not depend on act), then wave 0 polls the 64 counters
+// until all n1 gate/up blocks have arrived, then the 4 waves stream strided
+// column chunks of every selected down matrix and combine in LDS.  Every
+// output row is written once.
+//
+// Why this cannot deadlock: workgroups of a grid are dispatched in index
+// order (on each XCD), so every gate/up block is dispatched before any down
+// block that could occupy its slot, and gate/up blocks never wait.  Every wait
+// is nevertheless bounded (about 0.2 s); on expiry the block records a
+// timeout flag and finishes, so the kernel cannot hang.
+//
+// Why down blocks read fresh act without invalidating L2 (each XCD has its
+// own L2, not coherent with the others): blocks are dispatched to the XCDs
+// round-robin, block b to XCD b mod 8.  chunk_of_block maps the four blocks
+// 32 m + 8 s + x (s = 0..3), which share XCD x, to the four chunks
+// 32 m + 4 x + s, i.e. one 128-byte L2 line.  So every act line is written by
+// one XCD only.  At kernel start no L2 holds act lines (the kernel-boundary
+// acquire invalidates them), and no wave reads act before every gate/up block
+// has arrived.  Hence an XCD's L2 holds an act line only if its own writers
+// put it there (all of the line's writers go through that L2) or if a reader
+// fetched it from memory after it was complete.  Each gate/up block checks the
+// XCD it actually runs on (HW_REG_XCC_ID) and, if it is not b mod 8, raises a
+// flag; down blocks then fall back to a full agent-scope acquire (L2 and L1
+// invalidate).  Otherwise a down block only invalidates its CU's L1, in case
+// a writer on the same CU left a partial line there.  This saves the L2
+// invalidate per down block (about 6 us per layer at the Mixtral shape) and
+// keeps act dense, so the readers' loads stay fully coalesced.
+// ---------------------------------------------------------------------------
+struct Handoff {
+  unsigned* cnt;        // FusedWs::kCounters counters, FusedWs::kCounterStride words apart
+  unsigned* timeout;    // set to 1 if a wait expired (results then invalid)
+  unsigned* xcc_flag;   // set to 1 if a gate/up block ran on another XCD than b mod 8
+  int n1;               // gate/up blocks (the first n1 block ids), a multiple of 32
+  int chunks;           // k * bpk
+  unsigned spin_limit;  // polls before a wait gives up
+};
+
+// The chunk gate/up block b computes (a permutation of each aligned group of
+// 32 blocks).
+__host__ __device__ __forceinline__ int chunk_of_block(int b) {
+  return (b & ~31) + ((b & 7) << 2) + ((b >> 3) & 3);
+}
+
+// Rows [r0, r0 + RPW) of selected expert kk's gate/up matrices; the results go
+// to a[0 .. RPW) with agent-scope stores.
+template <typename WT, typename XT, int VEC, int RPW, int U>
+__device__ __forceinline__ void gateup_item(const WT* __restrict__ wbuf, const XT* __restrict__ xb,
+                                            float* a, const Geom& g, const TopK& t, int kk,
+                                            int r0, int lane) {
+  typedef typename WVec<WT, VEC>::type V;
+  constexpr int CH = kWave * VEC;
+  const WT* G = wbuf + (int64_t)topk_id(t, kk) * g.stride + (int64_t)r0 * g.h;
+  const WT* Up = G + g.off_up;
+  const int nrows = min(RPW, g.I - r0);
   float ag[RPW], au[RPW];
 #pragma unroll
   for (int j = 0; j < RPW; ++j) ag[j] = au[j] = 0.0f;
-
-  for (int c0 = lane * VEC; c0 < g.h; c0 += U * kWave * VEC) {
+  for (int c0 = lane * VEC; c0 < g.h; c0 += U * CH) {
     V wg[U][RPW], wu[U][RPW];
     float xv[U][VEC];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int c = c0 + u * kWave * VEC;
+      const int c = c0 + u * CH;
       const bool ok = c < g.h;
 #pragma unroll
       for (int j = 0; j < RPW; ++j) {
@@ -165,108 +397,178 @@ __global__ __launch_bounds__(kBlock) void k_gateup(const WT* __restrict__ wbuf,
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int j = 0; j < RPW; ++j) {
+      for (int j = 0; j < RPW; ++j)
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
           ag[j] = fmaf(velem(wg[u][j], i), xv[u][i], ag[j]);
           au[j] = fmaf(velem(wu[u][j], i), xv[u][i], au[j]);
         }
-      }
-    }
   }
-
-  float* a = act + ((int64_t)b * g.k + kk) * g.I + r0;
+  const float wk = topk_w(t, kk);
 #pragma unroll
   for (int j = 0; j < RPW; ++j) {
     const float gs = wave_sum(ag[j]);
     const float us = wave_sum(au[j]);
-    if (lane == 0 && j < nrows) a[j] = wk * (silu(gs) * us);
+    if (lane == 0 && j < nrows)
+      __hip_atomic_store(a + j, wk * (silu(gs) * us), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
-// grid (ceil(h / RPD), B), block 256.  Block owns output rows [r0, r0+RPD)
-// of token blockIdx.y; wave w takes column chunks w, w+4, ... of the
-// concatenated k * I columns (chunk = 64 * VEC columns inside one expert).
-template <typename WT, typename OT, int VEC, int RPD, int U>
-__global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
-                                                 const float* __restrict__ logits,
-                                                 const float* __restrict__ act,
-                                                 OT* __restrict__ out, Geom g) {
+// Down tile of a fused down block: U column chunks q = q0 + 4 u (chunk q is
+// columns [(q mod nch) * 64 VEC, +64 VEC) of selected expert q / nch), RPD rows
+// from r0.
+template <typename WT, int VEC, int RPD, int U>
+__device__ __forceinline__ void down_tile_load(typename WVec<WT, VEC>::type (&wv)[U][RPD],
+                                               const WT* __restrict__ wbuf, const Geom& g,
+                                               const TopK& t, int r0, int nrows, int q0,
+                                               int nch, int lane) {
   typedef typename WVec<WT, VEC>::type V;
-  __shared__ float part[kWavesPerBlock][RPD];
+  const int C = g.k * nch;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int q = q0 + u * kWavesPerBlock;
+    const int kk = q / nch;
+    const int c = (q - kk * nch) * kWave * VEC + lane * VEC;
+    const bool ok = q < C && c < g.I;
+    const WT* D = wbuf + (int64_t)topk_id(t, ok ? kk : 0) * g.stride + g.off_down +
+                  (int64_t)r0 * g.I + c;
+#pragma unroll
+    for (int j = 0; j < RPD; ++j)
+      wv[u][j] = (ok && j < nrows) ? load_w<WT, VEC>(D + (int64_t)j * g.I) : vzero<V>();
+  }
+}
+
+// acc[j] += tile row j . act over the tile's chunks (act of expert kk at
+// act + kk * act_row).
+template <typename V, int VEC, int RPD, int U>
+__device__ __forceinline__ void down_tile_fma(float (&acc)[RPD], const V (&wv)[U][RPD],
+                                              const float* act, const Geom& g,
+                                              int64_t act_row, int q0, int nch, int lane) {
+  const int C = g.k * nch;
+  float av[U][VEC];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int q = q0 + u * kWavesPerBlock;
+    const int kk = q / nch;
+    const int c = (q - kk * nch) * kWave * VEC + lane * VEC;
+    if (q < C && c < g.I) {
+      load_x<float, VEC>(act + kk * act_row + c, av[u]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) av[u][i] = 0.0f;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int j = 0; j < RPD; ++j)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[j] = fmaf(velem(wv[u][j], i), av[u][i], acc[j]);
+}
+
+template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2>
+__global__ __launch_bounds__(kBlock) void k_fused_ffn(
+    const WT* __restrict__ wbuf, const XT* __restrict__ x, const float* __restrict__ logits,
+    float* act, XT* __restrict__ out, int32_t* __restrict__ ids_out, float* __restrict__ w_out,
+    Geom g, Handoff hs) {
+  typedef typename WVec<WT, VEC>::type V;
+  static_assert(kWavesPerBlock * RPW == FusedWs::kActCols, "a gate/up block computes one chunk");
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int b = blockIdx.y;
-  const int r0 = blockIdx.x * RPD;
-  const int nrows = min(RPD, g.h - r0);
+  const int64_t act_row = FusedWs::act_row(g.I);
 
   TopK t;
-  wave_select_topk(logits + (int64_t)b * g.E, g.E, g.k, g.renorm, t);
+  wave_select_topk(logits, g.E, g.k, g.renorm, t);
 
+  if ((int)blockIdx.x < hs.n1) {
+    // ---- gate/up block ----
+    if (blockIdx.x == 0 && wave == 0) {
+#pragma unroll
+      for (int kk = 0; kk < WR_MAX_TOPK; ++kk) {
+        if (kk < g.k && lane == kk) {
+          if (ids_out != nullptr) ids_out[kk] = t.id[kk];
+          if (w_out != nullptr) w_out[kk] = t.w[kk];
+        }
+      }
+    }
+    const int items = (g.I + RPW - 1) / RPW;
+    const int bpk = (items + kWavesPerBlock - 1) / kWavesPerBlock;  // chunks per expert
+    const int G = chunk_of_block(blockIdx.x);
+    if (G < hs.chunks) {
+      const int kk = G / bpk;
+      const int it = (G - kk * bpk) * kWavesPerBlock + wave;
+      if (it < items)
+        gateup_item<WT, XT, VEC, RPW, U1>(wbuf, x, act + kk * act_row + it * RPW, g, t, kk,
+                                          it * RPW, lane);
+    }
+    if (threadIdx.x == 0 && xcc_id() != (blockIdx.x & 7u))
+      __hip_atomic_store(hs.xcc_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's act stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0)
+      __hip_atomic_fetch_add(hs.cnt + (blockIdx.x % FusedWs::kCounters) * FusedWs::kCounterStride,
+                             1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+
+  // ---- down block ----
+  __shared__ float part[kWavesPerBlock][RPD];
+  const int r0 = ((int)blockIdx.x - hs.n1) * RPD;
+  const int nrows = min(RPD, g.h - r0);
   const int nch = (g.I + kWave * VEC - 1) / (kWave * VEC);
   const int C = g.k * nch;
-  const float* ab = act + (int64_t)b * g.k * g.I;
+
+  V pre[U2][RPD];
+  down_tile_load<WT, VEC, RPD, U2>(pre, wbuf, g, t, r0, nrows, wave, nch, lane);
+
+  if (wave == 0) {
+    // Lane c waits for the blocks counted by counter c: ids b < n1, b % 64 == c.
+    const int c = lane;
+    const unsigned target =
+        c < hs.n1 ? (unsigned)((hs.n1 - c + FusedWs::kCounters - 1) / FusedWs::kCounters) : 0u;
+    const unsigned* ctr = hs.cnt + c * FusedWs::kCounterStride;
+    unsigned spins = 0;
+    while (__ballot(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+                    target) != 0) {
+      if (++spins > hs.spin_limit) {
+        if (lane == 0)
+          __hip_atomic_store(hs.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(8);
+    }
+    if (__hip_atomic_load(hs.xcc_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    else
+      invalidate_l1();
+  }
+  __syncthreads();
 
   float acc[RPD];
 #pragma unroll
   for (int j = 0; j < RPD; ++j) acc[j] = 0.0f;
-
-  for (int q0 = wave; q0 < C; q0 += U * kWavesPerBlock) {
-    V wv[U][RPD];
-    float av[U][VEC];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int q = q0 + u * kWavesPerBlock;
-      const int kk = q / nch;
-      const int c = (q - kk * nch) * kWave * VEC + lane * VEC;
-      const bool ok = q < C && c < g.I;
-      const int e = topk_id(t, kk < g.k ? kk : 0);
-      const WT* D = wbuf + (int64_t)e * g.stride + g.off_down + (int64_t)r0 * g.I + c;
-#pragma unroll
-      for (int j = 0; j < RPD; ++j) {
-        const bool okj = ok && j < nrows;
-        wv[u][j] = okj ? load_w<WT, VEC>(D + (int64_t)j * g.I) : vzero<V>();
-      }
-      if (ok) {
-        load_x<float, VEC>(ab + (int64_t)kk * g.I + c, av[u]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) av[u][i] = 0.0f;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-      for (int j = 0; j < RPD; ++j) {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[j] = fmaf(velem(wv[u][j], i), av[u][i], acc[j]);
-      }
-    }
+  down_tile_fma<V, VEC, RPD, U2>(acc, pre, act, g, act_row, wave, nch, lane);
+  for (int q0 = wave + kWavesPerBlock * U2; q0 < C; q0 += kWavesPerBlock * U2) {
+    V wv[U2][RPD];
+    down_tile_load<WT, VEC, RPD, U2>(wv, wbuf, g, t, r0, nrows, q0, nch, lane);
+    down_tile_fma<V, VEC, RPD, U2>(acc, wv, act, g, act_row, q0, nch, lane);
   }
-
 #pragma unroll
   for (int j = 0; j < RPD; ++j) {
     const float s = wave_sum(acc[j]);
     if (lane == 0) part[wave][j] = s;
   }
   __syncthreads();
-  if (wave == 0 && lane < nrows) {
-    float s = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWavesPerBlock; ++w) s += part[w][lane];
-    out[(int64_t)b * g.h + r0 + lane] = to_out<OT>(s);
-  }
+  if (wave == 0 && lane < nrows)
+    out[r0 + lane] = to_out<XT>((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
 }
 
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
 namespace {
-
-constexpr int kRPW = 2, kUG = 4;  // gate/up: rows per wave, chunk unroll
-constexpr int kRPD = 4, kUD = 4;  // down: rows per block, chunk unroll
 
 Geom make_geom(const Problem& p) {
   const int64_t es = p.wdt == WR_F16 ? 2 : 4;
@@ -283,6 +585,30 @@ Geom make_geom(const Problem& p) {
   return g;
 }
 
+// Compute units of the current device, cached per device.
+int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Persistent waves per token: the fewest waves that keep the largest share
+// minimal (ceil(items / cap)) with at most `cap` waves in total.
+int waves_for(int items, int B) {
+  const int cap = cu_count() * WR_WAVES_PER_CU;
+  const int per_tok = cap / B > 0 ? cap / B : 1;
+  const int ipw = (items + per_tok - 1) / per_tok;
+  return (items + ipw - 1) / ipw;
+}
+
 // 128-bit router loads need h % 4 == 0 and 16-byte aligned rows and x.
 bool router_vec4(const Problem& p) {
   const int xes = p.adt == WR_F16 ? 2 : 4;
@@ -290,32 +616,61 @@ bool router_vec4(const Problem& p) {
 }
 
 template <typename XT>
-hipError_t logits_t(const Problem& p, float* logits, hipStream_t s) {
-  dim3 grid((p.E + kWavesPerBlock - 1) / kWavesPerBlock, p.B);
+hipError_t logits_t(const Problem& p, float* logits, unsigned* zero, int nzero, int zstride,
+                    hipStream_t s) {
+  const dim3 grid(p.E, p.B);
   const XT* x = static_cast<const XT*>(p.x);
   if (router_vec4(p))
     hipLaunchKernelGGL((k_router_logits<XT, 4>), grid, dim3(kBlock), 0, s, p.gate_w, x, logits,
-                       p.E, p.h);
+                       p.E, p.h, zero, nzero, zstride);
   else
     hipLaunchKernelGGL((k_router_logits<XT, 1>), grid, dim3(kBlock), 0, s, p.gate_w, x, logits,
-                       p.E, p.h);
+                       p.E, p.h, zero, nzero, zstride);
+  return hipGetLastError();
+}
+
+// act chunks of the single-token fused kernel, and its gate/up blocks (the
+// chunk count rounded up to whole groups of 32 blocks).
+int fused_chunks(int I, int k) {
+  const int items = (I + WR_GU_RPW - 1) / WR_GU_RPW;
+  return k * ((items + kWavesPerBlock - 1) / kWavesPerBlock);
+}
+int fused_n1(int I, int k) { return (fused_chunks(I, k) + 31) / 32 * 32; }
+
+template <typename WT, typename XT, int VEC>
+hipError_t fused_t(const Problem& p, const FusedWs& w, hipStream_t s) {
+  const Geom g = make_geom(p);
+  Handoff hs;
+  hs.cnt = w.ctrl;
+  hs.timeout = w.ctrl + FusedWs::kTimeoutWord;
+  hs.xcc_flag = w.ctrl + FusedWs::kXccFlagWord;
+  hs.n1 = fused_n1(p.I, p.k);
+  hs.chunks = fused_chunks(p.I, p.k);
+  hs.spin_limit = 1u << 20;
+  const int n2 = (p.h + WR_FU_RPD - 1) / WR_FU_RPD;
+  hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, WR_GU_RPW, WR_GU_U, WR_FU_RPD, WR_FU_U>),
+                     dim3(hs.n1 + n2), dim3(kBlock), 0, s, static_cast<const WT*>(p.wbuf),
+                     static_cast<const XT*>(p.x), w.logits, w.act, static_cast<XT*>(p.out),
+                     p.topk_ids, p.topk_w, g, hs);
   return hipGetLastError();
 }
 
 template <typename WT, typename XT, int VEC>
 hipError_t ffn_t(const Problem& p, const FusedWs& w, hipStream_t s) {
+  constexpr int RPW = WR_GU_RPW, RPD = WR_DN_RPD;
+  if (p.B == 1) return fused_t<WT, XT, VEC>(p, w, s);
   const Geom g = make_geom(p);
   const WT* wb = static_cast<const WT*>(p.wbuf);
-  const int items = (p.I + kRPW - 1) / kRPW;
-  const int waves = p.k * items;
-  dim3 g1((waves + kWavesPerBlock - 1) / kWavesPerBlock, p.B);
-  hipLaunchKernelGGL((k_gateup<WT, XT, VEC, kRPW, kUG>), g1, dim3(kBlock), 0, s, wb,
-                     static_cast<const XT*>(p.x), w.logits, w.act, p.topk_ids, p.topk_w, g);
+  const int nw1 = waves_for(p.k * ((p.I + RPW - 1) / RPW), p.B);
+  const dim3 g1((nw1 + kWavesPerBlock - 1) / kWavesPerBlock, p.B);
+  hipLaunchKernelGGL((k_gateup<WT, XT, VEC, RPW, WR_GU_U>), g1, dim3(kBlock), 0, s, wb,
+                     static_cast<const XT*>(p.x), w.logits, w.act, p.topk_ids, p.topk_w, g, nw1);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  dim3 g2((p.h + kRPD - 1) / kRPD, p.B);
-  hipLaunchKernelGGL((k_down<WT, XT, VEC, kRPD, kUD>), g2, dim3(kBlock), 0, s, wb, w.logits,
-                     w.act, static_cast<XT*>(p.out), g);
+  const int nw2 = waves_for((p.h + RPD - 1) / RPD, p.B);
+  const dim3 g2((nw2 + kWavesPerBlock - 1) / kWavesPerBlock, p.B);
+  hipLaunchKernelGGL((k_down<WT, XT, VEC, RPD, WR_DN_U>), g2, dim3(kBlock), 0, s, wb, w.logits,
+                     w.act, static_cast<XT*>(p.out), g, nw2);
   return hipGetLastError();
 }
 
@@ -328,37 +683,36 @@ hipError_t ffn_x(const Problem& p, const FusedWs& w, hipStream_t s) {
 
 hipError_t run_ffn(const Problem& p, hipStream_t s) {
   const FusedWs w = FusedWs::carve(p.ws, p.E, p.I, p.k, p.B);
-  hipError_t err = launch_logits(p, w.logits, s);
+  // The single-token kernel's counters and timeout flag start each call at zero.
+  unsigned* zero = p.B == 1 ? w.ctrl : nullptr;
+  const int nz = FusedWs::kCtrlWords, zs = FusedWs::kCounterStride;
+  hipError_t err = p.adt == WR_F16 ? logits_t<f16>(p, w.logits, zero, nz, zs, s)
+                                   : logits_t<float>(p, w.logits, zero, nz, zs, s);
   if (err != hipSuccess) return err;
   return p.adt == WR_F16 ? ffn_x<f16>(p, w, s) : ffn_x<float>(p, w, s);
+}
+
+template <typename XT>
+hipError_t gate_t(const Problem& p, hipStream_t s) {
+  const XT* x = static_cast<const XT*>(p.x);
+  if (router_vec4(p))
+    hipLaunchKernelGGL((k_gate_topk<XT, 4>), dim3(p.B), dim3(1024), 0, s, p.gate_w, x, p.E, p.h,
+                       p.k, p.renorm, p.topk_ids, p.topk_w);
+  else
+    hipLaunchKernelGGL((k_gate_topk<XT, 1>), dim3(p.B), dim3(1024), 0, s, p.gate_w, x, p.E, p.h,
+                       p.k, p.renorm, p.topk_ids, p.topk_w);
+  return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_logits(const Problem& p, float* logits, hipStream_t s) {
-  return p.adt == WR_F16 ? logits_t<f16>(p, logits, s) : logits_t<float>(p, logits, s);
+  return p.adt == WR_F16 ? logits_t<f16>(p, logits, nullptr, 0, 0, s)
+                         : logits_t<float>(p, logits, nullptr, 0, 0, s);
 }
 
 hipError_t launch_gate_topk(const Problem& p, hipStream_t s) {
-  const int threads = 1024;
-  if (p.adt == WR_F16) {
-    const f16* x = static_cast<const f16*>(p.x);
-    if (router_vec4(p))
-      hipLaunchKernelGGL((k_gate_topk<f16, 4>), dim3(p.B), dim3(threads), 0, s, p.gate_w, x, p.E,
-                         p.h, p.k, p.renorm, p.topk_ids, p.topk_w);
-    else
-      hipLaunchKernelGGL((k_gate_topk<f16, 1>), dim3(p.B), dim3(threads), 0, s, p.gate_w, x, p.E,
-                         p.h, p.k, p.renorm, p.topk_ids, p.topk_w);
-  } else {
-    const float* x = static_cast<const float*>(p.x);
-    if (router_vec4(p))
-      hipLaunchKernelGGL((k_gate_topk<float, 4>), dim3(p.B), dim3(threads), 0, s, p.gate_w, x,
-                         p.E, p.h, p.k, p.renorm, p.topk_ids, p.topk_w);
-    else
-      hipLaunchKernelGGL((k_gate_topk<float, 1>), dim3(p.B), dim3(threads), 0, s, p.gate_w, x,
-                         p.E, p.h, p.k, p.renorm, p.topk_ids, p.topk_w);
-  }
-  return hipGetLastError();
+  return p.adt == WR_F16 ? gate_t<f16>(p, s) : gate_t<float>(p, s);
 }
 
 hipError_t launch_fused(const Problem& p, hipStream_t s) { return run_ffn(p, s); }
