@@ -1,25 +1,26 @@
 // Fused decode-time MoE kernels for gfx950 (wave64).
 //
-// The layer is three streaming passes:
-//   1. k_router_logits: one 4-wave workgroup per (expert, token) computes the
-//      router dot product (src/fused_moe.cu:100-112); each wave covers a
-//      quarter of the row, so one memory round trip covers it.
-//   2. k_gateup: a persistent grid of waves.  Each wave derives the top-K
-//      selection from the logits once (wave_select_topk: DPP max/sum and a
-//      64-bit ballot), then streams a contiguous share of the selected
-//      experts' gate/up rows with 128-bit non-temporal loads, RPW rows of
-//      each matrix at a time, reduces every row across the wave and writes
-//      act = w_kk * silu(gate . x) * (up . x) in fp32
-//      (src/fused_moe.cu:192-201, silu at :30-32).
-//   3. k_down: a persistent grid of waves; each wave owns whole output rows,
-//      streams those rows of every selected down matrix (contiguous I-long
-//      spans), accumulates sum_kk Wd_kk[r,:] . act_kk in fp32 registers and
-//      writes the row once (src/fused_moe.cu:203-224, without the reference's
-//      repeated global read-modify-write of the output).
-// The selected expert weights are the only large traffic; x, logits and act
-// are small and served from cache.  Work shares are contiguous row ranges
-// that differ by at most one item, and the grid is sized so that no wave
-// gets more items than necessary (balanced tail).
+// Every layer starts with k_router_logits: one 4-wave workgroup per (expert,
+// token) computes the router dot product (src/fused_moe.cu:100-112); each
+// wave covers a quarter of the row, so one memory round trip covers it.
+// Every consumer then derives the top-K selection from the logits itself
+// (wave_select_topk: DPP max/sum and a 64-bit ballot).
+//
+// Single token (the decode hot path): k_fused_ffn, ONE launch whose first
+// blocks stream the selected experts' gate/up rows and write
+// act = w_kk * silu(gate . x) * (up . x) in fp32 (src/fused_moe.cu:192-201,
+// silu at :30-32), and whose later blocks stream the selected down rows
+// against act and write every output row once (src/fused_moe.cu:203-224,
+// without the reference's repeated global read-modify-write of the output).
+// The hand-off between the two is described at k_fused_ffn.
+//
+// Several tokens: k_gateup and k_down, persistent grids with one grid row per
+// token; work shares are contiguous row ranges that differ by at most one
+// item.
+//
+// The selected expert weights are the only large traffic: 128-bit
+// non-temporal loads, 4 row streams per wave.  x, logits and act are small
+// and served from cache.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
