@@ -82,8 +82,19 @@ def test_workspace_bytes():
         ctrl + 256 + 2 * 14336 * 4)
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 64, 100, 3, 1) == (
         ctrl + 256 + 1280)  # 3 * 104 * 4 = 1248 -> 1280
-    assert lib.wr_workspace_bytes(capi.WR_KIND_BATCHED, 8, 4096, 14336, 2, 4) == (
-        ctrl + 4 * 256 + 8 * 14336 * 4)
+    # batched, B > 1: the larger of the per-token layout above and the
+    # grouped MFMA layout: logits, x as two fp16 terms, five [P] pair arrays,
+    # expert offsets / active list / count, act [P][I] and four K-slice
+    # partials [4][P][h] (P = B * k), each region rounded up to 256 bytes.
+    def up(n):
+        return (n + 255) // 256 * 256
+    B, E, h, I, k = 4, 8, 4096, 14336, 2
+    P = B * k
+    per_token = ctrl + B * 256 + P * I * 4
+    grouped = (up(B * 256) + 2 * up(B * h * 2) + 5 * up(P * 4) + up((E + 1) * 4) + up(E * 4)
+               + up(4) + up(P * I * 4) + up(4 * P * h * 4))
+    assert grouped == 1051648
+    assert lib.wr_workspace_bytes(capi.WR_KIND_BATCHED, E, h, I, k, B) == max(per_token, grouped)
     assert lib.wr_workspace_bytes(capi.WR_KIND_NAIVE, 8, 100, 10, 1, 1) == 256 + 3 * 256 + 2 * 512
     assert lib.wr_workspace_bytes(7, 8, 64, 64, 2, 1) == 0
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 65, 64, 64, 2, 1) == 0

@@ -159,6 +159,53 @@ def test_batched_empty_batch(cuda):
     assert out.shape == (0, h)
 
 
+GROUPED = [(8, 256, 512, 2, False), (16, 512, 1024, 2, True), (64, 256, 512, 6, False),
+           (8, 384, 640, 1, True)]
+
+
+@pytest.mark.parametrize("x_dtype", [F32, F16], ids=["xf32", "xf16"])
+@pytest.mark.parametrize("B", [2, 5, 33, 80])
+@pytest.mark.parametrize("cfg", GROUPED,
+                         ids=lambda c: f"E{c[0]}-h{c[1]}-I{c[2]}-k{c[3]}" + ("-renorm" if c[4] else ""))
+def test_grouped_batched_parity(cuda, cfg, B, x_dtype):
+    """The grouped MFMA batched path (fp16 weights, h and I multiples of 128).
+    Tokens cluster on one expert pair, so experts get anywhere from 1 to B
+    tokens (B = 80 puts more than 64 on one expert: two token passes).  Every
+    row's ids and weights are bit-identical to the single-token op and its
+    output equals that op's up to summation order; a subset is checked against
+    the oracle; two calls are bit-identical."""
+    E, h, I, k, rn = cfg
+    _, gw, buf = make_layer(E, h, I, F16, router_std=h ** -0.5, expert_std=0.05, seed=3,
+                            device=cuda)
+    pair = (1, 1) if k == 1 else (1, E - 1)  # k = 1: every token on one expert
+    x = clustered_batch(gw, B, pair=pair, alpha=4.0, seed=B, device=cuda).to(x_dtype)
+    print(f"[gpu] grouped E{E}-h{h}-I{I}-k{k} B={B} {x_dtype}", flush=True)
+    ids = torch.empty(B, k, dtype=torch.int32, device=cuda)
+    ws = torch.empty(B, k, dtype=torch.float32, device=cuda)
+    out = F.batched_fused_moe(x, gw, buf, E, h, I, k, rn, ids, ws)
+    again = F.batched_fused_moe(x, gw, buf, E, h, I, k, rn)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again), "grouped path is not deterministic"
+    counts = np.bincount(ids.cpu().numpy().ravel(), minlength=E)
+    assert counts.sum() == B * k
+    if B == 80:
+        assert counts.max() > 64, counts
+    checked = 0
+    for b in range(B):
+        s_ids = torch.empty(k, dtype=torch.int32, device=cuda)
+        s_ws = torch.empty(k, dtype=torch.float32, device=cuda)
+        single = F.fused_moe(x[b].contiguous(), gw, buf, E, h, I, k, rn, s_ids, s_ws)
+        assert torch.equal(s_ids, ids[b]) and torch.equal(s_ws, ws[b]), f"row {b} selection"
+        assert_same_up_to_order(out[b], single, label=f"row {b} vs single-token op")
+        if b % 8 == 0:
+            ref = oracle_token(x[b], gw, buf, E, h, I, k, rn)
+            if ref["robust"]:
+                assert_parity(out[b], ids[b], ws[b], ref, rel_tol=out_tol(x_dtype),
+                              label=f"grouped b={b}")
+                checked += 1
+    assert checked >= 1
+
+
 def test_errors_are_python_exceptions(cuda):
     E, h, I, k = 8, 64, 64, 2
     x, gw, buf = make_layer(E, h, I, F16, seed=0, device=cuda)
@@ -350,12 +397,12 @@ def test_full_size_configs(cuda, name, op):
     torch.cuda.empty_cache()
 
 
-def test_full_size_batched_clustered(cuda):
+@pytest.mark.parametrize("B", [16, 64])
+def test_full_size_batched_clustered(cuda, B):
     """Batched decode at Mixtral shape with tokens clustered on one expert pair."""
     cfg = CONFIGS["mixtral"]
     E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
     _, gw, buf = make_config_layer(cfg, seed=0, device=cuda, gen_device=cuda)
-    B = 16
     x = clustered_batch(gw, B, pair=(3, 5), alpha=4.0, seed=1, device=cuda)
     print(f"[gpu] full batched mixtral B={B}", flush=True)
     ids = torch.empty(B, k, dtype=torch.int32, device=cuda)
@@ -363,7 +410,7 @@ def test_full_size_batched_clustered(cuda):
     torch.cuda.synchronize()
     pairs = {tuple(sorted(r)) for r in ids.cpu().tolist()}
     assert (3, 5) in pairs
-    for b in (0, 7, 15):
+    for b in (0, 7, B - 1):
         ref = oracle_token(x[b], gw, buf, E, h, I, k, True)
         assert_parity(out[b], ids[b], None, ref, label=f"clustered b={b}")
     del buf

@@ -36,7 +36,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]
-HIP_SOURCES = ["wr_api.hip", "wr_kernels.hip", "wr_naive.hip"]
+HIP_SOURCES = ["wr_api.hip", "wr_kernels.hip", "wr_batched.hip", "wr_naive.hip"]
 
 
 def _run(cmd, **kw):

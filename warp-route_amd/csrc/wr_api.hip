@@ -7,6 +7,8 @@
 // (src/bindings.cpp:9-23, 35-43, 71-83, 110-125).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include <cstdint>
 
 #include "warp_route.h"
@@ -41,7 +43,10 @@ size_t ws_bytes(int kind, int E, int h, int I, int k, int B) {
     case WR_KIND_FUSED:
       return wr::FusedWs::bytes(E, I, k, 1);
     case WR_KIND_BATCHED:
-      return wr::FusedWs::bytes(E, I, k, B > 0 ? B : 1);
+      // B > 1 runs either the grouped MFMA path or the per-token kernels,
+      // depending on dtype and alignment: size for both.
+      return B > 1 ? std::max(wr::FusedWs::bytes(E, I, k, B), wr::BatchWs::bytes(E, h, I, k, B))
+                   : wr::FusedWs::bytes(E, I, k, 1);
     case WR_KIND_NAIVE:
       return wr::NaiveWs::bytes(E, h, I);
     default:

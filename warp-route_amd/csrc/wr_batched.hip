@@ -1,0 +1,424 @@
+// Batched decode MoE for gfx950: tokens grouped by expert, each selected
+// expert's weights streamed ONCE for all of its tokens, as small-M GEMMs on
+// the matrix cores.
+//
+// The reference's batched kernel runs one warp per token and re-reads every
+// selected expert's weights for every token (src/fused_moe_batched.cu:66-184).
+// Here a call with B tokens is five launches:
+//   1. k_router_logits (wr_kernels.hip): logits[B][64]; it also splits x into
+//      two fp16 terms, x = hi + lo (|x - (hi + lo)| <= 2^-22 |x|).
+//   2. k_route: one block selects every token's top-K (the same
+//      wave_select_topk as every other path, so ids and weights are
+//      bit-identical to the single-token op) and groups the (token, expert)
+//      pairs by expert, tokens ascending, with ballot prefix sums
+//      (deterministic, no atomics).
+//   3. k_gu_mfma: block (row tile, expert slot): 4 waves x 16 gate rows and
+//      the same 16 up rows each, all of the expert's tokens (up to 64 per
+//      pass); the token tile is staged in LDS and shared by the 4 waves.
+//      v_mfma_f32_16x16x32_f16 with A = weight rows (straight from HBM,
+//      exact fp16) and B = the hi and lo terms of x; products are exact and
+//      accumulate in fp32.  Epilogue: act[pair][row] = w * silu(g) * u
+//      (src/fused_moe.cu:192-201).
+//   4. k_dn_mfma: block (row tile, K slice, expert slot): the same scheme on
+//      the down rows against act (split into hi/lo fp16 while staging), four
+//      K slices so that the grid has enough blocks; partial sums per slice.
+//   5. k_combine: out[t] = sum over t's experts (selection order) and K
+//      slices (ascending) of the partials, in that fixed order.
+// Every sum has a fixed order, so results are deterministic.  The MFMA work
+// is padded to 16 tokens per tile; at 2 MFMAs per product term it stays far
+// below the time the weight stream takes (the path is HBM-bound).
+//
+// Requirements (else the per-token kernels in wr_kernels.hip run): fp16
+// weights with 16-byte aligned rows, h and I multiples of 128, and the fp16
+// range for x and act (|v| < 65504).
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "wr_device.h"
+#include "wr_internal.h"
+
+namespace wr {
+
+namespace {
+
+constexpr int kBlk = 256;       // 4 waves
+constexpr int kBK = 128;        // K step (columns per LDS tile)
+constexpr int kBM = 64;         // rows per block: 4 waves x 16
+constexpr int kMaxTok = 64;     // tokens per pass: 4 MFMA N tiles
+constexpr int kPieces = kBK / 8;        // 16-byte pieces per token row of a tile
+constexpr int kLdsRow = kPieces + 1;    // padded row: spreads lanes over the LDS banks
+
+typedef f16x8 H8;
+
+__device__ __forceinline__ f32x4 mfma(const H8& a, const H8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ H8 h8zero() {
+  H8 z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (f16)0.0f;
+  return z;
+}
+
+// ---------------------------------------------------------------------------
+// Routing: one block of 16 waves.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void k_route(const float* __restrict__ logits, int B, int E,
+                                                int k, int renorm, int32_t* __restrict__ ids_out,
+                                                float* __restrict__ w_out, BatchRoute r) {
+  __shared__ int s_cnt[WR_MAX_EXPERTS];
+  __shared__ int s_off[WR_MAX_EXPERTS];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int P = B * k;
+
+  for (int t = wave; t < B; t += nw) {
+    TopK tk;
+    wave_select_topk(logits + (int64_t)t * WR_MAX_EXPERTS, E, k, renorm, tk);
+#pragma unroll
+    for (int kk = 0; kk < WR_MAX_TOPK; ++kk) {
+      if (kk < k && lane == kk) {
+        const int q = t * k + kk;
+        r.sel_id[q] = tk.id[kk];
+        r.sel_w[q] = tk.w[kk];
+        if (ids_out != nullptr) ids_out[q] = tk.id[kk];
+        if (w_out != nullptr) w_out[q] = tk.w[kk];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Pairs per expert.
+  for (int e = wave; e < E; e += nw) {
+    int cnt = 0;
+    for (int q0 = 0; q0 < P; q0 += kWave) {
+      const int q = q0 + lane;
+      cnt += __popcll(__ballot(q < P && r.sel_id[q] == e));
+    }
+    if (lane == 0) s_cnt[e] = cnt;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int off = 0, na = 0;
+    for (int e = 0; e < E; ++e) {
+      s_off[e] = off;
+      r.off[e] = off;
+      if (s_cnt[e] > 0) r.active[na++] = e;
+      off += s_cnt[e];
+    }
+    r.off[E] = off;
+    *r.n_active = na;
+  }
+  __syncthreads();
+
+  // Stable placement: expert e's pairs in token order.
+  for (int e = wave; e < E; e += nw) {
+    int j = s_off[e];
+    for (int q0 = 0; q0 < P; q0 += kWave) {
+      const int q = q0 + lane;
+      const bool m = q < P && r.sel_id[q] == e;
+      const unsigned long long mask = __ballot(m);
+      if (m) {
+        const int pos = j + __popcll(mask & ((1ull << lane) - 1ull));
+        r.pair_tok[pos] = q / k;
+        r.pair_w[pos] = r.sel_w[q];
+        r.tok_pair[q] = pos;
+      }
+      j += __popcll(mask);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Token tiles in LDS.  xs[0] holds the hi terms, xs[1] the lo terms; row n is
+// token n of the pass, piece c covers columns [8 c, 8 c + 8) of the K step.
+// ---------------------------------------------------------------------------
+struct TokTile {
+  H8 hi[kMaxTok][kLdsRow];
+  H8 lo[kMaxTok][kLdsRow];
+};
+
+// One thread's share of a token tile, held in registers between the global
+// loads and the LDS stores: pieces i = threadIdx.x + kBlk * q.
+constexpr int kTilePieces = kMaxTok * kPieces / kBlk;  // 4
+
+// Gate/up: x tokens gathered through pair_tok; both terms precomputed.
+__device__ __forceinline__ void gu_tile_load(H8 (&hi)[kTilePieces], H8 (&lo)[kTilePieces],
+                                             const f16* __restrict__ x_hi,
+                                             const f16* __restrict__ x_lo, const int32_t* tok,
+                                             int mt, int h, int kb, bool with_lo) {
+#pragma unroll
+  for (int q = 0; q < kTilePieces; ++q) {
+    const int i = threadIdx.x + kBlk * q;
+    const int n = i / kPieces, c = i % kPieces;
+    hi[q] = lo[q] = h8zero();
+    if (n < mt) {
+      const int64_t off = (int64_t)tok[n] * h + kb + c * 8;
+      hi[q] = *reinterpret_cast<const H8*>(x_hi + off);
+      if (with_lo) lo[q] = *reinterpret_cast<const H8*>(x_lo + off);
+    }
+  }
+}
+
+// Down: act rows of the pass's pairs, fp32, split into two fp16 terms.
+__device__ __forceinline__ void dn_tile_load(H8 (&hi)[kTilePieces], H8 (&lo)[kTilePieces],
+                                             const float* __restrict__ act, int p0, int mt, int I,
+                                             int kb) {
+#pragma unroll
+  for (int q = 0; q < kTilePieces; ++q) {
+    const int i = threadIdx.x + kBlk * q;
+    const int n = i / kPieces, c = i % kPieces;
+    hi[q] = lo[q] = h8zero();
+    if (n < mt) {
+      const float* a = act + (int64_t)(p0 + n) * I + kb + c * 8;
+      const f32x4 v0 = *reinterpret_cast<const f32x4*>(a);
+      const f32x4 v1 = *reinterpret_cast<const f32x4*>(a + 4);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const float v = t < 4 ? v0[t] : v1[t - 4];
+        const f16 vh = (f16)v;
+        hi[q][t] = vh;
+        lo[q][t] = (f16)(v - (float)vh);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ void tile_store(TokTile& xs, const H8 (&hi)[kTilePieces],
+                                           const H8 (&lo)[kTilePieces], bool with_lo) {
+#pragma unroll
+  for (int q = 0; q < kTilePieces; ++q) {
+    const int i = threadIdx.x + kBlk * q;
+    const int n = i / kPieces, c = i % kPieces;
+    xs.hi[n][c] = hi[q];
+    if (with_lo) xs.lo[n][c] = lo[q];
+  }
+}
+
+// A operand for MFMA j of a K step: lane l holds row (l % 16), columns
+// kb + 32 j + 8 (l / 16) .. +8; `w` already points at the lane's row and
+// 8 (l / 16) column offset.
+__device__ __forceinline__ void a_load(H8 (&a)[4], const f16* __restrict__ w, int kb) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) a[j] = load_w<f16, 8>(w + kb + 32 * j);
+}
+
+// ---------------------------------------------------------------------------
+// Gate/up.  grid (I / 64, expert slots).  One pass covers up to 64 of the
+// expert's tokens as NT MFMA tiles of 16; NT is a template parameter so that
+// the K loop has no per-tile branches.
+// ---------------------------------------------------------------------------
+template <bool LO, int NT>
+__device__ __forceinline__ void gu_pass(TokTile& xs, const f16* __restrict__ Gw,
+                                        const f16* __restrict__ Uw, const f16* __restrict__ x_hi,
+                                        const f16* __restrict__ x_lo, const BatchRoute& r,
+                                        int p0, int mt, float* __restrict__ act, int row0,
+                                        const Geom& g, int lane) {
+  f32x4 ag[NT], au[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) ag[n] = au[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int32_t* tok = r.pair_tok + p0;
+  for (int kb = 0; kb < g.h; kb += kBK) {
+    H8 gc[4], uc[4];
+    a_load(gc, Gw, kb);  // HBM: issued first, consumed last
+    a_load(uc, Uw, kb);
+    {
+      H8 th[kTilePieces], tl[kTilePieces];
+      gu_tile_load(th, tl, x_hi, x_lo, tok, mt, g.h, kb, LO);
+      __syncthreads();  // every wave is done reading the previous tile
+      tile_store(xs, th, tl, LO);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        const int tn = n * 16 + (lane & 15), c = 4 * j + (lane >> 4);
+        const H8 bh = xs.hi[tn][c];
+        ag[n] = mfma(gc[j], bh, ag[n]);
+        au[n] = mfma(uc[j], bh, au[n]);
+        if (LO) {
+          const H8 bl = xs.lo[tn][c];
+          ag[n] = mfma(gc[j], bl, ag[n]);
+          au[n] = mfma(uc[j], bl, au[n]);
+        }
+      }
+    }
+  }
+  // D layout: lane holds token n*16 + (lane % 16), rows 4 (lane / 16) .. +4.
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int tn = n * 16 + (lane & 15);
+    if (tn < mt) {
+      const int p = p0 + tn;
+      const float w = r.pair_w[p];
+      f32x4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = w * (silu(ag[n][i]) * au[n][i]);
+      *reinterpret_cast<f32x4*>(act + (int64_t)p * g.I + row0 + (lane >> 4) * 4) = v;
+    }
+  }
+}
+
+template <bool LO>
+__global__ __launch_bounds__(kBlk) void k_gu_mfma(const f16* __restrict__ wbuf,
+                                                  const f16* __restrict__ x_hi,
+                                                  const f16* __restrict__ x_lo, BatchRoute r,
+                                                  float* __restrict__ act, Geom g) {
+  __shared__ TokTile xs;
+  const int slot = blockIdx.y;
+  if (slot >= *r.n_active) return;  // block-uniform
+  const int e = r.active[slot];
+  const int pbeg = r.off[e], M = r.off[e + 1] - pbeg;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int row0 = blockIdx.x * kBM + wave * 16;
+  const f16* Gw =
+      wbuf + (int64_t)e * g.stride + (int64_t)(row0 + (lane & 15)) * g.h + (lane >> 4) * 8;
+  const f16* Uw = Gw + g.off_up;
+  for (int m0 = 0; m0 < M; m0 += kMaxTok) {
+    const int mt = min(kMaxTok, M - m0);
+    switch ((mt + 15) / 16) {
+      case 1: gu_pass<LO, 1>(xs, Gw, Uw, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
+      case 2: gu_pass<LO, 2>(xs, Gw, Uw, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
+      case 3: gu_pass<LO, 3>(xs, Gw, Uw, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
+      default: gu_pass<LO, 4>(xs, Gw, Uw, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Down.  grid (h / 64, kKSplit, expert slots).  K slice ks covers steps
+// [nsteps * ks / kKSplit, nsteps * (ks + 1) / kKSplit).
+// ---------------------------------------------------------------------------
+template <int NT>
+__device__ __forceinline__ void dn_pass(TokTile& xs, const f16* __restrict__ Dw,
+                                        const float* __restrict__ act, int p0, int mt, int sb,
+                                        int se, float* __restrict__ y, int row0, const Geom& g,
+                                        int lane) {
+  f32x4 acc[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s = sb; s < se; ++s) {
+    const int kb = s * kBK;
+    H8 dc[4];
+    a_load(dc, Dw, kb);
+    {
+      H8 th[kTilePieces], tl[kTilePieces];
+      dn_tile_load(th, tl, act, p0, mt, g.I, kb);
+      __syncthreads();
+      tile_store(xs, th, tl, true);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        const int tn = n * 16 + (lane & 15), c = 4 * j + (lane >> 4);
+        acc[n] = mfma(dc[j], xs.hi[tn][c], acc[n]);
+        acc[n] = mfma(dc[j], xs.lo[tn][c], acc[n]);
+      }
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int tn = n * 16 + (lane & 15);
+    if (tn < mt)
+      *reinterpret_cast<f32x4*>(y + (int64_t)(p0 + tn) * g.h + row0 + (lane >> 4) * 4) = acc[n];
+  }
+}
+
+__global__ __launch_bounds__(kBlk) void k_dn_mfma(const f16* __restrict__ wbuf, BatchRoute r,
+                                                  const float* __restrict__ act,
+                                                  float* __restrict__ ypart, Geom g, int P) {
+  __shared__ TokTile xs;
+  const int slot = blockIdx.z;
+  if (slot >= *r.n_active) return;
+  const int e = r.active[slot];
+  const int pbeg = r.off[e], M = r.off[e + 1] - pbeg;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int row0 = blockIdx.x * kBM + wave * 16;
+  const int ks = blockIdx.y;
+  const int nsteps = g.I / kBK;
+  const int sb = nsteps * ks / BatchWs::kKSplit;
+  const int se = nsteps * (ks + 1) / BatchWs::kKSplit;
+  const f16* Dw = wbuf + (int64_t)e * g.stride + g.off_down +
+                  (int64_t)(row0 + (lane & 15)) * g.I + (lane >> 4) * 8;
+  float* y = ypart + (int64_t)ks * P * g.h;
+  for (int m0 = 0; m0 < M; m0 += kMaxTok) {
+    const int mt = min(kMaxTok, M - m0);
+    switch ((mt + 15) / 16) {
+      case 1: dn_pass<1>(xs, Dw, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
+      case 2: dn_pass<2>(xs, Dw, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
+      case 3: dn_pass<3>(xs, Dw, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
+      default: dn_pass<4>(xs, Dw, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
+    }
+  }
+}
+
+// out[t][row]: grid (ceil(h / 256), B).
+template <typename OT>
+__global__ __launch_bounds__(kBlk) void k_combine(const float* __restrict__ ypart, BatchRoute r,
+                                                  OT* __restrict__ out, int h, int k, int P) {
+  const int t = blockIdx.y;
+  const int row = blockIdx.x * kBlk + threadIdx.x;
+  if (row >= h) return;
+  float s = 0.0f;
+  for (int kk = 0; kk < k; ++kk) {
+    const int p = r.tok_pair[t * k + kk];
+#pragma unroll
+    for (int ks = 0; ks < BatchWs::kKSplit; ++ks) s += ypart[((int64_t)ks * P + p) * h + row];
+  }
+  out[(int64_t)t * h + row] = to_out<OT>(s);
+}
+
+template <typename XT>
+hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
+  Geom g;
+  g.E = p.E;
+  g.h = p.h;
+  g.I = p.I;
+  g.k = p.k;
+  g.renorm = p.renorm;
+  g.B = p.B;
+  g.stride = p.stride_b / 2;
+  g.off_up = p.off_up_b / 2;
+  g.off_down = p.off_down_b / 2;
+  const int P = p.B * p.k;
+  const int slots = std::min(p.E, P);
+  const f16* wb = static_cast<const f16*>(p.wbuf);
+
+  hipLaunchKernelGGL(k_route, dim3(1), dim3(1024), 0, s, w.logits, p.B, p.E, p.k, p.renorm,
+                     p.topk_ids, p.topk_w, w.route);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  constexpr bool LO = std::is_same<XT, float>::value;
+  hipLaunchKernelGGL((k_gu_mfma<LO>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s, wb, w.x_hi,
+                     w.x_lo, w.route, w.act, g);
+  if ((err = hipGetLastError()) != hipSuccess) return err;
+  hipLaunchKernelGGL(k_dn_mfma, dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s, wb,
+                     w.route, w.act, w.ypart, g, P);
+  if ((err = hipGetLastError()) != hipSuccess) return err;
+  hipLaunchKernelGGL((k_combine<XT>), dim3((p.h + kBlk - 1) / kBlk, p.B), dim3(kBlk), 0, s,
+                     w.ypart, w.route, static_cast<XT*>(p.out), p.h, p.k, P);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool grouped_ok(const Problem& p) {
+  return p.B > 1 && p.wdt == WR_F16 && p.vec == 8 && p.h % kBK == 0 && p.I % kBK == 0;
+}
+
+hipError_t launch_grouped(const Problem& p, hipStream_t s) {
+  const BatchWs w = BatchWs::carve(p.ws, p.E, p.h, p.I, p.k, p.B);
+  hipError_t err = launch_logits_split(p, w.logits, w.x_hi, w.x_lo, s);
+  if (err != hipSuccess) return err;
+  return p.adt == WR_F16 ? grouped_t<f16>(p, w, s) : grouped_t<float>(p, w, s);
+}
+
+}  // namespace wr

@@ -72,6 +72,65 @@ struct FusedWs {
   }
 };
 
+// Grouped batched path (wr_batched.hip): (token, expert) pairs grouped by
+// expert.  Pair q = t * k + kk is token t's kk-th selection; grouped index p
+// orders the pairs by expert, tokens ascending.
+struct BatchRoute {
+  int32_t* sel_id;    // [P] by q
+  float* sel_w;       // [P] by q
+  int32_t* pair_tok;  // [P] by p: token
+  float* pair_w;      // [P] by p: gate weight
+  int32_t* tok_pair;  // [P] by q: p
+  int32_t* off;       // [E + 1]: expert e's pairs are [off[e], off[e + 1])
+  int32_t* active;    // [E]: experts with pairs, ascending
+  int32_t* n_active;  // [1]
+};
+
+struct BatchWs {
+  static constexpr int kKSplit = 4;  // K slices of the down GEMM
+  float* logits;  // [B][WR_MAX_EXPERTS]
+  _Float16* x_hi;  // [B][h]: x = hi + lo
+  _Float16* x_lo;  // [B][h]
+  BatchRoute route;
+  float* act;    // [P][I], grouped pair order, scaled by the gate weight
+  float* ypart;  // [kKSplit][P][h]: down partial sums
+  static size_t bytes(int E, int h, int I, int k, int B) {
+    size_t n = 0;
+    carve_into(nullptr, &n, E, h, I, k, B);
+    return n;
+  }
+  static BatchWs carve(char* ws, int E, int h, int I, int k, int B) {
+    return carve_into(ws, nullptr, E, h, I, k, B);
+  }
+
+ private:
+  static BatchWs carve_into(char* ws, size_t* total, int E, int h, int I, int k, int B) {
+    BatchWs w;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+      char* p = ws == nullptr ? nullptr : ws + off;
+      off += align_up(bytes, kWsAlign);
+      return p;
+    };
+    const size_t P = (size_t)B * k;
+    w.logits = reinterpret_cast<float*>(take((size_t)B * WR_MAX_EXPERTS * 4));
+    w.x_hi = reinterpret_cast<_Float16*>(take((size_t)B * h * 2));
+    w.x_lo = reinterpret_cast<_Float16*>(take((size_t)B * h * 2));
+    w.route.sel_id = reinterpret_cast<int32_t*>(take(P * 4));
+    w.route.sel_w = reinterpret_cast<float*>(take(P * 4));
+    w.route.pair_tok = reinterpret_cast<int32_t*>(take(P * 4));
+    w.route.pair_w = reinterpret_cast<float*>(take(P * 4));
+    w.route.tok_pair = reinterpret_cast<int32_t*>(take(P * 4));
+    w.route.off = reinterpret_cast<int32_t*>(take((size_t)(E + 1) * 4));
+    w.route.active = reinterpret_cast<int32_t*>(take((size_t)E * 4));
+    w.route.n_active = reinterpret_cast<int32_t*>(take(4));
+    w.act = reinterpret_cast<float*>(take(P * I * 4));
+    w.ypart = reinterpret_cast<float*>(take((size_t)kKSplit * P * h * 4));
+    if (total != nullptr) *total = off;
+    return w;
+  }
+};
+
 struct NaiveWs {
   float *logits, *gate_vec, *up_vec, *act_vec, *expert_out, *accum;
   static size_t bytes(int E, int h, int I) {
@@ -99,6 +158,12 @@ struct NaiveWs {
 // Launchers (wr_kernels.hip, wr_naive.hip).  Each returns the first HIP
 // error it meets.
 hipError_t launch_logits(const Problem& p, float* logits, hipStream_t s);
+// Logits, plus x split into two fp16 terms x = hi + lo (lo = 0 for fp16 x).
+hipError_t launch_logits_split(const Problem& p, float* logits, _Float16* x_hi, _Float16* x_lo,
+                               hipStream_t s);
+// Grouped batched path: usable when grouped_ok(p).
+bool grouped_ok(const Problem& p);
+hipError_t launch_grouped(const Problem& p, hipStream_t s);
 hipError_t launch_gate_topk(const Problem& p, hipStream_t s);
 hipError_t launch_fused(const Problem& p, hipStream_t s);
 hipError_t launch_batched(const Problem& p, hipStream_t s);

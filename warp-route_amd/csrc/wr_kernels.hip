@@ -26,6 +26,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
+#include <type_traits>
 
 #include "wr_device.h"
 #include "wr_internal.h"
@@ -101,15 +102,30 @@ __device__ __forceinline__ float router_combine(const float* p) {
 // so that consumers can read all 64 with scalar loads).  Block (0, 0) also
 // zeroes the words zero[i * zstride], i < nzero (the fused kernel's arrival
 // counters and timeout flag), which the next kernel on the stream reads.
+// With x_hi != nullptr, block (e, b) also writes its 1/E share of token b's x
+// as two fp16 terms, hi = fp16(x) and lo = fp16(x - hi) (lo = 0 for fp16 x),
+// for the batched MFMA path.
 template <typename XT, int VEC>
 __global__ __launch_bounds__(kBlock) void k_router_logits(const float* __restrict__ gate_w,
                                                           const XT* __restrict__ x,
                                                           float* __restrict__ logits, int E,
                                                           int h, unsigned* __restrict__ zero,
-                                                          int nzero, int zstride) {
+                                                          int nzero, int zstride,
+                                                          f16* __restrict__ x_hi,
+                                                          f16* __restrict__ x_lo) {
   __shared__ float part[4];
   const int q = threadIdx.x / kWave;
   const int e = blockIdx.x, b = blockIdx.y;
+  if (x_hi != nullptr) {
+    const int cs = (h + E - 1) / E;
+    const int end = min(h, (e + 1) * cs);
+    for (int i = e * cs + (int)threadIdx.x; i < end; i += kBlock) {
+      const float v = (float)x[(int64_t)b * h + i];
+      const f16 vh = (f16)v;
+      x_hi[(int64_t)b * h + i] = vh;
+      x_lo[(int64_t)b * h + i] = std::is_same<XT, float>::value ? (f16)(v - (float)vh) : (f16)0.0f;
+    }
+  }
   if (zero != nullptr && e == 0 && b == 0 && (int)threadIdx.x < nzero)
     zero[(int64_t)threadIdx.x * zstride] = 0u;
   const float p = router_partial<XT, VEC>(gate_w + (int64_t)e * h, x + (int64_t)b * h, h, q);
@@ -618,15 +634,15 @@ bool router_vec4(const Problem& p) {
 
 template <typename XT>
 hipError_t logits_t(const Problem& p, float* logits, unsigned* zero, int nzero, int zstride,
-                    hipStream_t s) {
+                    hipStream_t s, f16* x_hi = nullptr, f16* x_lo = nullptr) {
   const dim3 grid(p.E, p.B);
   const XT* x = static_cast<const XT*>(p.x);
   if (router_vec4(p))
     hipLaunchKernelGGL((k_router_logits<XT, 4>), grid, dim3(kBlock), 0, s, p.gate_w, x, logits,
-                       p.E, p.h, zero, nzero, zstride);
+                       p.E, p.h, zero, nzero, zstride, x_hi, x_lo);
   else
     hipLaunchKernelGGL((k_router_logits<XT, 1>), grid, dim3(kBlock), 0, s, p.gate_w, x, logits,
-                       p.E, p.h, zero, nzero, zstride);
+                       p.E, p.h, zero, nzero, zstride, x_hi, x_lo);
   return hipGetLastError();
 }
 
@@ -718,6 +734,15 @@ hipError_t launch_gate_topk(const Problem& p, hipStream_t s) {
 
 hipError_t launch_fused(const Problem& p, hipStream_t s) { return run_ffn(p, s); }
 
-hipError_t launch_batched(const Problem& p, hipStream_t s) { return run_ffn(p, s); }
+hipError_t launch_logits_split(const Problem& p, float* logits, f16* x_hi, f16* x_lo,
+                               hipStream_t s) {
+  return p.adt == WR_F16 ? logits_t<f16>(p, logits, nullptr, 0, 0, s, x_hi, x_lo)
+                         : logits_t<float>(p, logits, nullptr, 0, 0, s, x_hi, x_lo);
+}
+
+hipError_t launch_batched(const Problem& p, hipStream_t s) {
+  if (grouped_ok(p)) return launch_grouped(p, s);
+  return run_ffn(p, s);
+}
 
 }  // namespace wr
