@@ -63,29 +63,49 @@ __device__ __forceinline__ H8 h8zero() {
 }
 
 // ---------------------------------------------------------------------------
-// Routing: one block of 16 waves.
+// Routing: one block of 16 waves.  The per-pair selection lives in LDS when it
+// fits (kRouteLds pairs), else in the workspace.
 // ---------------------------------------------------------------------------
+constexpr int kRouteLds = 4096;
+
 __global__ __launch_bounds__(1024) void k_route(const float* __restrict__ logits, int B, int E,
                                                 int k, int renorm, int32_t* __restrict__ ids_out,
                                                 float* __restrict__ w_out, BatchRoute r) {
   __shared__ int s_cnt[WR_MAX_EXPERTS];
   __shared__ int s_off[WR_MAX_EXPERTS];
+  __shared__ int s_id[kRouteLds];
+  __shared__ float s_w[kRouteLds];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
   const int P = B * k;
+  int* sel_id = P <= kRouteLds ? s_id : r.sel_id;
+  float* sel_w = P <= kRouteLds ? s_w : r.sel_w;
 
-  for (int t = wave; t < B; t += nw) {
-    TopK tk;
-    wave_select_topk(logits + (int64_t)t * WR_MAX_EXPERTS, E, k, renorm, tk);
+  // Selection: lane e holds logit e; a wave's next 4 tokens are loaded at once.
+  for (int t0 = wave; t0 < B; t0 += 4 * nw) {
+    float l[4];
 #pragma unroll
-    for (int kk = 0; kk < WR_MAX_TOPK; ++kk) {
-      if (kk < k && lane == kk) {
-        const int q = t * k + kk;
-        r.sel_id[q] = tk.id[kk];
-        r.sel_w[q] = tk.w[kk];
-        if (ids_out != nullptr) ids_out[q] = tk.id[kk];
-        if (w_out != nullptr) w_out[q] = tk.w[kk];
+    for (int i = 0; i < 4; ++i) {
+      const int t = t0 + i * nw;
+      l[i] = t < B ? logits[(int64_t)t * WR_MAX_EXPERTS + lane] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = t0 + i * nw;
+      if (t < B) {  // wave-uniform
+        TopK tk;
+        wave_select_topk_reg(l[i], E, k, renorm, tk);
+#pragma unroll
+        for (int kk = 0; kk < WR_MAX_TOPK; ++kk) {
+          if (kk < k && lane == kk) {
+            const int q = t * k + kk;
+            sel_id[q] = tk.id[kk];
+            sel_w[q] = tk.w[kk];
+            if (ids_out != nullptr) ids_out[q] = tk.id[kk];
+            if (w_out != nullptr) w_out[q] = tk.w[kk];
+          }
+        }
       }
     }
   }
@@ -96,7 +116,7 @@ __global__ __launch_bounds__(1024) void k_route(const float* __restrict__ logits
     int cnt = 0;
     for (int q0 = 0; q0 < P; q0 += kWave) {
       const int q = q0 + lane;
-      cnt += __popcll(__ballot(q < P && r.sel_id[q] == e));
+      cnt += __popcll(__ballot(q < P && sel_id[q] == e));
     }
     if (lane == 0) s_cnt[e] = cnt;
   }
@@ -119,12 +139,12 @@ __global__ __launch_bounds__(1024) void k_route(const float* __restrict__ logits
     int j = s_off[e];
     for (int q0 = 0; q0 < P; q0 += kWave) {
       const int q = q0 + lane;
-      const bool m = q < P && r.sel_id[q] == e;
+      const bool m = q < P && sel_id[q] == e;
       const unsigned long long mask = __ballot(m);
       if (m) {
         const int pos = j + __popcll(mask & ((1ull << lane) - 1ull));
         r.pair_tok[pos] = q / k;
-        r.pair_w[pos] = r.sel_w[q];
+        r.pair_w[pos] = sel_w[q];
         r.tok_pair[q] = pos;
       }
       j += __popcll(mask);
@@ -142,38 +162,48 @@ struct TokTile {
 };
 
 // One thread's share of a token tile, held in registers between the global
-// loads and the LDS stores: pieces i = threadIdx.x + kBlk * q.
+// loads and the LDS stores: pieces i = threadIdx.x + kBlk * q, token row
+// n = i / kPieces, 8 columns at 8 (i % kPieces) of the K step.
 constexpr int kTilePieces = kMaxTok * kPieces / kBlk;  // 4
 
-// Gate/up: x tokens gathered through pair_tok; both terms precomputed.
-__device__ __forceinline__ void gu_tile_load(H8 (&hi)[kTilePieces], H8 (&lo)[kTilePieces],
-                                             const f16* __restrict__ x_hi,
-                                             const f16* __restrict__ x_lo, const int32_t* tok,
-                                             int mt, int h, int kb, bool with_lo) {
+// Element offset of each piece's row start (plus its column), or -1 for a
+// padding token; fixed for a whole pass.
+__device__ __forceinline__ void tile_rows(int64_t (&off)[kTilePieces], const int32_t* rows,
+                                          int direct0, int mt, int ld) {
 #pragma unroll
   for (int q = 0; q < kTilePieces; ++q) {
     const int i = threadIdx.x + kBlk * q;
     const int n = i / kPieces, c = i % kPieces;
+    const int row = rows != nullptr ? (n < mt ? rows[n] : 0) : direct0 + n;
+    off[q] = n < mt ? (int64_t)row * ld + c * 8 : -1;
+  }
+}
+
+// Gate/up: x as two precomputed fp16 terms.
+__device__ __forceinline__ void gu_tile_load(H8 (&hi)[kTilePieces], H8 (&lo)[kTilePieces],
+                                             const f16* __restrict__ x_hi,
+                                             const f16* __restrict__ x_lo,
+                                             const int64_t (&off)[kTilePieces], int kb,
+                                             bool with_lo) {
+#pragma unroll
+  for (int q = 0; q < kTilePieces; ++q) {
     hi[q] = lo[q] = h8zero();
-    if (n < mt) {
-      const int64_t off = (int64_t)tok[n] * h + kb + c * 8;
-      hi[q] = *reinterpret_cast<const H8*>(x_hi + off);
-      if (with_lo) lo[q] = *reinterpret_cast<const H8*>(x_lo + off);
+    if (off[q] >= 0) {
+      hi[q] = *reinterpret_cast<const H8*>(x_hi + off[q] + kb);
+      if (with_lo) lo[q] = *reinterpret_cast<const H8*>(x_lo + off[q] + kb);
     }
   }
 }
 
-// Down: act rows of the pass's pairs, fp32, split into two fp16 terms.
+// Down: act rows, fp32, split into two fp16 terms.
 __device__ __forceinline__ void dn_tile_load(H8 (&hi)[kTilePieces], H8 (&lo)[kTilePieces],
-                                             const float* __restrict__ act, int p0, int mt, int I,
-                                             int kb) {
+                                             const float* __restrict__ act,
+                                             const int64_t (&off)[kTilePieces], int kb) {
 #pragma unroll
   for (int q = 0; q < kTilePieces; ++q) {
-    const int i = threadIdx.x + kBlk * q;
-    const int n = i / kPieces, c = i % kPieces;
     hi[q] = lo[q] = h8zero();
-    if (n < mt) {
-      const float* a = act + (int64_t)(p0 + n) * I + kb + c * 8;
+    if (off[q] >= 0) {
+      const float* a = act + off[q] + kb;
       const f32x4 v0 = *reinterpret_cast<const f32x4*>(a);
       const f32x4 v1 = *reinterpret_cast<const f32x4*>(a + 4);
 #pragma unroll
@@ -220,18 +250,25 @@ __device__ __forceinline__ void gu_pass(TokTile& xs, const f16* __restrict__ Gw,
   f32x4 ag[NT], au[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) ag[n] = au[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  const int32_t* tok = r.pair_tok + p0;
-  for (int kb = 0; kb < g.h; kb += kBK) {
-    H8 gc[4], uc[4];
-    a_load(gc, Gw, kb);  // HBM: issued first, consumed last
-    a_load(uc, Uw, kb);
-    {
-      H8 th[kTilePieces], tl[kTilePieces];
-      gu_tile_load(th, tl, x_hi, x_lo, tok, mt, g.h, kb, LO);
-      __syncthreads();  // every wave is done reading the previous tile
-      tile_store(xs, th, tl, LO);
-    }
+  int64_t off[kTilePieces];
+  tile_rows(off, r.pair_tok + p0, 0, mt, g.h);
+  const int ns = g.h / kBK;
+
+  // Software pipeline, one K step deep: step s's weight and token loads are
+  // issued before step s-1's MFMAs.
+  H8 g0[4], u0[4], g1[4], u1[4], th[kTilePieces], tl[kTilePieces];
+  a_load(g0, Gw, 0);
+  a_load(u0, Uw, 0);
+  gu_tile_load(th, tl, x_hi, x_lo, off, 0, LO);
+  auto step = [&](const H8 (&gc)[4], const H8 (&uc)[4], H8 (&gn)[4], H8 (&un)[4], int s) {
+    __syncthreads();  // every wave is done reading the previous tile
+    tile_store(xs, th, tl, LO);
     __syncthreads();
+    if (s + 1 < ns) {
+      a_load(gn, Gw, (s + 1) * kBK);
+      a_load(un, Uw, (s + 1) * kBK);
+      gu_tile_load(th, tl, x_hi, x_lo, off, (s + 1) * kBK, LO);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -247,7 +284,12 @@ __device__ __forceinline__ void gu_pass(TokTile& xs, const f16* __restrict__ Gw,
         }
       }
     }
+  };
+  for (int s = 0; s < ns; s += 2) {
+    step(g0, u0, g1, u1, s);
+    if (s + 1 < ns) step(g1, u1, g0, u0, s + 1);
   }
+
   // D layout: lane holds token n*16 + (lane % 16), rows 4 (lane / 16) .. +4.
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
@@ -302,25 +344,33 @@ __device__ __forceinline__ void dn_pass(TokTile& xs, const f16* __restrict__ Dw,
   f32x4 acc[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int s = sb; s < se; ++s) {
-    const int kb = s * kBK;
-    H8 dc[4];
-    a_load(dc, Dw, kb);
-    {
-      H8 th[kTilePieces], tl[kTilePieces];
-      dn_tile_load(th, tl, act, p0, mt, g.I, kb);
+  if (sb < se) {
+    int64_t off[kTilePieces];
+    tile_rows(off, nullptr, p0, mt, g.I);
+    H8 d0[4], d1[4], th[kTilePieces], tl[kTilePieces];
+    a_load(d0, Dw, sb * kBK);
+    dn_tile_load(th, tl, act, off, sb * kBK);
+    auto step = [&](const H8 (&dc)[4], H8 (&dn)[4], int s) {
       __syncthreads();
       tile_store(xs, th, tl, true);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int n = 0; n < NT; ++n) {
-        const int tn = n * 16 + (lane & 15), c = 4 * j + (lane >> 4);
-        acc[n] = mfma(dc[j], xs.hi[tn][c], acc[n]);
-        acc[n] = mfma(dc[j], xs.lo[tn][c], acc[n]);
+      __syncthreads();
+      if (s + 1 < se) {
+        a_load(dn, Dw, (s + 1) * kBK);
+        dn_tile_load(th, tl, act, off, (s + 1) * kBK);
       }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+          const int tn = n * 16 + (lane & 15), c = 4 * j + (lane >> 4);
+          acc[n] = mfma(dc[j], xs.hi[tn][c], acc[n]);
+          acc[n] = mfma(dc[j], xs.lo[tn][c], acc[n]);
+        }
+      }
+    };
+    for (int s = sb; s < se; s += 2) {
+      step(d0, d1, s);
+      if (s + 1 < se) step(d1, d0, s + 1);
     }
   }
 #pragma unroll
