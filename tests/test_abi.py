@@ -75,13 +75,13 @@ def test_workspace_bytes():
     lib = capi.lib()
     # fused: control block (64 arrival counters, a timeout flag and an XCD
     # flag, one 256-byte line each) + 64 fp32 logits per token (E padded to
-    # 64) + act: single token k rows of I rounded up to 8 columns, B > 1
+    # 64) + act: single token k rows of I rounded up to 16 columns, B > 1
     # B*k*I; fp32, rounded up to 256 bytes.
     ctrl = 66 * 256
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 4096, 14336, 2, 1) == (
         ctrl + 256 + 2 * 14336 * 4)
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 64, 100, 3, 1) == (
-        ctrl + 256 + 1280)  # 3 * 104 * 4 = 1248 -> 1280
+        ctrl + 256 + 1536)  # 3 * 112 * 4 = 1344 -> 1536
     # batched, B > 1: the larger of the per-token layout above and the
     # grouped MFMA layout: logits, x as two fp16 terms, five [P] pair arrays,
     # expert offsets / active list / count, act [P][I] and four K-slice

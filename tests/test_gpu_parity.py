@@ -274,12 +274,14 @@ def _fused_args(x, gw, buf, E, h, I, k, out, work, renorm=0):
                          ids=["small", "mixtral", "deepseek", "ragged"])
 def test_fused_handoff_never_times_out(cuda, shape):
     """Single-token fused kernel: every gate/up block incremented its arrival
-    counter (64 counters, 256 bytes apart; gate/up blocks = act chunks
-    k * ceil(ceil(I / 2) / 4) rounded up to a multiple of 32) and no down
-    block's bounded wait expired (timeout word after the counters).  The
-    workspace starts as junk: the router kernel must zero the control block on
-    every call.  The XCD flag (next word) says whether blocks ran on the XCDs
-    the act layout expects; either value gives correct results."""
+    counter (64 counters, 256 bytes apart) and no down block's bounded wait
+    expired (timeout word after the counters).  Gate/up blocks = act chunks
+    k * ceil(ceil(I / rpw) / 4), rounded up to a multiple of 8 * 32 / (4 rpw),
+    with rpw = 4 rows per wave for fp16 rows of at most 4 KB (h <= 2048, 16-byte
+    vectors), else 2.  The workspace starts as junk: the router kernel must
+    zero the control block on every call.  The XCD flag (next word) says
+    whether blocks ran on the XCDs the act layout expects; either value gives
+    correct results."""
     E, h, I, k = shape
     x, gw, buf = make_layer(E, h, I, F16, router_std=h ** -0.5, seed=2, device=cuda,
                             gen_device=cuda)
@@ -287,7 +289,10 @@ def test_fused_handoff_never_times_out(cuda, shape):
     work = torch.full((nws,), 0xAB, dtype=torch.uint8, device=cuda)
     out = torch.empty_like(x)
     a = _fused_args(x, gw, buf, E, h, I, k, out, work)
-    n1 = (k * (((I + 1) // 2 + 3) // 4) + 31) // 32 * 32
+    vec8 = h % 8 == 0 and I % 8 == 0
+    rpw = 4 if (vec8 and h * 2 <= 4096) else 2
+    group = 8 * (32 // (4 * rpw))
+    n1 = (k * (((I + rpw - 1) // rpw + 3) // 4) + group - 1) // group * group
     for _ in range(3):
         assert capi.call("wr_fused_moe", a, torch.cuda.current_stream().cuda_stream) == 0
         torch.cuda.synchronize()

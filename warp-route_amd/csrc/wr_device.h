@@ -119,22 +119,58 @@ __device__ __forceinline__ void wave_select_topk_reg(float l_in, int E, int k, i
   }
 }
 
-// Same, reading the E logits of one token from memory.  The reads are
-// wave-uniform scalar loads: every wave of a persistent grid reads the same
-// line at kernel start, and through the scalar cache that costs one L2
-// request per CU instead of one per wave (which serialises on one L2 channel).
-// `logits` must have WR_MAX_EXPERTS readable floats (entries >= E are ignored).
-__device__ __forceinline__ void wave_select_topk(const float* __restrict__ logits, int E, int k,
-                                                 int renorm, TopK& t) {
+// Lane e (< 16 NB) gets logit e from NB scalar loads of 16 floats, all issued
+// before the first is used.
+template <int NB>
+__device__ __forceinline__ float lane_logit(const float* __restrict__ logits) {
+  typedef float f16v __attribute__((ext_vector_type(16)));
   const int lane = threadIdx.x & (kWave - 1);
+  f16v v[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) v[b] = reinterpret_cast<const f16v*>(logits)[b];
   float l = 0.0f;
 #pragma unroll
-  for (int e = 0; e < WR_MAX_EXPERTS; ++e) {
-    const float v = __builtin_bit_cast(
-        float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, logits[e])));
-    l = (lane == e) ? v : l;
-  }
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) l = (lane == 16 * b + i) ? v[b][i] : l;
+  return l;
+}
+
+// Same, reading the E logits of one token from memory (16-byte aligned, with
+// WR_MAX_EXPERTS readable floats; entries >= E are ignored).  The reads are
+// wave-uniform scalar loads: every wave of a grid reads the same line at
+// kernel start, and through the scalar cache that costs one L2 request per
+// cache instead of one per wave (per-wave vector loads serialise on one L2
+// channel).  Only the 16-float batches that hold the E logits are loaded, all
+// in flight together: under a saturated memory system each extra round trip
+// before the first weight load costs microseconds per block.
+__device__ __forceinline__ void wave_select_topk(const float* __restrict__ logits, int E, int k,
+                                                 int renorm, TopK& t) {
+  float l;
+  if (E <= 16)
+    l = lane_logit<1>(logits);
+  else if (E <= 32)
+    l = lane_logit<2>(logits);
+  else
+    l = lane_logit<4>(logits);
   wave_select_topk_reg(l, E, k, renorm, t);
+}
+
+// Block-wide variant (every thread of the block must call it): for E <= 16
+// the wave-level scalar read above; for more experts wave 0 reads the logits
+// with one 256-byte vector load into LDS and every wave selects from there,
+// so the block waits for one memory round trip and sends one L2 request.
+__device__ __forceinline__ void block_select_topk(const float* __restrict__ logits, int E, int k,
+                                                  int renorm, TopK& t) {
+  if (E <= 16) {
+    wave_select_topk(logits, E, k, renorm, t);
+    return;
+  }
+  __shared__ float s_logits[WR_MAX_EXPERTS];
+  const int lane = threadIdx.x & (kWave - 1);
+  if (threadIdx.x < kWave) s_logits[lane] = logits[lane];
+  __syncthreads();
+  wave_select_topk_reg(s_logits[lane], E, k, renorm, t);
 }
 
 // Contiguous share [begin, end) of `total` items for worker w of n; shares

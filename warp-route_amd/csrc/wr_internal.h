@@ -41,19 +41,20 @@ struct FusedWs {
   static constexpr int kXccFlagWord = kTimeoutWord + kCounterStride;
   static constexpr int kCtrlWords = kCounters + 2;  // zeroed words, kCounterStride apart
   static constexpr size_t kCtrlBytes = (size_t)kCtrlWords * kCounterStride * 4;
-  // act rows are I rounded up to whole 8-column chunks.
-  static constexpr int kActCols = 8;
+  // Single-token act rows: I rounded up to whole chunks of `cols` columns, the
+  // columns one gate/up block computes (4 waves x rows per wave: 8 or 16).
+  static constexpr int kMaxActCols = 16;
 
   unsigned* ctrl;  // kCtrlBytes
   float* logits;   // [B][WR_MAX_EXPERTS]: token b's E logits, padded to 64
-  float* act;      // B == 1: [k][act_row(I)]; B > 1: [B][k][I].
+  float* act;      // B == 1: [k][act_row(I, cols)]; B > 1: [B][k][I].
                    // Values are already scaled by the gate weight.
 
-  __host__ __device__ static int64_t act_row(int I) {
-    return (int64_t)((I + kActCols - 1) / kActCols) * kActCols;
+  __host__ __device__ static int64_t act_row(int I, int cols) {
+    return (int64_t)((I + cols - 1) / cols) * cols;
   }
   static size_t act_floats(int I, int k, int B) {
-    return B == 1 ? (size_t)k * act_row(I) : (size_t)B * k * I;
+    return B == 1 ? (size_t)k * act_row(I, kMaxActCols) : (size_t)B * k * I;
   }
   static size_t bytes(int E, int I, int k, int B) {
     (void)E;

@@ -326,10 +326,11 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 // Single-token fused FFN: ONE launch, grid = [n1 gate/up blocks][n2 down
 // blocks], 4 waves per block.
 //
-// act is [k][act_row] fp32, in 8-column chunks; chunk G = kk * bpk + j holds
-// columns [8 j, 8 j + 8) of selected expert kk (bpk = chunks per expert).
-// Gate/up block b computes chunk G = chunk_of_block(b): its wave w computes
-// rows 8 j + 2 w and 8 j + 2 w + 1 of expert kk's gate and up matrices and
+// act is [k][act_row] fp32, in chunks of COLS = 4 RPW columns (RPW = rows
+// per wave, 2 or 4); chunk G = kk * bpk + j holds columns [COLS j, COLS j +
+// COLS) of selected expert kk (bpk = chunks per expert, act_row = bpk COLS).
+// Gate/up block b computes chunk G = chunk_of_block<LB>(b): its wave w
+// computes rows COLS j + RPW w .. + RPW of expert kk's gate and up matrices and
 // stores w_kk * silu(gate . x) * (up . x) with agent-scope stores, which are
 // written through to memory.  When all of them have completed, the block
 // increments arrival counter b mod 64 (the counters sit 256 bytes apart so
@@ -349,10 +350,11 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 //
 // Why down blocks read fresh act without invalidating L2 (each XCD has its
 // own L2, not coherent with the others): blocks are dispatched to the XCDs
-// round-robin, block b to XCD b mod 8.  chunk_of_block maps the four blocks
-// 32 m + 8 s + x (s = 0..3), which share XCD x, to the four chunks
-// 32 m + 4 x + s, i.e. one 128-byte L2 line.  So every act line is written by
-// one XCD only.  At kernel start no L2 holds act lines (the kernel-boundary
+// round-robin, block b to XCD b mod 8.  A 128-byte L2 line holds LB = 32 /
+// COLS chunks (4 or 2).  chunk_of_block<LB> maps the LB blocks
+// 8 LB m + 8 s + x (s < LB), which share XCD x, to the LB chunks
+// 8 LB m + LB x + s, i.e. one line.  So every act line is written by one XCD
+// only.  At kernel start no L2 holds act lines (the kernel-boundary
 // acquire invalidates them), and no wave reads act before every gate/up block
 // has arrived.  Hence an XCD's L2 holds an act line only if its own writers
 // put it there (all of the line's writers go through that L2) or if a reader
@@ -368,15 +370,16 @@ struct Handoff {
   unsigned* cnt;        // FusedWs::kCounters counters, FusedWs::kCounterStride words apart
   unsigned* timeout;    // set to 1 if a wait expired (results then invalid)
   unsigned* xcc_flag;   // set to 1 if a gate/up block ran on another XCD than b mod 8
-  int n1;               // gate/up blocks (the first n1 block ids), a multiple of 32
+  int n1;               // gate/up blocks (the first n1 block ids), a multiple of 8 LB
   int chunks;           // k * bpk
   unsigned spin_limit;  // polls before a wait gives up
 };
 
-// The chunk gate/up block b computes (a permutation of each aligned group of
-// 32 blocks).
+// The chunk gate/up block b computes: a permutation of each aligned group of
+// 8 LB blocks (LB = chunks per 128-byte act line).
+template <int LB>
 __host__ __device__ __forceinline__ int chunk_of_block(int b) {
-  return (b & ~31) + ((b & 7) << 2) + ((b >> 3) & 3);
+  return (b & ~(8 * LB - 1)) + (b & 7) * LB + ((b >> 3) & (LB - 1));
 }
 
 // Rows [r0, r0 + RPW) of selected expert kk's gate/up matrices; the results go
@@ -491,13 +494,15 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
     float* act, XT* __restrict__ out, int32_t* __restrict__ ids_out, float* __restrict__ w_out,
     Geom g, Handoff hs) {
   typedef typename WVec<WT, VEC>::type V;
-  static_assert(kWavesPerBlock * RPW == FusedWs::kActCols, "a gate/up block computes one chunk");
+  constexpr int COLS = kWavesPerBlock * RPW;  // act columns per gate/up block
+  constexpr int LB = 32 / COLS;               // chunks per 128-byte act line
+  static_assert(COLS * LB == 32 && COLS <= FusedWs::kMaxActCols, "unsupported rows per wave");
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int64_t act_row = FusedWs::act_row(g.I);
+  const int64_t act_row = FusedWs::act_row(g.I, COLS);
 
   TopK t;
-  wave_select_topk(logits, g.E, g.k, g.renorm, t);
+  block_select_topk(logits, g.E, g.k, g.renorm, t);
 
   if ((int)blockIdx.x < hs.n1) {
     // ---- gate/up block ----
@@ -512,7 +517,7 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
     }
     const int items = (g.I + RPW - 1) / RPW;
     const int bpk = (items + kWavesPerBlock - 1) / kWavesPerBlock;  // chunks per expert
-    const int G = chunk_of_block(blockIdx.x);
+    const int G = chunk_of_block<LB>(blockIdx.x);
     if (G < hs.chunks) {
       const int kk = G / bpk;
       const int it = (G - kk * bpk) * kWavesPerBlock + wave;
@@ -646,30 +651,48 @@ hipError_t logits_t(const Problem& p, float* logits, unsigned* zero, int nzero, 
   return hipGetLastError();
 }
 
+// Rows per gate/up wave of the single-token kernel: 4 (two column chunks in
+// flight) when a weight row is at most 4 KB, else 2 (four chunks in flight);
+// either way a wave reads about 32 KB per iteration, and short-row layers get
+// half as many blocks.
+int fused_rpw(const Problem& p) {
+  const int64_t row_bytes = (int64_t)p.h * (p.wdt == WR_F16 ? 2 : 4);
+  return (p.vec > 1 && row_bytes <= 4096) ? 4 : 2;
+}
+
 // act chunks of the single-token fused kernel, and its gate/up blocks (the
-// chunk count rounded up to whole groups of 32 blocks).
-int fused_chunks(int I, int k) {
-  const int items = (I + WR_GU_RPW - 1) / WR_GU_RPW;
+// chunk count rounded up to whole groups of 8 LB blocks).
+int fused_chunks(int I, int k, int rpw) {
+  const int items = (I + rpw - 1) / rpw;
   return k * ((items + kWavesPerBlock - 1) / kWavesPerBlock);
 }
-int fused_n1(int I, int k) { return (fused_chunks(I, k) + 31) / 32 * 32; }
+int fused_n1(int I, int k, int rpw) {
+  const int group = 8 * (32 / (kWavesPerBlock * rpw));
+  return (fused_chunks(I, k, rpw) + group - 1) / group * group;
+}
 
-template <typename WT, typename XT, int VEC>
-hipError_t fused_t(const Problem& p, const FusedWs& w, hipStream_t s) {
+template <typename WT, typename XT, int VEC, int RPW, int U1>
+hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   const Geom g = make_geom(p);
   Handoff hs;
   hs.cnt = w.ctrl;
   hs.timeout = w.ctrl + FusedWs::kTimeoutWord;
   hs.xcc_flag = w.ctrl + FusedWs::kXccFlagWord;
-  hs.n1 = fused_n1(p.I, p.k);
-  hs.chunks = fused_chunks(p.I, p.k);
+  hs.n1 = fused_n1(p.I, p.k, RPW);
+  hs.chunks = fused_chunks(p.I, p.k, RPW);
   hs.spin_limit = 1u << 20;
   const int n2 = (p.h + WR_FU_RPD - 1) / WR_FU_RPD;
-  hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, WR_GU_RPW, WR_GU_U, WR_FU_RPD, WR_FU_U>),
+  hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, WR_FU_RPD, WR_FU_U>),
                      dim3(hs.n1 + n2), dim3(kBlock), 0, s, static_cast<const WT*>(p.wbuf),
                      static_cast<const XT*>(p.x), w.logits, w.act, static_cast<XT*>(p.out),
                      p.topk_ids, p.topk_w, g, hs);
   return hipGetLastError();
+}
+
+template <typename WT, typename XT, int VEC>
+hipError_t fused_t(const Problem& p, const FusedWs& w, hipStream_t s) {
+  if (fused_rpw(p) == 4) return fused_rpw_t<WT, XT, VEC, 4, WR_GU_U / 2>(p, w, s);
+  return fused_rpw_t<WT, XT, VEC, 2, WR_GU_U>(p, w, s);
 }
 
 template <typename WT, typename XT, int VEC>
