@@ -16,6 +16,11 @@ bounded sample of the same layer.
 
   python bench.py [--steps K] [--warmup W] [--layers L] [--config mixtral]
   python bench.py --copy-probe     # plain device copy, for counter calibration
+
+Two further workloads of BASELINE.json configs[4] print their own JSON line
+(not the headline): --batch B[,B...] times batched_fused_moe on clustered
+Mixtral batches; --stack N times N independent Mixtral layers back to back,
+one token at a time (end-to-end MoE time per token).
 """
 from __future__ import annotations
 
@@ -94,6 +99,106 @@ def cpu_baseline(x, gw, buf, cfg, seconds: float):
     }
 
 
+def _timed(step, steps: int, warmup: int) -> float:
+    """Microseconds per call of step(i), K back-to-back calls between two
+    events on the current stream, after W untimed calls."""
+    import torch
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(steps):
+        step(i)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / steps
+
+
+def batched_bench(args) -> int:
+    """Batched decode: Mixtral layers, B tokens whose router logits
+    are biased toward one expert pair (synthetic.clustered_batch, alpha = 4),
+    through batched_fused_moe.  Bytes = the distinct selected experts' weights
+    per call, averaged over the rotated layers."""
+    import torch
+    from warp_route import functional as F
+    from warp_route.synthetic import CONFIGS, clustered_batch, make_config_layer
+    cfg = CONFIGS["mixtral"]
+    E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+    dev = torch.device("cuda:0")
+    layers = [make_config_layer(cfg, seed=s, device=dev, gen_device=dev)
+              for s in range(args.layers)]
+    for B in [int(v) for v in args.batch.split(",")]:
+        xs = [clustered_batch(gw, B, pair=(1, 2), alpha=4.0, seed=s, device=dev)
+              for s, (_, gw, _) in enumerate(layers)]
+        ids = torch.empty(B, k, dtype=torch.int32, device=dev)
+        distinct = []
+        for i, (_, gw, buf) in enumerate(layers):
+            F.batched_fused_moe(xs[i], gw, buf, E, h, I, k, cfg.renormalize, ids)
+            distinct.append(len(set(ids.cpu().numpy().ravel().tolist())))
+        L = len(layers)
+        us = _timed(lambda i: F.batched_fused_moe(xs[i % L], layers[i % L][1], layers[i % L][2],
+                                                  E, h, I, k, cfg.renormalize),
+                    args.steps, args.warmup)
+        nbytes = sum(distinct) / L * 3 * h * I * 2
+        gbps = nbytes / us / 1e3
+        print(json.dumps({
+            "metric": "µs per batched MoE layer call (Mixtral shape, clustered routing)",
+            "value": round(us, 2), "unit": "us/call", "higher_is_better": False,
+            "tokens_per_s": round(B / us * 1e6, 1), "us_per_token": round(us / B, 3),
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "dtype": "f16 weights, f32 accumulate",
+            "data": "synthetic (seeded random-init layers; clustered tokens, alpha 4)",
+            "config": {"workload": "mixtral MoE layer, batched decode", "batch": B,
+                       "distinct_experts_per_layer": distinct, "layers_rotated": L},
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                         "bytes": "distinct selected experts' fp16 weights"},
+        }), flush=True)
+    return 0
+
+
+def stack_bench(args) -> int:
+    """End-to-end MoE time per token through N independent Mixtral layers
+    (configs[4]: 32 layers, 90 GB of fp16 experts), one fused_moe call per
+    layer, back to back; every layer has its own token vector."""
+    import torch
+    from warp_route import functional as F
+    from warp_route.synthetic import CONFIGS, make_config_layer
+    cfg = CONFIGS["mixtral"]
+    E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+    dev = torch.device("cuda:0")
+    N = args.stack
+    log(f"[bench] generating {N} mixtral layers on the GPU")
+    stack = []
+    for s in range(N):
+        stack.append(make_config_layer(cfg, seed=s, device=dev, gen_device=dev))
+        if (s + 1) % 8 == 0:
+            log(f"[bench]   {s + 1} layers")
+    torch.cuda.synchronize()
+    weight_gb = sum(buf.numel() * buf.element_size() for _, _, buf in stack) / 1e9
+
+    def token(_):
+        for x, gw, buf in stack:
+            F.fused_moe(x, gw, buf, E, h, I, k, cfg.renormalize)
+
+    steps = max(1, args.steps // N)
+    us = _timed(token, steps, max(1, args.warmup // N))
+    nbytes = N * cfg.selected_bytes
+    gbps = nbytes / us / 1e3
+    print(json.dumps({
+        "metric": f"ms per token through a {N}-layer MoE stack (Mixtral shape, batch 1)",
+        "value": round(us / 1e3, 4), "unit": "ms/token", "higher_is_better": False,
+        "us_per_layer": round(us / N, 2), "n_gpus": 1, "tokens": steps,
+        "dtype": "f16 weights, f32 accumulate",
+        "data": "synthetic (seeded random-init layers drawn on the GPU)",
+        "config": {"workload": f"{N} independent mixtral MoE layers", "weights_GB": round(weight_gb, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4)},
+    }), flush=True)
+    return 0
+
+
 def copy_probe(nbytes: int, iters: int) -> dict:
     """Device-to-device copy of nbytes (torch's copy kernel): the achievable
     streaming ceiling, and the calibration run for FETCH_SIZE / WRITE_SIZE."""
@@ -124,6 +229,10 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true")
+    ap.add_argument("--batch", default=None,
+                    help="comma-separated batch sizes: time batched decode instead")
+    ap.add_argument("--stack", type=int, default=0,
+                    help="time one token through this many layers instead")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -141,6 +250,10 @@ def main() -> int:
     if args.copy_probe:
         print(json.dumps(copy_probe(1 << 30, 50)), flush=True)
         return 0
+    if args.batch:
+        return batched_bench(args)
+    if args.stack:
+        return stack_bench(args)
 
     from warp_route import functional as F
     from warp_route.synthetic import CONFIGS, make_config_layer
