@@ -228,22 +228,44 @@ __device__ __forceinline__ void tile_store(TokTile& xs, const H8 (&hi)[kTilePiec
   }
 }
 
-// A operand for MFMA j of a K step: lane l holds row (l % 16), columns
-// kb + 32 j + 8 (l / 16) .. +8; `w` already points at the lane's row and
-// 8 (l / 16) column offset.
-__device__ __forceinline__ void a_load(H8 (&a)[4], const f16* __restrict__ w, int kb) {
+// Weight tiles.  A wave's rows are loaded 4 rows x 256 bytes per instruction
+// (lane l: row 4 i + l / 16 of the instruction's group, 16 bytes at column
+// 8 (l % 16) of the K step): a streaming probe measured this pattern at 6.2
+// TB/s against 5.5 TB/s for MFMA fragments loaded straight from memory (16
+// rows x 64 bytes per instruction).  The wave stores its rows into its own LDS
+// tile (rows padded to 17 pieces, so the fragment reads below are free of bank
+// conflicts) and reads the MFMA A fragments from there: for MFMA j of the K
+// step, lane l takes row l % 16, columns 32 j + 8 (l / 16) .. + 8.
+template <int ROWS>
+struct WTile {
+  H8 w[ROWS][kLdsRow];
+};
+
+// Loads of one K step: ROWS / 4 instructions, group i = rows [4 i, 4 i + 4).
+// row_ptr(i) is this lane's address for group i at column 0 of the K step.
+template <int ROWS>
+__device__ __forceinline__ void w_load(H8 (&r)[ROWS / 4], const f16* const (&base)[ROWS / 4],
+                                       int kb) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) a[j] = load_w<f16, 8>(w + kb + 32 * j);
+  for (int i = 0; i < ROWS / 4; ++i) r[i] = load_w<f16, 8>(base[i] + kb);
+}
+
+template <int ROWS>
+__device__ __forceinline__ void w_store(WTile<ROWS>& t, const H8 (&r)[ROWS / 4], int lane) {
+#pragma unroll
+  for (int i = 0; i < ROWS / 4; ++i) t.w[4 * i + (lane >> 4)][lane & 15] = r[i];
 }
 
 // ---------------------------------------------------------------------------
 // Gate/up.  grid (I / 64, expert slots).  One pass covers up to 64 of the
 // expert's tokens as NT MFMA tiles of 16; NT is a template parameter so that
-// the K loop has no per-tile branches.
+// the K loop has no per-tile branches.  A wave's weight tile holds its 16 gate
+// rows (tile rows 0-15) and the same 16 up rows (tile rows 16-31).
 // ---------------------------------------------------------------------------
 template <bool LO, int NT>
-__device__ __forceinline__ void gu_pass(TokTile& xs, const f16* __restrict__ Gw,
-                                        const f16* __restrict__ Uw, const f16* __restrict__ x_hi,
+__device__ __forceinline__ void gu_pass(TokTile& xs, WTile<32>& wt,
+                                        const f16* const (&wbase)[8],
+                                        const f16* __restrict__ x_hi,
                                         const f16* __restrict__ x_lo, const BatchRoute& r,
                                         int p0, int mt, float* __restrict__ act, int row0,
                                         const Geom& g, int lane) {
@@ -254,40 +276,38 @@ __device__ __forceinline__ void gu_pass(TokTile& xs, const f16* __restrict__ Gw,
   tile_rows(off, r.pair_tok + p0, 0, mt, g.h);
   const int ns = g.h / kBK;
 
-  // Software pipeline, one K step deep: step s's weight and token loads are
-  // issued before step s-1's MFMAs.
-  H8 g0[4], u0[4], g1[4], u1[4], th[kTilePieces], tl[kTilePieces];
-  a_load(g0, Gw, 0);
-  a_load(u0, Uw, 0);
+  // Software pipeline, one K step deep: step s+1's weight and token loads are
+  // issued before step s's MFMAs.
+  H8 wr[8], th[kTilePieces], tl[kTilePieces];
+  w_load<32>(wr, wbase, 0);
   gu_tile_load(th, tl, x_hi, x_lo, off, 0, LO);
-  auto step = [&](const H8 (&gc)[4], const H8 (&uc)[4], H8 (&gn)[4], H8 (&un)[4], int s) {
-    __syncthreads();  // every wave is done reading the previous tile
+  for (int s = 0; s < ns; ++s) {
+    __syncthreads();  // every wave is done reading the previous tiles
     tile_store(xs, th, tl, LO);
+    w_store<32>(wt, wr, lane);
     __syncthreads();
     if (s + 1 < ns) {
-      a_load(gn, Gw, (s + 1) * kBK);
-      a_load(un, Uw, (s + 1) * kBK);
+      w_load<32>(wr, wbase, (s + 1) * kBK);
       gu_tile_load(th, tl, x_hi, x_lo, off, (s + 1) * kBK, LO);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const int c = 4 * j + (lane >> 4);
+      const H8 ga = wt.w[lane & 15][c];
+      const H8 ua = wt.w[16 + (lane & 15)][c];
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
-        const int tn = n * 16 + (lane & 15), c = 4 * j + (lane >> 4);
+        const int tn = n * 16 + (lane & 15);
         const H8 bh = xs.hi[tn][c];
-        ag[n] = mfma(gc[j], bh, ag[n]);
-        au[n] = mfma(uc[j], bh, au[n]);
+        ag[n] = mfma(ga, bh, ag[n]);
+        au[n] = mfma(ua, bh, au[n]);
         if (LO) {
           const H8 bl = xs.lo[tn][c];
-          ag[n] = mfma(gc[j], bl, ag[n]);
-          au[n] = mfma(uc[j], bl, au[n]);
+          ag[n] = mfma(ga, bl, ag[n]);
+          au[n] = mfma(ua, bl, au[n]);
         }
       }
     }
-  };
-  for (int s = 0; s < ns; s += 2) {
-    step(g0, u0, g1, u1, s);
-    if (s + 1 < ns) step(g1, u1, g0, u0, s + 1);
   }
 
   // D layout: lane holds token n*16 + (lane % 16), rows 4 (lane / 16) .. +4.
@@ -311,6 +331,7 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const f16* __restrict__ wbuf,
                                                   const f16* __restrict__ x_lo, BatchRoute r,
                                                   float* __restrict__ act, Geom g) {
   __shared__ TokTile xs;
+  __shared__ WTile<32> wts[kBlk / kWave];
   const int slot = blockIdx.y;
   if (slot >= *r.n_active) return;  // block-uniform
   const int e = r.active[slot];
@@ -318,16 +339,18 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const f16* __restrict__ wbuf,
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int row0 = blockIdx.x * kBM + wave * 16;
-  const f16* Gw =
-      wbuf + (int64_t)e * g.stride + (int64_t)(row0 + (lane & 15)) * g.h + (lane >> 4) * 8;
-  const f16* Uw = Gw + g.off_up;
+  const f16* G = wbuf + (int64_t)e * g.stride + (int64_t)(row0 + (lane >> 4)) * g.h + (lane & 15) * 8;
+  const f16* wbase[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) wbase[i] = G + (i < 4 ? 0 : g.off_up) + (int64_t)(4 * (i % 4)) * g.h;
+  WTile<32>& wt = wts[wave];
   for (int m0 = 0; m0 < M; m0 += kMaxTok) {
     const int mt = min(kMaxTok, M - m0);
     switch ((mt + 15) / 16) {
-      case 1: gu_pass<LO, 1>(xs, Gw, Uw, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
-      case 2: gu_pass<LO, 2>(xs, Gw, Uw, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
-      case 3: gu_pass<LO, 3>(xs, Gw, Uw, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
-      default: gu_pass<LO, 4>(xs, Gw, Uw, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
+      case 1: gu_pass<LO, 1>(xs, wt, wbase, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
+      case 2: gu_pass<LO, 2>(xs, wt, wbase, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
+      case 3: gu_pass<LO, 3>(xs, wt, wbase, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
+      default: gu_pass<LO, 4>(xs, wt, wbase, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
     }
   }
 }
@@ -337,7 +360,7 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const f16* __restrict__ wbuf,
 // [nsteps * ks / kKSplit, nsteps * (ks + 1) / kKSplit).
 // ---------------------------------------------------------------------------
 template <int NT>
-__device__ __forceinline__ void dn_pass(TokTile& xs, const f16* __restrict__ Dw,
+__device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt, const f16* const (&wbase)[4],
                                         const float* __restrict__ act, int p0, int mt, int sb,
                                         int se, float* __restrict__ y, int row0, const Geom& g,
                                         int lane) {
@@ -347,30 +370,29 @@ __device__ __forceinline__ void dn_pass(TokTile& xs, const f16* __restrict__ Dw,
   if (sb < se) {
     int64_t off[kTilePieces];
     tile_rows(off, nullptr, p0, mt, g.I);
-    H8 d0[4], d1[4], th[kTilePieces], tl[kTilePieces];
-    a_load(d0, Dw, sb * kBK);
+    H8 wr[4], th[kTilePieces], tl[kTilePieces];
+    w_load<16>(wr, wbase, sb * kBK);
     dn_tile_load(th, tl, act, off, sb * kBK);
-    auto step = [&](const H8 (&dc)[4], H8 (&dn)[4], int s) {
+    for (int s = sb; s < se; ++s) {
       __syncthreads();
       tile_store(xs, th, tl, true);
+      w_store<16>(wt, wr, lane);
       __syncthreads();
       if (s + 1 < se) {
-        a_load(dn, Dw, (s + 1) * kBK);
+        w_load<16>(wr, wbase, (s + 1) * kBK);
         dn_tile_load(th, tl, act, off, (s + 1) * kBK);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
+        const int c = 4 * j + (lane >> 4);
+        const H8 da = wt.w[lane & 15][c];
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
-          const int tn = n * 16 + (lane & 15), c = 4 * j + (lane >> 4);
-          acc[n] = mfma(dc[j], xs.hi[tn][c], acc[n]);
-          acc[n] = mfma(dc[j], xs.lo[tn][c], acc[n]);
+          const int tn = n * 16 + (lane & 15);
+          acc[n] = mfma(da, xs.hi[tn][c], acc[n]);
+          acc[n] = mfma(da, xs.lo[tn][c], acc[n]);
         }
       }
-    };
-    for (int s = sb; s < se; s += 2) {
-      step(d0, d1, s);
-      if (s + 1 < se) step(d1, d0, s + 1);
     }
   }
 #pragma unroll
@@ -385,6 +407,7 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const f16* __restrict__ wbuf, 
                                                   const float* __restrict__ act,
                                                   float* __restrict__ ypart, Geom g, int P) {
   __shared__ TokTile xs;
+  __shared__ WTile<16> wts[kBlk / kWave];
   const int slot = blockIdx.z;
   if (slot >= *r.n_active) return;
   const int e = r.active[slot];
@@ -396,16 +419,20 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const f16* __restrict__ wbuf, 
   const int nsteps = g.I / kBK;
   const int sb = nsteps * ks / BatchWs::kKSplit;
   const int se = nsteps * (ks + 1) / BatchWs::kKSplit;
-  const f16* Dw = wbuf + (int64_t)e * g.stride + g.off_down +
-                  (int64_t)(row0 + (lane & 15)) * g.I + (lane >> 4) * 8;
+  const f16* D = wbuf + (int64_t)e * g.stride + g.off_down +
+                 (int64_t)(row0 + (lane >> 4)) * g.I + (lane & 15) * 8;
+  const f16* wbase[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wbase[i] = D + (int64_t)(4 * i) * g.I;
   float* y = ypart + (int64_t)ks * P * g.h;
+  WTile<16>& wt = wts[wave];
   for (int m0 = 0; m0 < M; m0 += kMaxTok) {
     const int mt = min(kMaxTok, M - m0);
     switch ((mt + 15) / 16) {
-      case 1: dn_pass<1>(xs, Dw, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
-      case 2: dn_pass<2>(xs, Dw, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
-      case 3: dn_pass<3>(xs, Dw, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
-      default: dn_pass<4>(xs, Dw, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
+      case 1: dn_pass<1>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
+      case 2: dn_pass<2>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
+      case 3: dn_pass<3>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
+      default: dn_pass<4>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
     }
   }
 }
