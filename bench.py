@@ -19,8 +19,9 @@ bounded sample of the same layer.
 
 Two further workloads of BASELINE.json configs[4] print their own JSON line
 (not the headline): --batch B[,B...] times batched_fused_moe on clustered
-Mixtral batches; --stack N times N independent Mixtral layers back to back,
-one token at a time (end-to-end MoE time per token).
+Mixtral batches; --stack N [--graph] times one decode step through N
+independent Mixtral layers chained with residual adds (end-to-end MoE time
+per token), launched op by op and, with --graph, from one captured HIP graph.
 """
 from __future__ import annotations
 
@@ -160,39 +161,47 @@ def batched_bench(args) -> int:
 
 def stack_bench(args) -> int:
     """End-to-end MoE time per token through N independent Mixtral layers
-    (configs[4]: 32 layers, 90 GB of fp16 experts), one fused_moe call per
-    layer, back to back; every layer has its own token vector."""
+    (configs[4]: 32 layers, 90 GB of fp16 experts), chained with residual adds
+    (warp_route.stack.MoEStack): one decode step, launched op by op and, with
+    --graph, replayed from one captured HIP graph."""
     import torch
-    from warp_route import functional as F
+    from warp_route.stack import MoEStack
     from warp_route.synthetic import CONFIGS, make_config_layer
     cfg = CONFIGS["mixtral"]
     E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
     dev = torch.device("cuda:0")
     N = args.stack
     log(f"[bench] generating {N} mixtral layers on the GPU")
-    stack = []
+    layers, x0 = [], None
     for s in range(N):
-        stack.append(make_config_layer(cfg, seed=s, device=dev, gen_device=dev))
+        x, gw, buf = make_config_layer(cfg, seed=s, device=dev, gen_device=dev)
+        layers.append((gw, buf))
+        x0 = x if x0 is None else x0
         if (s + 1) % 8 == 0:
             log(f"[bench]   {s + 1} layers")
     torch.cuda.synchronize()
-    weight_gb = sum(buf.numel() * buf.element_size() for _, _, buf in stack) / 1e9
-
-    def token(_):
-        for x, gw, buf in stack:
-            F.fused_moe(x, gw, buf, E, h, I, k, cfg.renormalize)
-
+    weight_gb = sum(buf.numel() * buf.element_size() for _, buf in layers) / 1e9
+    stack = MoEStack(layers, E, h, I, k, cfg.renormalize, residual=True)
     steps = max(1, args.steps // N)
-    us = _timed(token, steps, max(1, args.warmup // N))
+    warm = max(1, args.warmup // N)
+    us_eager = _timed(lambda i: stack(x0), steps, warm)
+    us_graph = None
+    if args.graph:
+        graphed = stack.capture(x0)
+        us_graph = _timed(lambda i: graphed(x0), steps, warm)
+    us = us_graph if us_graph is not None else us_eager
     nbytes = N * cfg.selected_bytes
     gbps = nbytes / us / 1e3
     print(json.dumps({
         "metric": f"ms per token through a {N}-layer MoE stack (Mixtral shape, batch 1)",
         "value": round(us / 1e3, 4), "unit": "ms/token", "higher_is_better": False,
         "us_per_layer": round(us / N, 2), "n_gpus": 1, "tokens": steps,
+        "eager_ms_per_token": round(us_eager / 1e3, 4),
+        "graph_ms_per_token": None if us_graph is None else round(us_graph / 1e3, 4),
         "dtype": "f16 weights, f32 accumulate",
         "data": "synthetic (seeded random-init layers drawn on the GPU)",
-        "config": {"workload": f"{N} independent mixtral MoE layers", "weights_GB": round(weight_gb, 1)},
+        "config": {"workload": f"{N} independent mixtral MoE layers, residual chain",
+                   "weights_GB": round(weight_gb, 1), "graph": bool(args.graph)},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4)},
     }), flush=True)
@@ -233,6 +242,8 @@ def main() -> int:
                     help="comma-separated batch sizes: time batched decode instead")
     ap.add_argument("--stack", type=int, default=0,
                     help="time one token through this many layers instead")
+    ap.add_argument("--graph", action="store_true",
+                    help="with --stack: also replay the step from a captured HIP graph")
     args = ap.parse_args()
 
     if args.gpus != 1:

@@ -73,11 +73,11 @@ def test_layout_rejects_bad_arguments():
 
 def test_workspace_bytes():
     lib = capi.lib()
-    # fused: control block (64 arrival counters, a timeout flag and an XCD
-    # flag, one 256-byte line each) + 64 fp32 logits per token (E padded to
-    # 64) + act: single token k rows of I rounded up to 16 columns, B > 1
-    # B*k*I; fp32, rounded up to 256 bytes.
-    ctrl = 66 * 256
+    # fused: control block (64 arrival counters, a timeout flag, an unused
+    # word and 64 XCD-rotation masks, one 256-byte line each) + 64 fp32 logits
+    # per token (E padded to 64) + act: single token k rows of I rounded up to
+    # 16 columns, B > 1 B*k*I; fp32, rounded up to 256 bytes.
+    ctrl = 130 * 256
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 4096, 14336, 2, 1) == (
         ctrl + 256 + 2 * 14336 * 4)
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 64, 100, 3, 1) == (

@@ -132,3 +132,16 @@ def test_moelayer_pack_cache():
     assert b is not a
     ge, ue, de = O.expert_views(b.numpy(), 1, 3, 8, 4)
     np.testing.assert_array_equal(ue, layer.up_proj[1].data.half().numpy())
+
+
+def test_moe_stack_validates_layers():
+    from warp_route.stack import MoEStack
+    with pytest.raises(ValueError):
+        MoEStack([], 8, 64, 128, 2)
+    gw = torch.zeros(8, 64)
+    buf = torch.zeros(10)
+    with pytest.raises(ValueError, match="gate_w must be"):
+        MoEStack([(torch.zeros(4, 64), buf)], 8, 64, 128, 2)
+    stack = MoEStack([(gw, buf)], 8, 64, 128, 2)
+    with pytest.raises(ValueError, match="1D or 2D"):
+        stack(torch.zeros(2, 2, 64))

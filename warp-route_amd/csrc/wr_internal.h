@@ -33,13 +33,15 @@ constexpr size_t kWsAlign = 256;
 // Workspace carving.  Every region starts on a 256-byte boundary.
 struct FusedWs {
   // Single-token hand-off, one 256-byte line per word: kCounters arrival
-  // counters, the wait-timeout flag, and the flag "a gate/up block ran on an
-  // unexpected XCD".  The router kernel of each single-token call zeroes them.
+  // counters, the wait-timeout flag, an unused word, then kCounters XCD-
+  // rotation masks (gate/up block b ORs bit (its XCD - b) mod 8 into mask
+  // b mod kCounters).  The router kernel of each single-token call zeroes
+  // them.
   static constexpr int kCounters = 64;
   static constexpr int kCounterStride = 64;  // words (256 bytes)
   static constexpr int kTimeoutWord = kCounters * kCounterStride;
-  static constexpr int kXccFlagWord = kTimeoutWord + kCounterStride;
-  static constexpr int kCtrlWords = kCounters + 2;  // zeroed words, kCounterStride apart
+  static constexpr int kRotWord = kTimeoutWord + 2 * kCounterStride;
+  static constexpr int kCtrlWords = 2 * kCounters + 2;  // zeroed words, kCounterStride apart
   static constexpr size_t kCtrlBytes = (size_t)kCtrlWords * kCounterStride * 4;
   // Single-token act rows: I rounded up to whole chunks of `cols` columns, the
   // columns one gate/up block computes (4 waves x rows per wave: 8 or 16).

@@ -100,8 +100,9 @@ __device__ __forceinline__ float router_combine(const float* p) {
 
 // grid (E, B), block 256.  Token b's logits go to logits[b * 64 + e] (padded
 // so that consumers can read all 64 with scalar loads).  Block (0, 0) also
-// zeroes the words zero[i * zstride], i < nzero (the fused kernel's arrival
-// counters and timeout flag), which the next kernel on the stream reads.
+// zeroes the words zero[i * zstride], i < nzero <= kBlock (the fused kernel's
+// arrival counters, timeout flag and rotation masks), which the next kernel on
+// the stream reads.
 // With x_hi != nullptr, block (e, b) also writes its 1/E share of token b's x
 // as two fp16 terms, hi = fp16(x) and lo = fp16(x - hi) (lo = 0 for fp16 x),
 // for the batched MFMA path.
@@ -350,26 +351,29 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 //
 // Why down blocks read fresh act without invalidating L2 (each XCD has its
 // own L2, not coherent with the others): blocks are dispatched to the XCDs
-// round-robin, block b to XCD b mod 8.  A 128-byte L2 line holds LB = 32 /
-// COLS chunks (4 or 2).  chunk_of_block<LB> maps the LB blocks
-// 8 LB m + 8 s + x (s < LB), which share XCD x, to the LB chunks
+// round-robin, block b to XCD (b + r) mod 8 for some rotation r (0 for a
+// plain launch; a launch from a captured graph was measured at r = 7).  So
+// blocks whose indices agree mod 8 share an XCD.  A 128-byte L2 line holds
+// LB = 32 / COLS chunks (4 or 2).  chunk_of_block<LB> maps the LB blocks
+// 8 LB m + 8 s + x (s < LB), which share an XCD, to the LB chunks
 // 8 LB m + LB x + s, i.e. one line.  So every act line is written by one XCD
 // only.  At kernel start no L2 holds act lines (the kernel-boundary
 // acquire invalidates them), and no wave reads act before every gate/up block
 // has arrived.  Hence an XCD's L2 holds an act line only if its own writers
 // put it there (all of the line's writers go through that L2) or if a reader
-// fetched it from memory after it was complete.  Each gate/up block checks the
-// XCD it actually runs on (HW_REG_XCC_ID) and, if it is not b mod 8, raises a
-// flag; down blocks then fall back to a full agent-scope acquire (L2 and L1
-// invalidate).  Otherwise a down block only invalidates its CU's L1, in case
-// a writer on the same CU left a partial line there.  This saves the L2
+// fetched it from memory after it was complete.  Each gate/up block records
+// the rotation it actually ran with, (HW_REG_XCC_ID - b) mod 8, as a bit in
+// one of 64 masks; a down block ORs the 64 masks and, unless exactly one bit
+// is set (one rotation for the whole grid), falls back to a full agent-scope
+// acquire (L2 and L1 invalidate).  Otherwise it only invalidates its CU's L1,
+// in case a writer on the same CU left a partial line there.  This saves the L2
 // invalidate per down block (about 6 us per layer at the Mixtral shape) and
 // keeps act dense, so the readers' loads stay fully coalesced.
 // ---------------------------------------------------------------------------
 struct Handoff {
   unsigned* cnt;        // FusedWs::kCounters counters, FusedWs::kCounterStride words apart
   unsigned* timeout;    // set to 1 if a wait expired (results then invalid)
-  unsigned* xcc_flag;   // set to 1 if a gate/up block ran on another XCD than b mod 8
+  unsigned* rot;        // FusedWs::kCounters rotation masks, FusedWs::kCounterStride words apart
   int n1;               // gate/up blocks (the first n1 block ids), a multiple of 8 LB
   int chunks;           // k * bpk
   unsigned spin_limit;  // polls before a wait gives up
@@ -525,8 +529,10 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
         gateup_item<WT, XT, VEC, RPW, U1>(wbuf, x, act + kk * act_row + it * RPW, g, t, kk,
                                           it * RPW, lane);
     }
-    if (threadIdx.x == 0 && xcc_id() != (blockIdx.x & 7u))
-      __hip_atomic_store(hs.xcc_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0)
+      __hip_atomic_fetch_or(hs.rot + (blockIdx.x % FusedWs::kCounters) * FusedWs::kCounterStride,
+                            1u << ((xcc_id() - blockIdx.x) & 7u), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's act stores have completed
     __syncthreads();
     if (threadIdx.x == 0)
@@ -561,7 +567,15 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
       }
       __builtin_amdgcn_s_sleep(8);
     }
-    if (__hip_atomic_load(hs.xcc_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
+    // One rotation for every gate/up block <=> exactly one bit in the OR of
+    // the masks.
+    const unsigned m = __hip_atomic_load(hs.rot + c * FusedWs::kCounterStride, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    unsigned all = 0;
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit)
+      if (__ballot((m >> bit) & 1u) != 0) all |= 1u << bit;
+    if (__popc(all) != 1)
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     else
       invalidate_l1();
@@ -677,7 +691,7 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   Handoff hs;
   hs.cnt = w.ctrl;
   hs.timeout = w.ctrl + FusedWs::kTimeoutWord;
-  hs.xcc_flag = w.ctrl + FusedWs::kXccFlagWord;
+  hs.rot = w.ctrl + FusedWs::kRotWord;
   hs.n1 = fused_n1(p.I, p.k, RPW);
   hs.chunks = fused_chunks(p.I, p.k, RPW);
   hs.spin_limit = 1u << 20;
@@ -723,7 +737,8 @@ hipError_t ffn_x(const Problem& p, const FusedWs& w, hipStream_t s) {
 
 hipError_t run_ffn(const Problem& p, hipStream_t s) {
   const FusedWs w = FusedWs::carve(p.ws, p.E, p.I, p.k, p.B);
-  // The single-token kernel's counters and timeout flag start each call at zero.
+  // The single-token kernel's control words start each call at zero.
+  static_assert(FusedWs::kCtrlWords <= kBlock, "one router thread zeroes each control word");
   unsigned* zero = p.B == 1 ? w.ctrl : nullptr;
   const int nz = FusedWs::kCtrlWords, zs = FusedWs::kCounterStride;
   hipError_t err = p.adt == WR_F16 ? logits_t<f16>(p, w.logits, zero, nz, zs, s)
