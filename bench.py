@@ -15,6 +15,7 @@ cpu_baseline = the reference's pure-torch MoE (fp32, host cores) timed on a
 bounded sample of the same layer.
 
   python bench.py [--steps K] [--warmup W] [--layers L] [--config mixtral]
+  python bench.py --weights fp8    # the same layers in bf16 or fp8 E4M3 (not the headline)
   python bench.py --copy-probe     # plain device copy, for counter calibration
 
 Two further workloads of BASELINE.json configs[4] print their own JSON line
@@ -60,7 +61,8 @@ def cpu_baseline(x, gw, buf, cfg, seconds: float):
     """The reference's pure-torch MoE (tests/test_python.py:15-37, plus
     renormalisation) in fp32 on the host, on the same layer: router, softmax,
     top-k and the selected experts' FFN.  Only the selected experts are
-    materialised as fp32 host tensors (upcast from the same fp16 weights)."""
+    materialised as fp32 host tensors (upcast from the same fp16 weights;
+    bf16 and fp8 blocks are decoded, fp8 with its scales)."""
     import torch
     from oracle import moe_oracle as O
 
@@ -70,15 +72,15 @@ def cpu_baseline(x, gw, buf, cfg, seconds: float):
     xc, gwc = x.float().cpu(), gw.float().cpu()
     logits = gwc @ xc
     sel = torch.topk(torch.softmax(logits, 0), k).indices.tolist()
-    es = buf.element_size()
-    stride = O.layout_offsets(E, h, I, es)["expert_stride"] // es
-    nel = I * h
+    fmt = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16",
+           torch.float8_e4m3fn: "fp8"}[buf.dtype]
+    stride = O.weight_layout(E, h, I, fmt)["expert_stride"]
+    raw = buf.view(torch.uint8)
     gp, up, dp = [None] * E, [None] * E, [None] * E
     for e in sel:
-        base = e * stride
-        gp[e] = buf[base:base + nel].view(I, h).float().cpu()
-        up[e] = buf[base + nel:base + 2 * nel].view(I, h).float().cpu()
-        dp[e] = buf[base + 2 * nel:base + 3 * nel].view(h, I).float().cpu()
+        blk = raw[e * stride:(e + 1) * stride].cpu().numpy()
+        gp[e], up[e], dp[e] = (torch.from_numpy(m).float()
+                               for m in O.expert_matrices(blk, 0, E, h, I, fmt))
     for _ in range(2):
         O.torch_moe_reference_cpu(xc, gwc, gp, up, dp, k, cfg.renormalize)
     times = []
@@ -235,6 +237,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--config", default="mixtral", choices=["mixtral", "deepseek", "dbrx"])
+    ap.add_argument("--weights", default="fp16", choices=["fp16", "bf16", "fp8"],
+                    help="expert weight format (the headline is fp16)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true")
@@ -269,10 +273,11 @@ def main() -> int:
     from warp_route import functional as F
     from warp_route.synthetic import CONFIGS, make_config_layer
 
-    cfg = CONFIGS[args.config]
+    wdt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn}
+    cfg = CONFIGS[args.config].with_weights(wdt[args.weights])
     E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
     dev = torch.device("cuda:0")
-    log(f"[bench] generating {args.layers} {cfg.name} layers on the GPU")
+    log(f"[bench] generating {args.layers} {cfg.name} {args.weights} layers on the GPU")
     layers = [make_config_layer(cfg, seed=s, device=dev, gen_device=dev)
               for s in range(args.layers)]
     torch.cuda.synchronize()
@@ -316,7 +321,8 @@ def main() -> int:
 
     achieved = sel_bytes / (us * 1e-6) / 1e9
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"traffic_{cfg.name}.json")
+    suffix = "" if args.weights == "fp16" else f"_{args.weights}"
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{cfg.name}{suffix}.json")
     if os.path.exists(tfile):
         traffic = json.load(open(tfile)).get("hbm_bytes_per_call")
 
@@ -331,11 +337,12 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 weights, f32 accumulate",
+        "dtype": {"fp16": "f16", "bf16": "bf16", "fp8": "fp8 e4m3 (per-channel fp32 scales)"}[
+            args.weights] + " weights, f32 accumulate",
         "data": "synthetic (seeded random-init layers drawn on the GPU)",
         "config": {"workload": f"{cfg.name} MoE layer, decode batch 1", "hidden": h,
                    "intermediate": I, "experts": E, "top_k": k,
-                   "renormalize": cfg.renormalize, "weight_dtype": "fp16",
+                   "renormalize": cfg.renormalize, "weight_dtype": args.weights,
                    "x_dtype": "fp32", "layers_rotated": args.layers,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,

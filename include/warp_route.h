@@ -19,10 +19,10 @@
  *               behaviour)
  *   out       = sum_kk w[kk] * Wd_e (silu(Wg_e x) * (Wu_e x)),  e = ids[kk]
  *                                                        (src/fused_moe.cu:167-224)
- * Gating and accumulation are fp32.  Expert weights are fp32 or fp16 in the
- * packed expert layout (src/expert_layout.cuh:5-18): per expert
- * [gate I x h][up I x h][down h x I], row-major, expert stride rounded up to
- * 128 bytes.
+ * Gating and accumulation are fp32.  Expert weights are fp32, fp16, bf16 or
+ * fp8 (e4m3) in the packed expert layout (src/expert_layout.cuh:5-18): per
+ * expert [gate I x h][up I x h][down h x I], row-major, expert stride rounded
+ * up to 128 bytes.  fp8 blocks also hold fp32 scales (wr_layout_dtype).
  *
  * Streams: work is enqueued asynchronously on `stream` (a hipStream_t passed
  * as void*, NULL = the null stream).  The reference launched on the legacy
@@ -70,8 +70,12 @@ typedef enum wr_status {
   WR_EHIP = 100               /* a HIP runtime call failed                     */
 } wr_status;
 
-/* Element type tags. */
-typedef enum wr_dtype { WR_F32 = 0, WR_F16 = 1 } wr_dtype;
+/* Element type tags.  Expert weights may use any of them; x and out are
+ * WR_F32 or WR_F16.  WR_BF16 is bfloat16 (the top 16 bits of an fp32).
+ * WR_FP8_E4M3 is the OCP 8-bit float E4M3: sign, 4 exponent bits (bias 7),
+ * 3 mantissa bits, subnormals, no infinities, NaN = S.1111.111, largest
+ * finite value 448.  The reference stores fp32 only. */
+typedef enum wr_dtype { WR_F32 = 0, WR_F16 = 1, WR_BF16 = 2, WR_FP8_E4M3 = 3 } wr_dtype;
 
 /* Which entry point a workspace is sized for. */
 typedef enum wr_kind { WR_KIND_FUSED = 0, WR_KIND_BATCHED = 1, WR_KIND_NAIVE = 2 } wr_kind;
@@ -93,7 +97,7 @@ typedef struct wr_offsets {
 typedef struct wr_moe_args {
   const float *gate_w;     /* [E, h] fp32 router, row-major                      */
   const void *weight_buf;  /* packed experts, element type weight_dtype          */
-  int64_t weight_bytes;    /* bytes readable at weight_buf                       */
+  int64_t weight_bytes;    /* bytes readable at weight_buf, >= wr_weight_bytes() */
   int32_t weight_dtype;    /* wr_dtype                                           */
   int32_t num_experts;     /* E                                                  */
   int32_t hidden_dim;      /* h                                                  */
@@ -110,6 +114,29 @@ typedef struct wr_moe_args {
   size_t workspace_bytes;
 } wr_moe_args;
 
+/* Expert block layout for a weight dtype.  For WR_F32, WR_F16 and WR_BF16
+ * the offsets are those of wr_layout with elem_bytes 4, 2, 2 and
+ * scale_offset is -1.  For WR_FP8_E4M3 the three matrices hold 1-byte codes
+ * q at the same element offsets (gate 0, up I h, down 2 I h), followed at
+ * scale_offset = 3 I h rounded up to 16 bytes by three fp32 arrays of I
+ * values, s_gate, s_up and s_down, with
+ *   gate[r][c] = fp8(q_gate[r][c]) * s_gate[r]    (per gate row)
+ *   up[r][c]   = fp8(q_up[r][c])   * s_up[r]      (per up row)
+ *   down[r][c] = fp8(q_down[r][c]) * s_down[c]    (per down column)
+ * and expert_stride = scale_offset + 12 I rounded up to 128 bytes.  All three
+ * scale arrays are indexed by the intermediate index, so a kernel applies
+ * s_down to act (silu(gate x) * (up x)) instead of to the down rows.  Has no
+ * counterpart in the reference, whose layout is fp32 only. */
+typedef struct wr_layout_info {
+  int64_t gate_proj_offset;
+  int64_t up_proj_offset;
+  int64_t down_proj_offset;
+  int64_t scale_offset;   /* -1: no scales                                  */
+  int64_t expert_stride;
+  int32_t elem_bytes;     /* bytes per matrix element: 4, 2 or 1            */
+  int32_t weight_dtype;   /* wr_dtype                                       */
+} wr_layout_info;
+
 /* Human-readable name of a status code (never NULL). */
 WR_API const char *wr_status_str(int status);
 
@@ -123,6 +150,17 @@ WR_API int wr_layout(int num_experts, int hidden_dim, int intermediate_dim,
  * Replaces total_weight_bytes (src/expert_layout.cuh:74-77). */
 WR_API int64_t wr_total_weight_bytes(int num_experts, int hidden_dim,
                                      int intermediate_dim, int elem_bytes);
+
+/* Layout of one expert block of weight_dtype (see wr_layout_info).  Extends
+ * compute_offsets (src/expert_layout.cuh:34-47) to the reduced-precision
+ * weight types. */
+WR_API int wr_layout_dtype(int num_experts, int hidden_dim, int intermediate_dim,
+                           int weight_dtype, wr_layout_info *out);
+
+/* Total packed bytes of all experts for weight_dtype, or -1 for invalid
+ * arguments.  Extends total_weight_bytes (src/expert_layout.cuh:74-77). */
+WR_API int64_t wr_weight_bytes(int num_experts, int hidden_dim, int intermediate_dim,
+                               int weight_dtype);
 
 /* Device workspace an entry point of `kind` needs, or 0 for invalid
  * arguments.  The reference allocated naive scratch with cudaMalloc on every

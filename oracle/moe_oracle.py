@@ -21,9 +21,16 @@ Citations are ``file:line`` into that repository:
                                         src/naive_moe.cu:181-241
   torch_moe_reference_cpu               tests/test_python.py:15-37 (fp32 torch,
                                         plus the renormalise flag)
+  decode_bf16 / decode_e4m3 /           no reference counterpart (its weights are
+  weight_layout / expert_matrices       fp32 only): the bf16 and OCP fp8 E4M3
+                                        weight formats of include/warp_route.h
+                                        (wr_dtype, wr_layout_info), decoded
+                                        from their published bit layouts
 
 Every function is pinned by tests in ``tests/test_oracle.py`` against checks
-that do not retype its formula: hand-computed byte tables and padding cases
+that do not retype its formula (the decoders: every bf16 and E4M3 code
+against torch's own dtype conversions; the fp8 layout: hand-computed byte
+tables): hand-computed byte tables and padding cases
 for the layout, pack/unpack round trips, math.fsum exact sums for the
 logits, scipy's softmax and brute-force sorting for the selection,
 constructed exact ties, pure-Python loops on tiny shapes and the identity /
@@ -105,6 +112,92 @@ def expert_views(buf: np.ndarray, e: int, num_experts: int, hidden_dim: int,
     g = buf[base + off["gate_proj_offset"] // es:][:n].reshape(intermediate_dim, hidden_dim)
     u = buf[base + off["up_proj_offset"] // es:][:n].reshape(intermediate_dim, hidden_dim)
     d = buf[base + off["down_proj_offset"] // es:][:n].reshape(hidden_dim, intermediate_dim)
+    return g, u, d
+
+
+# ----------------------------------------------------------------------------
+# Reduced-precision weight formats (no reference counterpart)
+# ----------------------------------------------------------------------------
+WEIGHT_FORMATS = ("f32", "f16", "bf16", "fp8")
+
+
+def decode_bf16(bits: np.ndarray) -> np.ndarray:
+    """bfloat16 bit patterns (uint16) -> float64: the 16 bits are the high
+    half of an IEEE binary32."""
+    b = np.asarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)
+    with np.errstate(invalid="ignore"):  # signalling NaN patterns stay NaN
+        return b.view(np.float32).astype(np.float64)
+
+
+def decode_e4m3(codes: np.ndarray) -> np.ndarray:
+    """OCP 8-bit float E4M3 codes (uint8) -> float64.  Bits s.eeee.mmm,
+    exponent bias 7: e = 0 is subnormal, (-1)^s * m/8 * 2^-6; otherwise
+    (-1)^s * (1 + m/8) * 2^(e-7); s.1111.111 is NaN; there are no infinities
+    (the largest finite value, s.1111.110, is 448)."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 0xF
+    m = (c & 0x7).astype(np.float64)
+    mag = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    mag = np.where((e == 0xF) & (m == 7), np.nan, mag)
+    return sign * mag
+
+
+def weight_layout(num_experts: int, hidden_dim: int, intermediate_dim: int,
+                  fmt: str) -> Dict[str, int]:
+    """Expert block layout per weight format (wr_layout_dtype).  f32, f16 and
+    bf16: layout_offsets with 4, 2, 2 bytes per element and no scales.  fp8:
+    1-byte codes at element offsets 0, I h, 2 I h; scales at 3 I h rounded up
+    to 16 bytes (fp32 s_gate[I], s_up[I], s_down[I]); stride rounded up to
+    128 bytes."""
+    if fmt not in WEIGHT_FORMATS:
+        raise ValueError(f"unknown weight format {fmt!r}")
+    if fmt != "fp8":
+        es = {"f32": 4, "f16": 2, "bf16": 2}[fmt]
+        out = layout_offsets(num_experts, hidden_dim, intermediate_dim, es)
+        out.update(scale_offset=-1, elem_bytes=es)
+        return out
+    n = intermediate_dim * hidden_dim
+    sc = (3 * n + 15) // 16 * 16
+    stride = (sc + 12 * intermediate_dim + EXPERT_ALIGN - 1) // EXPERT_ALIGN * EXPERT_ALIGN
+    return {"gate_proj_offset": 0, "up_proj_offset": n, "down_proj_offset": 2 * n,
+            "scale_offset": sc, "expert_stride": stride, "elem_bytes": 1}
+
+
+def expert_matrices(raw: np.ndarray, e: int, num_experts: int, hidden_dim: int,
+                    intermediate_dim: int, fmt: str):
+    """(gate [I,h], up [I,h], down [h,I]) of expert e as float64, decoded from
+    the raw bytes (uint8) of a packed buffer in weight format ``fmt``.  fp8
+    matrices are dequantized: gate and up rows times their row scale, down
+    columns times their column scale."""
+    raw = np.asarray(raw, dtype=np.uint8)
+    lo = weight_layout(num_experts, hidden_dim, intermediate_dim, fmt)
+    h, I = hidden_dim, intermediate_dim
+    n = I * h
+    base = e * lo["expert_stride"]
+    es = lo["elem_bytes"]
+
+    def mat(off, rows, cols):
+        b = raw[base + off:base + off + n * es]
+        if fmt == "f32":
+            v = b.view(np.float32).astype(np.float64)
+        elif fmt == "f16":
+            v = b.view(np.float16).astype(np.float64)
+        elif fmt == "bf16":
+            v = decode_bf16(b.view(np.uint16))
+        else:
+            v = decode_e4m3(b)
+        return v.reshape(rows, cols)
+
+    g = mat(lo["gate_proj_offset"], I, h)
+    u = mat(lo["up_proj_offset"], I, h)
+    d = mat(lo["down_proj_offset"], h, I)
+    if fmt == "fp8":
+        sc = raw[base + lo["scale_offset"]:base + lo["scale_offset"] + 12 * I]
+        s = sc.view(np.float32).astype(np.float64).reshape(3, I)
+        g = g * s[0][:, None]
+        u = u * s[1][:, None]
+        d = d * s[2][None, :]
     return g, u, d
 
 

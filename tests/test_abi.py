@@ -22,8 +22,9 @@ def declared_symbols():
 
 def test_header_declares_the_expected_entry_points():
     assert sorted(declared_symbols()) == sorted([
-        "wr_status_str", "wr_layout", "wr_total_weight_bytes", "wr_workspace_bytes",
-        "wr_gate_topk", "wr_fused_moe", "wr_batched_fused_moe", "wr_naive_moe"])
+        "wr_status_str", "wr_layout", "wr_total_weight_bytes", "wr_layout_dtype",
+        "wr_weight_bytes", "wr_workspace_bytes", "wr_gate_topk", "wr_fused_moe",
+        "wr_batched_fused_moe", "wr_naive_moe"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -40,7 +41,8 @@ def test_header_constants_match_binding():
     for name in ("WR_OK", "WR_EINVAL_NULL", "WR_EINVAL_SHAPE", "WR_EINVAL_TOPK",
                  "WR_EINVAL_EXPERTS", "WR_EINVAL_DTYPE", "WR_EINVAL_WEIGHT_SIZE",
                  "WR_EINVAL_WORKSPACE", "WR_EINVAL_BATCH", "WR_EINVAL_KIND", "WR_EHIP",
-                 "WR_F32", "WR_F16", "WR_KIND_FUSED", "WR_KIND_BATCHED", "WR_KIND_NAIVE"):
+                 "WR_F32", "WR_F16", "WR_BF16", "WR_FP8_E4M3", "WR_KIND_FUSED",
+                 "WR_KIND_BATCHED", "WR_KIND_NAIVE"):
         m = re.search(rf"\b{name} = (\d+)", text)
         assert m and int(m.group(1)) == getattr(capi, name), name
 
@@ -50,6 +52,39 @@ def test_struct_layout_matches_header_order():
     assert ctypes.sizeof(capi.WrMoeArgs) == 104
     assert capi.WrMoeArgs.x.offset == 56
     assert ctypes.sizeof(capi.WrOffsets) == 32
+    assert ctypes.sizeof(capi.WrLayoutInfo) == 48
+
+
+FMT = {capi.WR_F32: "f32", capi.WR_F16: "f16", capi.WR_BF16: "bf16", capi.WR_FP8_E4M3: "fp8"}
+TDT = {capi.WR_F32: "float32", capi.WR_F16: "float16", capi.WR_BF16: "bfloat16",
+       capi.WR_FP8_E4M3: "float8_e4m3fn"}
+
+
+@pytest.mark.parametrize("wdt", sorted(FMT))
+@pytest.mark.parametrize("E,h,I", [(8, 4096, 14336), (64, 2048, 1408), (2, 3, 5), (3, 7, 1)])
+def test_layout_dtype_agrees_with_python_and_oracle(E, h, I, wdt):
+    import torch
+    from oracle import moe_oracle as O
+    got = capi.layout_dtype(E, h, I, wdt)
+    want = O.weight_layout(E, h, I, FMT[wdt])
+    assert {k: got[k] for k in want} == want and got["weight_dtype"] == wdt
+    assert F.weight_layout(E, h, I, getattr(torch, TDT[wdt])) == want
+    assert capi.lib().wr_weight_bytes(E, h, I, wdt) == E * want["expert_stride"]
+
+
+def test_fp8_layout_byte_table():
+    """Hand-computed: E=8, h=4096, I=14336 (Mixtral): codes 3 I h =
+    176,160,768 bytes (a multiple of 16), then 12 I = 172,032 bytes of
+    scales; 176,332,800 is a multiple of 128.  h=3, I=5: codes 45 bytes,
+    scales at 48, 60 bytes of them, stride 128."""
+    assert capi.layout_dtype(8, 4096, 14336, capi.WR_FP8_E4M3) == {
+        "gate_proj_offset": 0, "up_proj_offset": 58720256, "down_proj_offset": 117440512,
+        "scale_offset": 176160768, "expert_stride": 176332800, "elem_bytes": 1,
+        "weight_dtype": capi.WR_FP8_E4M3}
+    lo = capi.layout_dtype(2, 3, 5, capi.WR_FP8_E4M3)
+    assert (lo["up_proj_offset"], lo["down_proj_offset"], lo["scale_offset"],
+            lo["expert_stride"]) == (15, 30, 48, 128)
+    assert capi.layout_dtype(2, 3, 5, capi.WR_BF16)["scale_offset"] == -1
 
 
 @pytest.mark.parametrize("E,h,I,es", [(8, 4096, 14336, 2), (64, 2048, 1408, 2),
@@ -69,6 +104,11 @@ def test_layout_rejects_bad_arguments():
     assert lib.wr_layout(1, 4, 4, 3, ctypes.byref(o)) == capi.WR_EINVAL_DTYPE
     assert lib.wr_layout(1, 4, 4, 2, None) == capi.WR_EINVAL_NULL
     assert lib.wr_total_weight_bytes(1, 0, 4, 2) == -1
+    info = capi.WrLayoutInfo()
+    assert lib.wr_layout_dtype(1, 4, 4, 4, ctypes.byref(info)) == capi.WR_EINVAL_DTYPE
+    assert lib.wr_layout_dtype(1, 4, 0, 1, ctypes.byref(info)) == capi.WR_EINVAL_SHAPE
+    assert lib.wr_layout_dtype(1, 4, 4, 1, None) == capi.WR_EINVAL_NULL
+    assert lib.wr_weight_bytes(1, 4, 4, -1) == -1
 
 
 def test_workspace_bytes():
@@ -138,8 +178,9 @@ CASES = [
     ("num_experts", 65, capi.WR_EINVAL_EXPERTS),
     ("top_k", 0, capi.WR_EINVAL_TOPK),
     ("top_k", 7, capi.WR_EINVAL_TOPK),
-    ("weight_dtype", 2, capi.WR_EINVAL_DTYPE),
+    ("weight_dtype", 4, capi.WR_EINVAL_DTYPE),
     ("act_dtype", -1, capi.WR_EINVAL_DTYPE),
+    ("act_dtype", capi.WR_BF16, capi.WR_EINVAL_DTYPE),
     ("gate_w", None, capi.WR_EINVAL_NULL),
     ("x", None, capi.WR_EINVAL_NULL),
     ("out", None, capi.WR_EINVAL_NULL),
@@ -156,6 +197,20 @@ def test_validation_codes(entry, field, value, want):
     a = valid_args()
     setattr(a, field, value)
     assert capi.call(entry, a) == want
+
+
+@pytest.mark.parametrize("wdt", [capi.WR_BF16, capi.WR_FP8_E4M3])
+def test_weight_size_is_checked_per_format(wdt):
+    """One byte short of wr_weight_bytes is rejected for every format (the
+    fp8 layout is smaller than fp16's, and holds its scales)."""
+    a = valid_args()
+    a.weight_dtype = wdt
+    need = capi.lib().wr_weight_bytes(a.num_experts, a.hidden_dim, a.intermediate_dim, wdt)
+    a.weight_bytes = need - 1
+    a.workspace = None  # so that a passing size check still stops before HIP
+    assert capi.call("wr_fused_moe", a) == capi.WR_EINVAL_WEIGHT_SIZE
+    a.weight_bytes = need
+    assert capi.call("wr_fused_moe", a) == capi.WR_EINVAL_WORKSPACE
 
 
 def test_top_k_above_num_experts_is_rejected():

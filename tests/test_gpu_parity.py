@@ -23,6 +23,8 @@ from warp_route.synthetic import CONFIGS, clustered_batch, make_config_layer, ma
 pytestmark = pytest.mark.gpu
 
 F32, F16 = torch.float32, torch.float16
+BF16, FP8 = torch.bfloat16, torch.float8_e4m3fn
+WNAME = {F32: "f32", F16: "f16", BF16: "bf16", FP8: "fp8"}
 
 # (E, h, I, k, weight dtype, renormalize)
 SMALL = [
@@ -43,7 +45,7 @@ SMALL = [
 
 def ids_of(c):
     E, h, I, k, wd, rn = c
-    return f"E{E}-h{h}-I{I}-k{k}-{'f16' if wd == F16 else 'f32'}{'-renorm' if rn else ''}"
+    return f"E{E}-h{h}-I{I}-k{k}-{WNAME[wd]}{'-renorm' if rn else ''}"
 
 
 def robust_layer(E, h, I, wd, k, device, x_dtype=F32, batch=None, seed0=0):
@@ -73,6 +75,53 @@ def test_single_token_parity(cuda, op, cfg, x_dtype):
     ws = torch.empty(k, dtype=torch.float32, device=cuda)
     fn = F.fused_moe if op == "fused" else F.naive_moe
     print(f"[gpu] {op} {ids_of(cfg)} x={x_dtype} seed={seed}", flush=True)
+    out = fn(x, gw, buf, E, h, I, k, rn, ids, ws)
+    torch.cuda.synchronize()
+    assert out.dtype == x_dtype and out.shape == (h,)
+    ref = oracle_token(x, gw, buf, E, h, I, k, rn)
+    assert_parity(out, ids, ws, ref, rel_tol=out_tol(x_dtype), label=f"{op} {ids_of(cfg)}")
+
+
+# Reduced-precision weights: bf16, and fp8 E4M3 with per-channel scales.
+LOWP = [
+    (8, 256, 512, 2, BF16, False),
+    (8, 256, 512, 2, FP8, True),
+    (64, 256, 512, 6, FP8, False),
+    (16, 512, 1024, 4, FP8, True),
+    (8, 1024, 2048, 2, BF16, True),
+    (8, 4096, 1024, 2, FP8, True),    # 4 KB fp8 rows
+    (8, 6144, 512, 2, FP8, False),    # fp8 rows longer than 4 KB
+    (8, 6144, 512, 2, BF16, False),   # bf16 rows longer than 4 KB: 2 rows per wave
+    (5, 100, 36, 2, BF16, False),     # h % 8 != 0: scalar path
+    (5, 100, 36, 2, FP8, True),       # h % 16 != 0: scalar path
+    (3, 48, 40, 3, FP8, False),       # I % 16 != 0: scalar path, k == E
+]
+
+
+@pytest.mark.parametrize("x_dtype", [F32, F16], ids=["xf32", "xf16"])
+@pytest.mark.parametrize("cfg", LOWP, ids=ids_of)
+@pytest.mark.parametrize("op", ["fused", "naive", "batched"])
+def test_low_precision_weight_parity(cuda, op, cfg, x_dtype):
+    """The oracle decodes the same bf16 / fp8 bytes (fp8: codes times their
+    gate-row, up-row and down-column scales) and runs the fp64 layer; the bar
+    is the same as for fp16 weights."""
+    E, h, I, k, wd, rn = cfg
+    B = 3 if op == "batched" else None
+    x, gw, buf, seed = robust_layer(E, h, I, wd, k, cuda, x_dtype, batch=B)
+    print(f"[gpu] lowp {op} {ids_of(cfg)} x={x_dtype} seed={seed}", flush=True)
+    if op == "batched":
+        ids = torch.empty(B, k, dtype=torch.int32, device=cuda)
+        ws = torch.empty(B, k, dtype=torch.float32, device=cuda)
+        out = F.batched_fused_moe(x, gw, buf, E, h, I, k, rn, ids, ws)
+        torch.cuda.synchronize()
+        for b in range(B):
+            ref = oracle_token(x[b], gw, buf, E, h, I, k, rn)
+            assert_parity(out[b], ids[b], ws[b], ref, rel_tol=out_tol(x_dtype),
+                          label=f"batched {ids_of(cfg)} b={b}")
+        return
+    ids = torch.empty(k, dtype=torch.int32, device=cuda)
+    ws = torch.empty(k, dtype=torch.float32, device=cuda)
+    fn = F.fused_moe if op == "fused" else F.naive_moe
     out = fn(x, gw, buf, E, h, I, k, rn, ids, ws)
     torch.cuda.synchronize()
     assert out.dtype == x_dtype and out.shape == (h,)
@@ -290,7 +339,8 @@ def _fused_args(x, gw, buf, E, h, I, k, out, work, renorm=0):
     a = capi.WrMoeArgs()
     a.gate_w, a.weight_buf = gw.data_ptr(), buf.data_ptr()
     a.weight_bytes = buf.numel() * buf.element_size()
-    a.weight_dtype = capi.WR_F16
+    a.weight_dtype = {F32: capi.WR_F32, F16: capi.WR_F16, BF16: capi.WR_BF16,
+                      FP8: capi.WR_FP8_E4M3}[buf.dtype]
     a.act_dtype = capi.WR_F16 if x.dtype == torch.float16 else capi.WR_F32
     a.num_experts, a.hidden_dim, a.intermediate_dim, a.top_k = E, h, I, k
     a.renormalize, a.batch_size = renorm, 1
@@ -299,31 +349,35 @@ def _fused_args(x, gw, buf, E, h, I, k, out, work, renorm=0):
     return a
 
 
-@pytest.mark.parametrize("shape", [(16, 512, 256, 4), (8, 4096, 14336, 2), (64, 2048, 1408, 6),
-                                   (8, 192, 100, 3)],
-                         ids=["small", "mixtral", "deepseek", "ragged"])
+@pytest.mark.parametrize("shape", [(16, 512, 256, 4, F16), (8, 4096, 14336, 2, F16),
+                                   (64, 2048, 1408, 6, F16), (8, 192, 100, 3, F16),
+                                   (8, 4096, 14336, 2, FP8), (16, 6144, 10752, 4, FP8)],
+                         ids=["small", "mixtral", "deepseek", "ragged", "mixtral-fp8",
+                              "dbrx-fp8"])
 def test_fused_handoff_never_times_out(cuda, shape):
     """Single-token fused kernel: every gate/up block incremented its arrival
     counter (64 counters, 256 bytes apart) and no down block's bounded wait
     expired (timeout word after the counters).  Gate/up blocks = act chunks
     k * ceil(ceil(I / rpw) / 4), rounded up to a multiple of 8 * 32 / (4 rpw),
     with rpw = 4 rows per wave for fp16 rows of at most 4 KB (h <= 2048, 16-byte
-    vectors), else 2.  The workspace starts as junk: the router kernel must
+    vectors) and for all 16-byte-vector fp8 rows, else 2.  The workspace starts as junk: the router kernel must
     zero the control block on every call.  The 64 rotation masks (after the
     timeout word and one unused word) each hold one bit per XCD rotation
     (XCD - block) mod 8 that gate/up blocks b with b mod 64 equal to the
     mask's index ran with; masks of indices with no blocks stay zero.  Any set
     of bits gives correct results (more than one rotation switches the down
     blocks to a full acquire)."""
-    E, h, I, k = shape
-    x, gw, buf = make_layer(E, h, I, F16, router_std=h ** -0.5, seed=2, device=cuda,
+    E, h, I, k, wd = shape
+    x, gw, buf = make_layer(E, h, I, wd, router_std=h ** -0.5, seed=2, device=cuda,
                             gen_device=cuda)
     nws = capi.lib().wr_workspace_bytes(capi.WR_KIND_FUSED, E, h, I, k, 1)
     work = torch.full((nws,), 0xAB, dtype=torch.uint8, device=cuda)
     out = torch.empty_like(x)
     a = _fused_args(x, gw, buf, E, h, I, k, out, work)
-    vec8 = h % 8 == 0 and I % 8 == 0
-    rpw = 4 if (vec8 and h * 2 <= 4096) else 2
+    if wd == FP8:
+        rpw = 4 if (h % 16 == 0 and I % 16 == 0) else 2
+    else:
+        rpw = 4 if (h % 8 == 0 and I % 8 == 0 and h * 2 <= 4096) else 2
     group = 8 * (32 // (4 * rpw))
     n1 = (k * (((I + rpw - 1) // rpw + 3) // 4) + group - 1) // group * group
     for _ in range(3):
@@ -416,26 +470,29 @@ def test_moelayer(cuda):
 FULL = ["mixtral", "deepseek", "dbrx"]
 
 
+@pytest.mark.parametrize("wd", [F16, FP8, BF16], ids=["f16", "fp8", "bf16"])
 @pytest.mark.parametrize("name", FULL)
 @pytest.mark.parametrize("op", ["fused", "naive"])
-def test_full_size_configs(cuda, name, op):
+def test_full_size_configs(cuda, name, op, wd):
     """BASELINE configs at full size (weights drawn on the GPU), parity on the
-    selected experts."""
-    cfg = CONFIGS[name]
+    selected experts; also with the same layers in fp8 and bf16."""
+    if wd == BF16 and name != "mixtral":
+        pytest.skip("bf16 shares the fp16 kernels' geometry; Mixtral covers it")
+    cfg = CONFIGS[name].with_weights(wd)
     E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
     for seed in range(20):
         x, gw, buf = make_config_layer(cfg, seed=seed, device=cuda, gen_device=cuda)
         if O.selection_is_robust(f64(gw), f64(x), k):
             break
         del buf
-    print(f"[gpu] full {name} {op} seed={seed}", flush=True)
+    print(f"[gpu] full {name} {op} {WNAME[wd]} seed={seed}", flush=True)
     ids = torch.empty(k, dtype=torch.int32, device=cuda)
     ws = torch.empty(k, dtype=torch.float32, device=cuda)
     fn = F.fused_moe if op == "fused" else F.naive_moe
     out = fn(x, gw, buf, E, h, I, k, cfg.renormalize, ids, ws)
     torch.cuda.synchronize()
     ref = oracle_token(x, gw, buf, E, h, I, k, cfg.renormalize)
-    assert_parity(out, ids, ws, ref, label=f"{name} {op}")
+    assert_parity(out, ids, ws, ref, label=f"{name} {op} {WNAME[wd]}")
     del buf
     torch.cuda.empty_cache()
 

@@ -145,3 +145,64 @@ def test_moe_stack_validates_layers():
     stack = MoEStack([(gw, buf)], 8, 64, 128, 2)
     with pytest.raises(ValueError, match="1D or 2D"):
         stack(torch.zeros(2, 2, 64))
+
+
+def test_fp8_packer_error_bound_and_scales():
+    """_pack_expert_weights(float8_e4m3fn): decoded by the oracle, every
+    element is within half an E4M3 step of the original (2^-4 relative in the
+    normal range, 2^-10 * scale among subnormals); each gate/up row's and each
+    down column's largest |value| lands exactly on +-448 * scale."""
+    E, h, I = 3, 40, 24
+    g = torch.Generator().manual_seed(0)
+    mats = [[torch.randn(s, generator=g) * 0.03 for s in ((I, h), (I, h), (h, I))]
+            for _ in range(E)]
+    mats[1][0][3].zero_()  # an all-zero gate row: scale 1, codes 0
+    buf = F._pack_expert_weights([m[0] for m in mats], [m[1] for m in mats],
+                                 [m[2] for m in mats], E, h, I, dtype=torch.float8_e4m3fn)
+    assert buf.dtype == torch.float8_e4m3fn
+    raw = buf.view(torch.uint8).numpy()
+    lo = F.weight_layout(E, h, I, torch.float8_e4m3fn)
+    for e in range(E):
+        dq = O.expert_matrices(raw, e, E, h, I, "fp8")
+        sc = raw[e * lo["expert_stride"] + lo["scale_offset"]:][:12 * I].view(np.float32)
+        sc = sc.reshape(3, I).astype(np.float64)
+        for j, (w, d) in enumerate(zip(mats[e], dq)):
+            w = w.double().numpy()
+            s = sc[j][:, None] if j < 2 else sc[j][None, :]
+            bound = np.maximum(np.abs(w) * 2.0 ** -4, s * 2.0 ** -10) * (1 + 1e-6)
+            assert np.all(np.abs(d - w) <= bound), (e, j)
+            amax = np.abs(w).max(axis=1 if j < 2 else 0)
+            np.testing.assert_allclose(sc[j], np.where(amax > 0, amax / 448.0, 1.0), rtol=1e-6)
+            top = np.abs(d).max(axis=1 if j < 2 else 0)
+            np.testing.assert_allclose(top, amax, rtol=1e-6)
+    assert np.all(O.expert_matrices(raw, 1, E, h, I, "fp8")[0][3] == 0)
+
+
+def test_bf16_packer_is_exact_cast():
+    E, h, I = 2, 16, 8
+    g = torch.Generator().manual_seed(1)
+    mats = [[torch.randn(s, generator=g) for s in ((I, h), (I, h), (h, I))] for _ in range(E)]
+    buf = F._pack_expert_weights([m[0] for m in mats], [m[1] for m in mats],
+                                 [m[2] for m in mats], E, h, I, dtype=torch.bfloat16)
+    raw = buf.view(torch.uint8).numpy()
+    for e in range(E):
+        for w, d in zip(mats[e], O.expert_matrices(raw, e, E, h, I, "bf16")):
+            np.testing.assert_array_equal(d, w.to(torch.bfloat16).double().numpy())
+
+
+def test_synthetic_fp8_layer_is_the_quantized_fp32_layer():
+    """Same seed, same draws: the fp8 layer decodes to within the E4M3 bound
+    of the fp32 layer, and the router and x are identical."""
+    x8, gw8, b8 = make_layer(4, 64, 32, torch.float8_e4m3fn, seed=5)
+    x32, gw32, b32 = make_layer(4, 64, 32, torch.float32, seed=5)
+    assert torch.equal(x8, x32) and torch.equal(gw8, gw32)
+    r8, r32 = b8.view(torch.uint8).numpy(), b32.view(torch.uint8).numpy()
+    for e in range(4):
+        for d, w in zip(O.expert_matrices(r8, e, 4, 64, 32, "fp8"),
+                        O.expert_matrices(r32, e, 4, 64, 32, "f32")):
+            assert np.abs(d - w).max() <= 2.0 ** -4 * np.abs(w).max() * (1 + 1e-6)
+
+
+def test_moelayer_rejects_unknown_weight_dtype():
+    with pytest.raises(ValueError, match="weight_dtype"):
+        warp_route.MoELayer(4, 32, 32, 2, weight_dtype=torch.int8)

@@ -258,3 +258,79 @@ def test_batch_rows_equal_single_token_results():
         r = O.moe_forward(xb[b], gw.numpy(), buf, E, h, I, 2, True)
         np.testing.assert_array_equal(rb["out"][b], r["out"])
         np.testing.assert_array_equal(rb["ids"][b], r["ids"])
+
+
+# ----------------------------------------------------------------------------
+# Reduced-precision weight formats
+# ----------------------------------------------------------------------------
+def test_decode_e4m3_matches_torch_for_every_code():
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).to(torch.float64).numpy()
+    got = O.decode_e4m3(codes)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    np.testing.assert_array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
+    # hand-checked codes: 1.0, -1.0, 448 (largest), 2^-9 (smallest subnormal), NaN
+    assert O.decode_e4m3(np.array([0x38, 0xB8, 0x7E, 0x01], np.uint8)).tolist() == [
+        1.0, -1.0, 448.0, 2.0 ** -9]
+    assert np.isnan(O.decode_e4m3(np.array([0x7F, 0xFF], np.uint8))).all()
+
+
+def test_decode_bf16_matches_torch_for_every_code():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).to(torch.float64).numpy()
+    got = O.decode_bf16(bits)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(got)
+    np.testing.assert_array_equal(got[ok], want[ok])
+
+
+def _raw_block(layout, codes, scales=None):
+    raw = np.zeros(layout["expert_stride"], np.uint8)
+    raw[:len(codes)] = codes
+    if scales is not None:
+        sc = np.asarray(scales, np.float32).view(np.uint8)
+        raw[layout["scale_offset"]:layout["scale_offset"] + len(sc)] = sc
+    return raw
+
+
+def test_fp8_expert_matrices_hand_computed():
+    """E=1, h=2, I=2: gate codes 1, -1 / 2, 0.5; up 1.5, 2^-6 / 0, -2; down
+    1, 2 / -1, 0.5.  Scales: gate rows (2, 3), up rows (0.25, 4), down
+    columns (10, 100).  Down is scaled per column: down[r][c] * s_down[c]."""
+    lo = O.weight_layout(1, 2, 2, "fp8")
+    assert (lo["up_proj_offset"], lo["down_proj_offset"], lo["scale_offset"],
+            lo["expert_stride"]) == (4, 8, 16, 128)
+    codes = [0x38, 0xB8, 0x40, 0x30,   # gate
+             0x3C, 0x08, 0x00, 0xC0,   # up
+             0x38, 0x40, 0xB8, 0x30]   # down
+    raw = _raw_block(lo, codes, [2, 3, 0.25, 4, 10, 100])
+    g, u, d = O.expert_matrices(raw, 0, 1, 2, 2, "fp8")
+    np.testing.assert_array_equal(g, [[2.0, -2.0], [6.0, 1.5]])
+    np.testing.assert_array_equal(u, [[0.375, 0.25 * 2.0 ** -6], [0.0, -8.0]])
+    np.testing.assert_array_equal(d, [[10.0, 200.0], [-10.0, 50.0]])
+
+
+def test_bf16_expert_matrices_hand_computed():
+    """bf16 0x3F80 = 1.0, 0xC000 = -2.0, 0x3F00 = 0.5, 0x4040 = 3.0."""
+    lo = O.weight_layout(1, 1, 2, "bf16")
+    vals = np.array([0x3F80, 0xC000, 0x3F00, 0x4040, 0x3F80, 0x3F00], np.uint16)
+    raw = _raw_block(lo, vals.view(np.uint8))
+    g, u, d = O.expert_matrices(raw, 0, 1, 1, 2, "bf16")
+    np.testing.assert_array_equal(g, [[1.0], [-2.0]])
+    np.testing.assert_array_equal(u, [[0.5], [3.0]])
+    np.testing.assert_array_equal(d, [[1.0, 0.5]])
+
+
+@pytest.mark.parametrize("fmt,np_dt", [("f32", np.float32), ("f16", np.float16)])
+def test_expert_matrices_agree_with_expert_views(fmt, np_dt):
+    rng = np.random.default_rng(0)
+    E, h, I = 3, 5, 7
+    mats = [[rng.standard_normal(s).astype(np_dt) for s in ((I, h), (I, h), (h, I))]
+            for _ in range(E)]
+    buf = O.pack_expert_weights([m[0] for m in mats], [m[1] for m in mats],
+                                [m[2] for m in mats], E, h, I, dtype=np_dt)
+    for e in range(E):
+        a = O.expert_matrices(buf.view(np.uint8), e, E, h, I, fmt)
+        b = O.expert_views(buf, e, E, h, I)
+        for x, y in zip(a, b):
+            np.testing.assert_array_equal(x, y.astype(np.float64))

@@ -8,8 +8,9 @@
 //   topk_ids=None      optional int32 [k] / [B,k] output of selected experts
 //   topk_weights=None  optional fp32 [k] / [B,k] output of their weights
 // Differences from the reference, all compatible with its call forms:
-//   * weight_buf may be float32 (the reference layout) or float16; hidden may
-//     be float32 or float16 and the output takes its dtype; gate_w is float32.
+//   * weight_buf may be float32 (the reference layout), float16, bfloat16 or
+//     float8_e4m3fn (codes plus fp32 scales, wr_layout_dtype); hidden may be
+//     float32 or float16 and the output takes its dtype; gate_w is float32.
 //   * top_k may be 1..min(6, num_experts) on every op (the reference's fused
 //     and batched ops accepted only 1 or 2, src/bindings.cpp:75,117).
 //   * work is enqueued on the current HIP stream of hidden's device and the
@@ -39,6 +40,19 @@ int dtype_tag(const torch::Tensor& t, const char* name) {
   return -1;
 }
 
+int weight_dtype_tag(const torch::Tensor& t) {
+  switch (t.scalar_type()) {
+    case torch::kFloat32: return WR_F32;
+    case torch::kFloat16: return WR_F16;
+    case torch::kBFloat16: return WR_BF16;
+    case torch::kFloat8_e4m3fn: return WR_FP8_E4M3;
+    default:
+      TORCH_CHECK(false, "weight_buf must be float32, float16, bfloat16 or float8_e4m3fn, got ",
+                  t.scalar_type());
+  }
+  return -1;
+}
+
 void check_common(const torch::Tensor& gate_w, const torch::Tensor& weight_buf, int num_experts,
                   int hidden_dim, int intermediate_dim, int top_k,
                   const torch::Device& dev) {
@@ -50,7 +64,7 @@ void check_common(const torch::Tensor& gate_w, const torch::Tensor& weight_buf, 
               gate_w.sizes());
   WR_CHECK_DEVICE(weight_buf);
   WR_CHECK_CONTIGUOUS(weight_buf);
-  dtype_tag(weight_buf, "weight_buf");
+  const int wdt = weight_dtype_tag(weight_buf);
   TORCH_CHECK(gate_w.device() == dev && weight_buf.device() == dev,
               "hidden, gate_w and weight_buf must be on the same device");
   TORCH_CHECK(num_experts >= 1 && hidden_dim >= 1 && intermediate_dim >= 1,
@@ -60,7 +74,7 @@ void check_common(const torch::Tensor& gate_w, const torch::Tensor& weight_buf, 
   TORCH_CHECK(top_k >= 1 && top_k <= WR_MAX_TOPK && top_k <= num_experts,
               "top_k must be in [1, min(", WR_MAX_TOPK, ", num_experts)], got ", top_k);
   const int64_t es = weight_buf.element_size();
-  const int64_t need = wr_total_weight_bytes(num_experts, hidden_dim, intermediate_dim, (int)es);
+  const int64_t need = wr_weight_bytes(num_experts, hidden_dim, intermediate_dim, wdt);
   TORCH_CHECK(weight_buf.numel() * es >= need, "weight_buf too small: need ", need,
               " bytes, got ", weight_buf.numel() * es);
 }
@@ -84,7 +98,7 @@ wr_moe_args make_args(const torch::Tensor& hidden, const torch::Tensor& gate_w,
   a.gate_w = gate_w.data_ptr<float>();
   a.weight_buf = weight_buf.data_ptr();
   a.weight_bytes = weight_buf.numel() * (int64_t)weight_buf.element_size();
-  a.weight_dtype = dtype_tag(weight_buf, "weight_buf");
+  a.weight_dtype = weight_dtype_tag(weight_buf);
   a.num_experts = E;
   a.hidden_dim = h;
   a.intermediate_dim = I;
@@ -263,11 +277,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("gate_w"), py::arg("weight_buf"), py::arg("num_experts"), py::arg("hidden_dim"),
         py::arg("intermediate_dim"), py::arg("top_k"), py::arg("renormalize") = false, opt, optw);
   m.def("fused_moe_forward", &fused_moe_forward,
-        "Fused decode MoE forward for one token (fp32 or fp16 weights)", py::arg("hidden"),
+        "Fused decode MoE forward for one token (fp32, fp16, bf16 or fp8 e4m3 weights)", py::arg("hidden"),
         py::arg("gate_w"), py::arg("weight_buf"), py::arg("num_experts"), py::arg("hidden_dim"),
         py::arg("intermediate_dim"), py::arg("top_k"), py::arg("renormalize") = false, opt, optw);
   m.def("batched_fused_moe_forward", &batched_fused_moe_forward,
-        "Batched fused MoE forward for B tokens (fp32 or fp16 weights)", py::arg("hidden_batch"),
+        "Batched fused MoE forward for B tokens (fp32, fp16, bf16 or fp8 e4m3 weights)", py::arg("hidden_batch"),
         py::arg("gate_w"), py::arg("weight_buf"), py::arg("num_experts"), py::arg("hidden_dim"),
         py::arg("intermediate_dim"), py::arg("top_k"), py::arg("renormalize") = false, opt, optw);
   m.def("gate_topk", &gate_topk, "Router logits, softmax and top-K", py::arg("hidden"),
@@ -278,4 +292,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("total_weight_bytes", &wr_total_weight_bytes, "Packed layout size in bytes (-1 if invalid)",
         py::arg("num_experts"), py::arg("hidden_dim"), py::arg("intermediate_dim"),
         py::arg("elem_bytes"));
+  m.def("weight_bytes", &wr_weight_bytes,
+        "Packed layout size in bytes for a wr_dtype tag (-1 if invalid)", py::arg("num_experts"),
+        py::arg("hidden_dim"), py::arg("intermediate_dim"), py::arg("weight_dtype"));
 }

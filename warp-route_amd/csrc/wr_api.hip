@@ -36,7 +36,37 @@ int check_dims(int E, int h, int I, int k) {
   return WR_OK;
 }
 
-bool dtype_ok(int d) { return d == WR_F32 || d == WR_F16; }
+bool act_dtype_ok(int d) { return d == WR_F32 || d == WR_F16; }
+
+// Bytes per matrix element of a weight dtype, 0 if unknown.
+int weight_es(int d) {
+  switch (d) {
+    case WR_F32: return 4;
+    case WR_F16: return 2;
+    case WR_BF16: return 2;
+    case WR_FP8_E4M3: return 1;
+    default: return 0;
+  }
+}
+
+// Expert block layout of a weight dtype (arguments already checked).
+wr_layout_info layout_of(int64_t E, int64_t h, int64_t I, int wdt) {
+  wr_layout_info o;
+  o.weight_dtype = wdt;
+  o.elem_bytes = weight_es(wdt);
+  o.gate_proj_offset = 0;
+  o.scale_offset = -1;
+  if (wdt != WR_FP8_E4M3) {
+    o.expert_stride = stride_bytes(E, h, I, o.elem_bytes, &o.up_proj_offset, &o.down_proj_offset);
+    return o;
+  }
+  o.up_proj_offset = I * h;
+  o.down_proj_offset = 2 * I * h;
+  o.scale_offset = (3 * I * h + 15) / 16 * 16;
+  const int64_t raw = o.scale_offset + 3 * I * 4;
+  o.expert_stride = (raw + WR_EXPERT_ALIGN - 1) / WR_EXPERT_ALIGN * WR_EXPERT_ALIGN;
+  return o;
+}
 
 size_t ws_bytes(int kind, int E, int h, int I, int k, int B) {
   switch (kind) {
@@ -59,7 +89,7 @@ size_t ws_bytes(int kind, int E, int h, int I, int k, int B) {
 // 16-byte aligned weight and activation pointers); anything else takes the
 // scalar path.
 int choose_vec(const wr_moe_args* a) {
-  const int v = a->weight_dtype == WR_F16 ? 8 : 4;
+  const int v = 16 / weight_es(a->weight_dtype);
   if (a->hidden_dim % v != 0 || a->intermediate_dim % v != 0) return 1;
   if (reinterpret_cast<uintptr_t>(a->weight_buf) % 16 != 0) return 1;
   if (reinterpret_cast<uintptr_t>(a->x) % 16 != 0) return 1;
@@ -71,7 +101,7 @@ int validate(const wr_moe_args* a, int kind, Problem* p) {
   if (a == nullptr) return WR_EINVAL_NULL;
   int st = check_dims(a->num_experts, a->hidden_dim, a->intermediate_dim, a->top_k);
   if (st != WR_OK) return st;
-  if (!dtype_ok(a->weight_dtype) || !dtype_ok(a->act_dtype)) return WR_EINVAL_DTYPE;
+  if (weight_es(a->weight_dtype) == 0 || !act_dtype_ok(a->act_dtype)) return WR_EINVAL_DTYPE;
   const bool single = kind == WR_KIND_FUSED || kind == WR_KIND_NAIVE;
   if (single ? a->batch_size != 1 : a->batch_size < 0) return WR_EINVAL_BATCH;
   if (a->batch_size == 0) {
@@ -83,17 +113,16 @@ int validate(const wr_moe_args* a, int kind, Problem* p) {
     if (a->topk_ids == nullptr || a->topk_weights == nullptr) return WR_EINVAL_NULL;
   } else {
     if (a->weight_buf == nullptr || a->out == nullptr) return WR_EINVAL_NULL;
-    const int es = a->weight_dtype == WR_F16 ? 2 : 4;
-    int64_t up = 0, down = 0;
-    const int64_t stride =
-        stride_bytes(a->num_experts, a->hidden_dim, a->intermediate_dim, es, &up, &down);
-    if (a->weight_bytes < stride * a->num_experts) return WR_EINVAL_WEIGHT_SIZE;
+    const wr_layout_info lo =
+        layout_of(a->num_experts, a->hidden_dim, a->intermediate_dim, a->weight_dtype);
+    if (a->weight_bytes < lo.expert_stride * a->num_experts) return WR_EINVAL_WEIGHT_SIZE;
     const size_t need = ws_bytes(kind, a->num_experts, a->hidden_dim, a->intermediate_dim,
                                  a->top_k, a->batch_size);
     if (a->workspace == nullptr || a->workspace_bytes < need) return WR_EINVAL_WORKSPACE;
-    p->stride_b = stride;
-    p->off_up_b = up;
-    p->off_down_b = down;
+    p->stride_b = lo.expert_stride;
+    p->off_up_b = lo.up_proj_offset;
+    p->off_down_b = lo.down_proj_offset;
+    p->off_scale_b = lo.scale_offset;
   }
   p->gate_w = a->gate_w;
   p->wbuf = a->weight_buf;
@@ -128,7 +157,8 @@ WR_API const char* wr_status_str(int status) {
     case WR_EINVAL_SHAPE: return "num_experts, hidden_dim and intermediate_dim must be >= 1";
     case WR_EINVAL_TOPK: return "top_k must be in [1, min(6, num_experts)]";
     case WR_EINVAL_EXPERTS: return "num_experts exceeds WR_MAX_EXPERTS (64)";
-    case WR_EINVAL_DTYPE: return "unsupported dtype (weights and activations must be fp32 or fp16)";
+    case WR_EINVAL_DTYPE:
+      return "unsupported dtype (weights: fp32, fp16, bf16 or fp8 e4m3; activations: fp32 or fp16)";
     case WR_EINVAL_WEIGHT_SIZE: return "weight_buf is smaller than the packed expert layout";
     case WR_EINVAL_WORKSPACE: return "workspace is NULL or smaller than wr_workspace_bytes()";
     case WR_EINVAL_BATCH: return "invalid batch_size";
@@ -155,6 +185,23 @@ WR_API int64_t wr_total_weight_bytes(int num_experts, int hidden_dim, int interm
                                      int elem_bytes) {
   wr_offsets o;
   if (wr_layout(num_experts, hidden_dim, intermediate_dim, elem_bytes, &o) != WR_OK) return -1;
+  return (int64_t)num_experts * o.expert_stride;
+}
+
+WR_API int wr_layout_dtype(int num_experts, int hidden_dim, int intermediate_dim,
+                           int weight_dtype, wr_layout_info* out) {
+  if (out == nullptr) return WR_EINVAL_NULL;
+  if (num_experts < 1 || hidden_dim < 1 || intermediate_dim < 1) return WR_EINVAL_SHAPE;
+  if (weight_es(weight_dtype) == 0) return WR_EINVAL_DTYPE;
+  *out = layout_of(num_experts, hidden_dim, intermediate_dim, weight_dtype);
+  return WR_OK;
+}
+
+WR_API int64_t wr_weight_bytes(int num_experts, int hidden_dim, int intermediate_dim,
+                               int weight_dtype) {
+  wr_layout_info o;
+  if (wr_layout_dtype(num_experts, hidden_dim, intermediate_dim, weight_dtype, &o) != WR_OK)
+    return -1;
   return (int64_t)num_experts * o.expert_stride;
 }
 

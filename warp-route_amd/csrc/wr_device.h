@@ -18,6 +18,19 @@ typedef _Float16 f16;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Storage tags of weight types without arithmetic here: bfloat16 and OCP fp8
+// E4M3 (sign, 4 exponent bits with bias 7, 3 mantissa bits).  Pointer
+// arithmetic on them steps by their size; wdec decodes them.
+struct bf16w {
+  uint16_t bits;
+};
+struct fp8w {
+  uint8_t bits;
+};
+static_assert(sizeof(bf16w) == 2 && sizeof(fp8w) == 1, "weight tags must be packed");
 
 // Shape and layout of one MoE problem, passed to kernels by value.  Offsets
 // and the expert stride are in elements of the weight type: the stride is a
@@ -25,6 +38,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 struct Geom {
   int E, h, I, k, renorm, B;
   int64_t stride, off_up, off_down;
+  int64_t off_scale;  // fp8 only: byte offset of the scales in an expert block
 };
 
 // ---------------------------------------------------------------------------
@@ -209,8 +223,8 @@ __device__ __forceinline__ float topk_w(const TopK& t, int kk) {
 }
 
 // ---------------------------------------------------------------------------
-// Vector loads.  VEC elements per lane: 8 x fp16 or 4 x fp32 is one 128-bit
-// access; VEC = 1 is the scalar path for unaligned shapes.
+// Vector loads.  VEC elements per lane: 16 x fp8, 8 x fp16 / bf16 or 4 x fp32
+// is one 128-bit access; VEC = 1 is the scalar path for unaligned shapes.
 // ---------------------------------------------------------------------------
 template <typename T, int VEC>
 struct WVec;
@@ -222,6 +236,20 @@ template <>
 struct WVec<float, 4> { typedef f32x4 type; };
 template <>
 struct WVec<float, 1> { typedef float type; };
+template <>
+struct WVec<bf16w, 8> { typedef u32x4 type; };
+template <>
+struct WVec<bf16w, 1> { typedef uint16_t type; };
+template <>
+struct WVec<fp8w, 16> { typedef u32x4 type; };
+template <>
+struct WVec<fp8w, 1> { typedef uint8_t type; };
+
+// Natural vector width of a weight type: elements per 128-bit access.
+template <typename WT>
+constexpr int wvec_width() {
+  return 16 / (int)sizeof(WT);
+}
 
 // Streaming weight load: read once per call, so mark it non-temporal.
 template <typename T, int VEC>
@@ -238,9 +266,44 @@ __device__ __forceinline__ float velem(const V& v, int i) {
   }
 }
 
+// Element i of a loaded weight vector as fp32 (exact for every type).  bf16
+// is the top half of an fp32; fp8 E4M3 goes through v_cvt_pk_f32_fp8, which
+// on gfx950 decodes the OCP E4M3 format (checked against all 256 codes) and
+// converts two bytes per instruction (the pair is shared by i and i ^ 1).
+template <typename WT, typename V>
+__device__ __forceinline__ float wdec(const V& v, int i) {
+  if constexpr (std::is_same<WT, bf16w>::value) {
+    if constexpr (std::is_same<V, uint16_t>::value) {
+      return __uint_as_float((uint32_t)v << 16);
+    } else {
+      const uint32_t w = v[i >> 1];
+      return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
+    }
+  } else if constexpr (std::is_same<WT, fp8w>::value) {
+    if constexpr (std::is_same<V, uint8_t>::value) {
+      return __builtin_amdgcn_cvt_pk_f32_fp8((int)v, false)[0];
+    } else {
+      const int w = (int)v[i >> 2];
+      const f32x2 pr = (i & 2) ? __builtin_amdgcn_cvt_pk_f32_fp8(w, true)
+                               : __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+      return pr[i & 1];
+    }
+  } else {
+    return velem(v, i);
+  }
+}
+
+// Per-row fp8 scales of expert block `blk` (three fp32 arrays of I values at
+// byte offset off_scale: gate rows, up rows, down columns).
+template <typename WT>
+__device__ __forceinline__ const float* wscales(const WT* blk, int64_t off_scale) {
+  return reinterpret_cast<const float*>(reinterpret_cast<const char*>(blk) + off_scale);
+}
+
 template <typename V>
 __device__ __forceinline__ V vzero() {
-  if constexpr (std::is_same<V, f16>::value || std::is_same<V, float>::value) {
+  if constexpr (std::is_same<V, f16>::value || std::is_same<V, float>::value ||
+                std::is_integral<V>::value) {
     return V(0);
   } else {
     V z;
@@ -262,10 +325,13 @@ __device__ __forceinline__ void load_x(const XT* __restrict__ p, float (&v)[VEC]
       v[4 * q + 2] = t[2];
       v[4 * q + 3] = t[3];
     }
-  } else if constexpr (std::is_same<XT, f16>::value && VEC == 8) {
-    const f16x8 t = *reinterpret_cast<const f16x8*>(p);
+  } else if constexpr (std::is_same<XT, f16>::value && VEC % 8 == 0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (float)t[i];
+    for (int q = 0; q < VEC / 8; ++q) {
+      const f16x8 t = *reinterpret_cast<const f16x8*>(p + 8 * q);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[8 * q + i] = (float)t[i];
+    }
   } else if constexpr (std::is_same<XT, f16>::value && VEC == 4) {
     const f16x4 t = *reinterpret_cast<const f16x4*>(p);
 #pragma unroll

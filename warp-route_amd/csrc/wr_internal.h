@@ -24,7 +24,8 @@ struct Problem {
   char* ws;
   size_t ws_bytes;
   int64_t stride_b, off_up_b, off_down_b;  // layout, bytes
-  int vec;  // elements per lane per weight access: 8 (fp16), 4 (fp32) or 1
+  int64_t off_scale_b;  // fp8 scales [3][I] fp32 within an expert block, bytes; -1 if none
+  int vec;  // elements per lane per weight access: 16 / element bytes, or 1
 };
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }

@@ -167,6 +167,22 @@ __global__ __launch_bounds__(1024) void k_gate_topk(const float* __restrict__ ga
   }
 }
 
+// act for intermediate index r of the expert block at blk, from the gate and
+// up dot products gs and us and the gate weight wk:
+//   wk * silu(gs) * us                                   (unscaled types)
+//   wk * silu(gs * s_gate[r]) * (us * s_up[r]) * s_down[r]  (fp8: the per-row
+//     gate/up scales, and the down scale of column r folded into act)
+template <typename WT>
+__device__ __forceinline__ float act_value(const WT* blk, const Geom& g, int r, float wk,
+                                           float gs, float us) {
+  if constexpr (std::is_same<WT, fp8w>::value) {
+    const float* sc = wscales(blk, g.off_scale);
+    return (wk * (silu(gs * sc[r]) * (us * sc[g.I + r]))) * sc[2 * g.I + r];
+  } else {
+    return wk * (silu(gs) * us);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Gate/up: grid (ceil(nw / 4), B).  Wave w of token b owns items
 // share(k * ceil(I / RPW), w, nw); item it covers rows [r0, r0 + RPW) of
@@ -240,8 +256,8 @@ __global__ __launch_bounds__(kBlock) void k_gateup(const WT* __restrict__ wbuf,
         for (int j = 0; j < RPW; ++j)
 #pragma unroll
           for (int i = 0; i < VEC; ++i) {
-            ag[j] = fmaf(velem(wg[u][j], i), xv[u][i], ag[j]);
-            au[j] = fmaf(velem(wu[u][j], i), xv[u][i], au[j]);
+            ag[j] = fmaf(wdec<WT>(wg[u][j], i), xv[u][i], ag[j]);
+            au[j] = fmaf(wdec<WT>(wu[u][j], i), xv[u][i], au[j]);
           }
     }
 
@@ -251,7 +267,8 @@ __global__ __launch_bounds__(kBlock) void k_gateup(const WT* __restrict__ wbuf,
     for (int j = 0; j < RPW; ++j) {
       const float gs = wave_sum(ag[j]);
       const float us = wave_sum(au[j]);
-      if (lane == 0 && j < nrows) a[j] = wk * (silu(gs) * us);
+      if (lane == 0 && j < nrows) a[j] = act_value<WT>(wbuf + (int64_t)e * g.stride, g, r0 + j,
+                                                       wk, gs, us);
     }
   }
 }
@@ -311,7 +328,7 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 #pragma unroll
           for (int j = 0; j < RPD; ++j)
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) acc[j] = fmaf(velem(wv[u][j], i), av[u][i], acc[j]);
+            for (int i = 0; i < VEC; ++i) acc[j] = fmaf(wdec<WT>(wv[u][j], i), av[u][i], acc[j]);
       }
     }
 
@@ -426,17 +443,19 @@ __device__ __forceinline__ void gateup_item(const WT* __restrict__ wbuf, const X
       for (int j = 0; j < RPW; ++j)
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          ag[j] = fmaf(velem(wg[u][j], i), xv[u][i], ag[j]);
-          au[j] = fmaf(velem(wu[u][j], i), xv[u][i], au[j]);
+          ag[j] = fmaf(wdec<WT>(wg[u][j], i), xv[u][i], ag[j]);
+          au[j] = fmaf(wdec<WT>(wu[u][j], i), xv[u][i], au[j]);
         }
   }
   const float wk = topk_w(t, kk);
+  const WT* blk = wbuf + (int64_t)topk_id(t, kk) * g.stride;
 #pragma unroll
   for (int j = 0; j < RPW; ++j) {
     const float gs = wave_sum(ag[j]);
     const float us = wave_sum(au[j]);
     if (lane == 0 && j < nrows)
-      __hip_atomic_store(a + j, wk * (silu(gs) * us), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a + j, act_value<WT>(blk, g, r0 + j, wk, gs, us), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -466,7 +485,7 @@ __device__ __forceinline__ void down_tile_load(typename WVec<WT, VEC>::type (&wv
 
 // acc[j] += tile row j . act over the tile's chunks (act of expert kk at
 // act + kk * act_row).
-template <typename V, int VEC, int RPD, int U>
+template <typename WT, typename V, int VEC, int RPD, int U>
 __device__ __forceinline__ void down_tile_fma(float (&acc)[RPD], const V (&wv)[U][RPD],
                                               const float* act, const Geom& g,
                                               int64_t act_row, int q0, int nch, int lane) {
@@ -489,7 +508,7 @@ __device__ __forceinline__ void down_tile_fma(float (&acc)[RPD], const V (&wv)[U
 #pragma unroll
     for (int j = 0; j < RPD; ++j)
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) acc[j] = fmaf(velem(wv[u][j], i), av[u][i], acc[j]);
+      for (int i = 0; i < VEC; ++i) acc[j] = fmaf(wdec<WT>(wv[u][j], i), av[u][i], acc[j]);
 }
 
 template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2>
@@ -585,11 +604,11 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   float acc[RPD];
 #pragma unroll
   for (int j = 0; j < RPD; ++j) acc[j] = 0.0f;
-  down_tile_fma<V, VEC, RPD, U2>(acc, pre, act, g, act_row, wave, nch, lane);
+  down_tile_fma<WT, V, VEC, RPD, U2>(acc, pre, act, g, act_row, wave, nch, lane);
   for (int q0 = wave + kWavesPerBlock * U2; q0 < C; q0 += kWavesPerBlock * U2) {
     V wv[U2][RPD];
     down_tile_load<WT, VEC, RPD, U2>(wv, wbuf, g, t, r0, nrows, q0, nch, lane);
-    down_tile_fma<V, VEC, RPD, U2>(acc, wv, act, g, act_row, q0, nch, lane);
+    down_tile_fma<WT, V, VEC, RPD, U2>(acc, wv, act, g, act_row, q0, nch, lane);
   }
 #pragma unroll
   for (int j = 0; j < RPD; ++j) {
@@ -606,8 +625,12 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
 // ---------------------------------------------------------------------------
 namespace {
 
+int64_t weight_es(int wdt) {
+  return wdt == WR_F32 ? 4 : (wdt == WR_FP8_E4M3 ? 1 : 2);
+}
+
 Geom make_geom(const Problem& p) {
-  const int64_t es = p.wdt == WR_F16 ? 2 : 4;
+  const int64_t es = weight_es(p.wdt);
   Geom g;
   g.E = p.E;
   g.h = p.h;
@@ -618,6 +641,7 @@ Geom make_geom(const Problem& p) {
   g.stride = p.stride_b / es;
   g.off_up = p.off_up_b / es;
   g.off_down = p.off_down_b / es;
+  g.off_scale = p.off_scale_b;
   return g;
 }
 
@@ -668,10 +692,11 @@ hipError_t logits_t(const Problem& p, float* logits, unsigned* zero, int nzero, 
 // Rows per gate/up wave of the single-token kernel: 4 (two column chunks in
 // flight) when a weight row is at most 4 KB, else 2 (four chunks in flight);
 // either way a wave reads about 32 KB per iteration, and short-row layers get
-// half as many blocks.
+// half as many blocks.  fp8 rows always take 4: four chunks of 16 fp32 x
+// values per lane would cost 64 VGPRs and a wave per SIMD.
 int fused_rpw(const Problem& p) {
-  const int64_t row_bytes = (int64_t)p.h * (p.wdt == WR_F16 ? 2 : 4);
-  return (p.vec > 1 && row_bytes <= 4096) ? 4 : 2;
+  const int64_t row_bytes = (int64_t)p.h * weight_es(p.wdt);
+  return (p.vec > 1 && (row_bytes <= 4096 || p.wdt == WR_FP8_E4M3)) ? 4 : 2;
 }
 
 // act chunks of the single-token fused kernel, and its gate/up blocks (the
@@ -695,8 +720,13 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   hs.n1 = fused_n1(p.I, p.k, RPW);
   hs.chunks = fused_chunks(p.I, p.k, RPW);
   hs.spin_limit = 1u << 20;
-  const int n2 = (p.h + WR_FU_RPD - 1) / WR_FU_RPD;
-  hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, WR_FU_RPD, WR_FU_U>),
+  // fp8 down blocks take twice the rows and half the chunks in flight: the
+  // same weight bytes per tile as fp16, and half the act reads per weight byte.
+  constexpr bool kFp8 = std::is_same<WT, fp8w>::value;
+  constexpr int RPD = kFp8 ? 2 * WR_FU_RPD : WR_FU_RPD;
+  constexpr int U2 = kFp8 ? WR_FU_U / 2 : WR_FU_U;
+  const int n2 = (p.h + RPD - 1) / RPD;
+  hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2>),
                      dim3(hs.n1 + n2), dim3(kBlock), 0, s, static_cast<const WT*>(p.wbuf),
                      static_cast<const XT*>(p.x), w.logits, w.act, static_cast<XT*>(p.out),
                      p.topk_ids, p.topk_w, g, hs);
@@ -712,12 +742,14 @@ hipError_t fused_t(const Problem& p, const FusedWs& w, hipStream_t s) {
 template <typename WT, typename XT, int VEC>
 hipError_t ffn_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   constexpr int RPW = WR_GU_RPW, RPD = WR_DN_RPD;
+  // fp8: half the chunks in flight (16 fp32 x values per chunk and lane).
+  constexpr int U1 = std::is_same<WT, fp8w>::value ? WR_GU_U / 2 : WR_GU_U;
   if (p.B == 1) return fused_t<WT, XT, VEC>(p, w, s);
   const Geom g = make_geom(p);
   const WT* wb = static_cast<const WT*>(p.wbuf);
   const int nw1 = waves_for(p.k * ((p.I + RPW - 1) / RPW), p.B);
   const dim3 g1((nw1 + kWavesPerBlock - 1) / kWavesPerBlock, p.B);
-  hipLaunchKernelGGL((k_gateup<WT, XT, VEC, RPW, WR_GU_U>), g1, dim3(kBlock), 0, s, wb,
+  hipLaunchKernelGGL((k_gateup<WT, XT, VEC, RPW, U1>), g1, dim3(kBlock), 0, s, wb,
                      static_cast<const XT*>(p.x), w.logits, w.act, p.topk_ids, p.topk_w, g, nw1);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
@@ -728,11 +760,20 @@ hipError_t ffn_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <typename WT, typename XT>
+hipError_t ffn_w(const Problem& p, const FusedWs& w, hipStream_t s) {
+  constexpr int V = wvec_width<WT>();
+  return p.vec == V ? ffn_t<WT, XT, V>(p, w, s) : ffn_t<WT, XT, 1>(p, w, s);
+}
+
 template <typename XT>
 hipError_t ffn_x(const Problem& p, const FusedWs& w, hipStream_t s) {
-  if (p.wdt == WR_F16)
-    return p.vec == 8 ? ffn_t<f16, XT, 8>(p, w, s) : ffn_t<f16, XT, 1>(p, w, s);
-  return p.vec == 4 ? ffn_t<float, XT, 4>(p, w, s) : ffn_t<float, XT, 1>(p, w, s);
+  switch (p.wdt) {
+    case WR_F16: return ffn_w<f16, XT>(p, w, s);
+    case WR_BF16: return ffn_w<bf16w, XT>(p, w, s);
+    case WR_FP8_E4M3: return ffn_w<fp8w, XT>(p, w, s);
+    default: return ffn_w<float, XT>(p, w, s);
+  }
 }
 
 hipError_t run_ffn(const Problem& p, hipStream_t s) {

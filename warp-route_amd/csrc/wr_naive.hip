@@ -23,12 +23,14 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kWpb = kBlock / kWave;
 
-// y[r] = W[r, :] . v for r < rows; one wave per row (src/naive_moe.cu:79-111
-// computes the same product on one 256-thread block).
+// y[r] = W[r, :] . v (times scale[r] when scale != nullptr: fp8 row scales)
+// for r < rows; one wave per row (src/naive_moe.cu:79-111 computes the same
+// product on one 256-thread block).
 template <typename WT, typename VT, int VEC>
 __global__ __launch_bounds__(kBlock) void k_matvec(const WT* __restrict__ W,
                                                    const VT* __restrict__ v,
-                                                   float* __restrict__ y, int rows, int cols) {
+                                                   float* __restrict__ y, int rows, int cols,
+                                                   const float* __restrict__ scale) {
   typedef typename WVec<WT, VEC>::type V;
   const int lane = threadIdx.x & (kWave - 1);
   const int r = blockIdx.x * kWpb + threadIdx.x / kWave;
@@ -40,17 +42,21 @@ __global__ __launch_bounds__(kBlock) void k_matvec(const WT* __restrict__ W,
     float xv[VEC];
     load_x<VT, VEC>(v + c, xv);
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) acc = fmaf(velem(wv, i), xv[i], acc);
+    for (int i = 0; i < VEC; ++i) acc = fmaf(wdec<WT>(wv, i), xv[i], acc);
   }
   acc = wave_sum(acc);
-  if (lane == 0) y[r] = acc;
+  if (lane == 0) y[r] = scale != nullptr ? acc * scale[r] : acc;
 }
 
-// act = silu(gate) * up (src/naive_moe.cu:117-128).
+// act = silu(gate) * up (src/naive_moe.cu:117-128), times the fp8 down-column
+// scale when col_scale != nullptr.
 __global__ void k_swiglu(const float* __restrict__ gate, const float* __restrict__ up,
-                         float* __restrict__ act, int n) {
+                         float* __restrict__ act, int n, const float* __restrict__ col_scale) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) act[i] = silu(gate[i]) * up[i];
+  if (i < n) {
+    const float a = silu(gate[i]) * up[i];
+    act[i] = col_scale != nullptr ? a * col_scale[i] : a;
+  }
 }
 
 // accum = (first ? 0 : accum) + w * expert_out; the last expert also writes
@@ -117,7 +123,6 @@ void host_softmax_topk(const float* logits, int E, int k, int renorm, HostTopK& 
 
 template <typename WT, typename XT, int VEC>
 hipError_t naive_t(const Problem& p, const NaiveWs& w, const HostTopK& t, hipStream_t s) {
-  const int64_t es = sizeof(WT);
   const char* base = static_cast<const char*>(p.wbuf);
   const XT* x = static_cast<const XT*>(p.x);
   XT* out = static_cast<XT*>(p.out);
@@ -127,15 +132,17 @@ hipError_t naive_t(const Problem& p, const NaiveWs& w, const HostTopK& t, hipStr
     const WT* G = reinterpret_cast<const WT*>(eb);
     const WT* U = reinterpret_cast<const WT*>(eb + p.off_up_b);
     const WT* D = reinterpret_cast<const WT*>(eb + p.off_down_b);
-    (void)es;
+    // fp8: s_gate, s_up, s_down, I floats each (per gate row, up row, down column)
+    const float* sc =
+        p.off_scale_b >= 0 ? reinterpret_cast<const float*>(eb + p.off_scale_b) : nullptr;
     hipLaunchKernelGGL((k_matvec<WT, XT, VEC>), gI, dim3(kBlock), 0, s, G, x, w.gate_vec, p.I,
-                       p.h);
+                       p.h, sc);
     hipLaunchKernelGGL((k_matvec<WT, XT, VEC>), gI, dim3(kBlock), 0, s, U, x, w.up_vec, p.I,
-                       p.h);
+                       p.h, sc != nullptr ? sc + p.I : nullptr);
     hipLaunchKernelGGL(k_swiglu, dim3((p.I + 255) / 256), dim3(256), 0, s, w.gate_vec, w.up_vec,
-                       w.act_vec, p.I);
+                       w.act_vec, p.I, sc != nullptr ? sc + 2 * p.I : nullptr);
     hipLaunchKernelGGL((k_matvec<WT, float, VEC>), gH, dim3(kBlock), 0, s, D, w.act_vec,
-                       w.expert_out, p.h, p.I);
+                       w.expert_out, p.h, p.I, static_cast<const float*>(nullptr));
     hipLaunchKernelGGL((k_weighted_accum<XT>), dim3((p.h + 255) / 256), dim3(256), 0, s, w.accum,
                        w.expert_out, t.w[kk], p.h, kk == 0 ? 1 : 0,
                        kk == p.k - 1 ? out : static_cast<XT*>(nullptr));
@@ -145,11 +152,20 @@ hipError_t naive_t(const Problem& p, const NaiveWs& w, const HostTopK& t, hipStr
   return hipSuccess;
 }
 
+template <typename WT, typename XT>
+hipError_t naive_w(const Problem& p, const NaiveWs& w, const HostTopK& t, hipStream_t s) {
+  constexpr int V = wvec_width<WT>();
+  return p.vec == V ? naive_t<WT, XT, V>(p, w, t, s) : naive_t<WT, XT, 1>(p, w, t, s);
+}
+
 template <typename XT>
 hipError_t naive_x(const Problem& p, const NaiveWs& w, const HostTopK& t, hipStream_t s) {
-  if (p.wdt == WR_F16)
-    return p.vec == 8 ? naive_t<f16, XT, 8>(p, w, t, s) : naive_t<f16, XT, 1>(p, w, t, s);
-  return p.vec == 4 ? naive_t<float, XT, 4>(p, w, t, s) : naive_t<float, XT, 1>(p, w, t, s);
+  switch (p.wdt) {
+    case WR_F16: return naive_w<f16, XT>(p, w, t, s);
+    case WR_BF16: return naive_w<bf16w, XT>(p, w, t, s);
+    case WR_FP8_E4M3: return naive_w<fp8w, XT>(p, w, t, s);
+    default: return naive_w<float, XT>(p, w, t, s);
+  }
 }
 
 }  // namespace

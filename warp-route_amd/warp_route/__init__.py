@@ -15,11 +15,12 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from .functional import (MAX_EXPERTS, MAX_TOPK, _pack_expert_weights, batched_fused_moe,
-                         expert_layout, fused_moe, gate_topk, naive_moe)
+from .functional import (MAX_EXPERTS, MAX_TOPK, WEIGHT_DTYPES, _pack_expert_weights,
+                         batched_fused_moe, expert_layout, fused_moe, gate_topk, naive_moe,
+                         quantize_fp8, weight_layout)
 
 __all__ = ["MoELayer", "fused_moe", "naive_moe", "batched_fused_moe", "gate_topk",
-           "expert_layout", "_pack_expert_weights"]
+           "expert_layout", "weight_layout", "quantize_fp8", "_pack_expert_weights"]
 
 
 class MoELayer(nn.Module):
@@ -33,7 +34,8 @@ class MoELayer(nn.Module):
         top_k: experts per token, 1 <= top_k <= min(6, num_experts).
         renormalize: divide the selected weights by their sum.
         weight_dtype: dtype of the packed expert buffer the kernels read
-            (torch.float32 as in the reference, or torch.float16).
+            (torch.float32 as in the reference, torch.float16, torch.bfloat16,
+            or torch.float8_e4m3fn with per-channel fp32 scales).
     """
 
     def __init__(self, num_experts: int, hidden_dim: int, intermediate_dim: int,
@@ -45,6 +47,8 @@ class MoELayer(nn.Module):
         if not 1 <= top_k <= min(MAX_TOPK, num_experts):
             raise ValueError(
                 f"top_k must be in [1, min({MAX_TOPK}, num_experts)], got {top_k}")
+        if weight_dtype not in WEIGHT_DTYPES:
+            raise ValueError(f"weight_dtype must be one of {WEIGHT_DTYPES}, got {weight_dtype}")
         self.num_experts = num_experts
         self.hidden_dim = hidden_dim
         self.intermediate_dim = intermediate_dim

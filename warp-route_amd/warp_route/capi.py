@@ -31,6 +31,8 @@ WR_EHIP = 100
 
 WR_F32 = 0
 WR_F16 = 1
+WR_BF16 = 2
+WR_FP8_E4M3 = 3
 
 WR_KIND_FUSED = 0
 WR_KIND_BATCHED = 1
@@ -40,6 +42,13 @@ WR_KIND_NAIVE = 2
 class WrOffsets(ctypes.Structure):
     _fields_ = [("gate_proj_offset", ctypes.c_int64), ("up_proj_offset", ctypes.c_int64),
                 ("down_proj_offset", ctypes.c_int64), ("expert_stride", ctypes.c_int64)]
+
+
+class WrLayoutInfo(ctypes.Structure):
+    _fields_ = [("gate_proj_offset", ctypes.c_int64), ("up_proj_offset", ctypes.c_int64),
+                ("down_proj_offset", ctypes.c_int64), ("scale_offset", ctypes.c_int64),
+                ("expert_stride", ctypes.c_int64), ("elem_bytes", ctypes.c_int32),
+                ("weight_dtype", ctypes.c_int32)]
 
 
 class WrMoeArgs(ctypes.Structure):
@@ -78,6 +87,10 @@ def lib() -> ctypes.CDLL:
         l.wr_layout.restype = ctypes.c_int
         l.wr_total_weight_bytes.argtypes = [ctypes.c_int] * 4
         l.wr_total_weight_bytes.restype = ctypes.c_int64
+        l.wr_layout_dtype.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(WrLayoutInfo)]
+        l.wr_layout_dtype.restype = ctypes.c_int
+        l.wr_weight_bytes.argtypes = [ctypes.c_int] * 4
+        l.wr_weight_bytes.restype = ctypes.c_int64
         l.wr_workspace_bytes.argtypes = [ctypes.c_int] * 6
         l.wr_workspace_bytes.restype = ctypes.c_size_t
         for name in ("wr_gate_topk", "wr_fused_moe", "wr_batched_fused_moe", "wr_naive_moe"):
@@ -98,6 +111,14 @@ def layout(E: int, h: int, I: int, elem_bytes: int) -> dict:
     if st != WR_OK:
         raise ValueError(status_str(st))
     return {f: getattr(o, f) for f, _ in WrOffsets._fields_}
+
+
+def layout_dtype(E: int, h: int, I: int, weight_dtype: int) -> dict:
+    o = WrLayoutInfo()
+    st = lib().wr_layout_dtype(E, h, I, weight_dtype, ctypes.byref(o))
+    if st != WR_OK:
+        raise ValueError(status_str(st))
+    return {f: getattr(o, f) for f, _ in WrLayoutInfo._fields_}
 
 
 def call(name: str, args: WrMoeArgs, stream: int = 0) -> int:

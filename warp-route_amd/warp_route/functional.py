@@ -13,7 +13,8 @@ trailing keyword arguments add:
   topk_weights  optional preallocated float32 tensor of the same shape that
                 receives their gate weights
 
-``weight_buf`` may be float32 (the reference layout) or float16; ``x`` may be
+``weight_buf`` may be float32 (the reference layout), float16, bfloat16 or
+float8_e4m3fn (codes plus fp32 scales, see ``weight_layout``); ``x`` may be
 float32 or float16 and the output has x's dtype.  Work runs on the current
 HIP stream without a device synchronisation.  There is no CPU fallback: the
 ops raise if the HIP extension is missing.
@@ -28,6 +29,8 @@ import torch
 MAX_EXPERTS = 64  # src/gate.cuh:5
 MAX_TOPK = 6      # src/gate.cuh:7
 EXPERT_ALIGN = 128
+FP8_MAX = 448.0   # largest finite OCP E4M3 value
+WEIGHT_DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.float8_e4m3fn)
 
 
 @functools.lru_cache(maxsize=1)
@@ -57,6 +60,42 @@ def expert_layout(num_experts: int, hidden_dim: int, intermediate_dim: int,
             "expert_stride": stride}
 
 
+def weight_layout(num_experts: int, hidden_dim: int, intermediate_dim: int,
+                  dtype: torch.dtype) -> dict:
+    """Byte layout of one expert block for a weight dtype (wr_layout_dtype).
+
+    float32 / float16 / bfloat16: ``expert_layout`` with the element size, no
+    scales.  float8_e4m3fn: 1-byte codes at the same element offsets, then at
+    ``scale_offset`` (3 I h rounded up to 16 bytes) three fp32 arrays of I
+    values: gate row scales, up row scales and down column scales, so that
+    gate[r][c] = q * s_gate[r], up[r][c] = q * s_up[r] and
+    down[r][c] = q * s_down[c]; the stride covers them, rounded up to 128."""
+    if dtype not in WEIGHT_DTYPES:
+        raise ValueError(f"weight dtype must be one of {WEIGHT_DTYPES}, got {dtype}")
+    es = torch.empty((), dtype=dtype).element_size()
+    if dtype != torch.float8_e4m3fn:
+        out = expert_layout(num_experts, hidden_dim, intermediate_dim, es)
+        out.update(scale_offset=-1, elem_bytes=es)
+        return out
+    n = intermediate_dim * hidden_dim
+    sc = (3 * n + 15) // 16 * 16
+    stride = (sc + 12 * intermediate_dim + EXPERT_ALIGN - 1) // EXPERT_ALIGN * EXPERT_ALIGN
+    return {"gate_proj_offset": 0, "up_proj_offset": n, "down_proj_offset": 2 * n,
+            "scale_offset": sc, "expert_stride": stride, "elem_bytes": 1}
+
+
+def quantize_fp8(w: torch.Tensor, dim: int):
+    """(codes, scales) of ``w`` in OCP E4M3 with one fp32 scale per slice
+    along ``dim`` (dim=1: per row, dim=0: per column):
+    scale = max|w| / 448 over the slice (1 for an all-zero slice), codes =
+    round-to-nearest-even of w / scale, within +-448 by construction."""
+    wf = w.to(torch.float32)
+    amax = wf.abs().amax(dim=dim, keepdim=True)
+    scale = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
+    q = (wf / scale).clamp_(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return q, scale.reshape(-1)
+
+
 def _pack_expert_weights(
     gate_proj: List[torch.Tensor],
     up_proj: List[torch.Tensor],
@@ -71,21 +110,36 @@ def _pack_expert_weights(
 
     Per expert, row-major: [gate_proj I x h][up_proj I x h][down_proj h x I],
     each expert block zero-padded to a 128-byte boundary.  ``dtype`` selects
-    float32 (the reference's only layout, the default) or float16.  The buffer
-    is created on the device of ``gate_proj[0]``.
+    float32 (the reference's only layout, the default), float16, bfloat16, or
+    float8_e4m3fn, which quantizes with ``quantize_fp8`` (gate and up per row,
+    down per column) and stores the scales after the codes
+    (``weight_layout``).  The buffer is created on the device of
+    ``gate_proj[0]``.
     """
-    if dtype not in (torch.float32, torch.float16):
-        raise ValueError(f"dtype must be torch.float32 or torch.float16, got {dtype}")
-    es = torch.empty((), dtype=dtype).element_size()
-    off = expert_layout(num_experts, hidden_dim, intermediate_dim, es)
+    off = weight_layout(num_experts, hidden_dim, intermediate_dim, dtype)
+    es = off["elem_bytes"]
     stride_el = off["expert_stride"] // es
     n = intermediate_dim * hidden_dim
     buf = torch.zeros(num_experts * stride_el, dtype=dtype, device=gate_proj[0].device)
+    if dtype != torch.float8_e4m3fn:
+        for e in range(num_experts):
+            base = e * stride_el
+            buf[base:base + n] = gate_proj[e].reshape(-1)
+            buf[base + n:base + 2 * n] = up_proj[e].reshape(-1)
+            buf[base + 2 * n:base + 3 * n] = down_proj[e].reshape(-1)
+        return buf
+    raw = buf.view(torch.uint8)
+    I = intermediate_dim
     for e in range(num_experts):
         base = e * stride_el
-        buf[base:base + n] = gate_proj[e].reshape(-1)
-        buf[base + n:base + 2 * n] = up_proj[e].reshape(-1)
-        buf[base + 2 * n:base + 3 * n] = down_proj[e].reshape(-1)
+        qg, sg = quantize_fp8(gate_proj[e], 1)
+        qu, su = quantize_fp8(up_proj[e], 1)
+        qd, sd = quantize_fp8(down_proj[e], 0)
+        buf[base:base + n] = qg.reshape(-1)
+        buf[base + n:base + 2 * n] = qu.reshape(-1)
+        buf[base + 2 * n:base + 3 * n] = qd.reshape(-1)
+        sc = base + off["scale_offset"]
+        raw[sc:sc + 12 * I].view(torch.float32).copy_(torch.cat([sg, su, sd]))
     return buf
 
 

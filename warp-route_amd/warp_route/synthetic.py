@@ -5,17 +5,20 @@ Draw order, all in fp32 from one generator seeded with ``seed``:
 x [B, h] ~ N(0, 1); router [E, h] ~ N(0, router_std); then for each expert e:
 gate [I, h], up [I, h], down [h, I] ~ N(0, expert_std).  The expert matrices
 are cast to ``weight_dtype`` straight into the packed expert layout
-(src/expert_layout.cuh:5-18), so a full layer never exists in fp32.
+(src/expert_layout.cuh:5-18), so a full layer never exists in fp32; for
+float8_e4m3fn each matrix is quantized with ``quantize_fp8`` (same draws, so
+an fp8 layer is the quantized fp16 layer of the same seed).
 """
 from __future__ import annotations
 
+import dataclasses
 import math
 from dataclasses import dataclass
 from typing import Optional
 
 import torch
 
-from .functional import expert_layout
+from .functional import quantize_fp8, weight_layout
 
 
 @dataclass(frozen=True)
@@ -33,9 +36,21 @@ class MoEConfig:
     @property
     def selected_bytes(self) -> int:
         """Weight bytes of k distinct experts: the algorithmic traffic of one
-        batch-1 call (3 * h * I * elem_bytes per expert)."""
-        es = torch.empty((), dtype=self.weight_dtype).element_size()
-        return self.top_k * 3 * self.hidden_dim * self.intermediate_dim * es
+        batch-1 call (3 * h * I * elem_bytes per expert, plus 12 I bytes of
+        scales for fp8)."""
+        return self.top_k * expert_weight_bytes(self.hidden_dim, self.intermediate_dim,
+                                                self.weight_dtype)
+
+    def with_weights(self, dtype: torch.dtype) -> "MoEConfig":
+        return dataclasses.replace(self, weight_dtype=dtype)
+
+
+def expert_weight_bytes(hidden_dim: int, intermediate_dim: int, dtype: torch.dtype) -> int:
+    """Bytes a kernel must read for one selected expert: its three matrices,
+    and for fp8 its three scale arrays."""
+    es = torch.empty((), dtype=dtype).element_size()
+    n = 3 * hidden_dim * intermediate_dim * es
+    return n + (12 * intermediate_dim if dtype == torch.float8_e4m3fn else 0)
 
 
 CONFIGS = {
@@ -65,18 +80,29 @@ def make_layer(num_experts: int, hidden_dim: int, intermediate_dim: int,
     x = torch.randn(shape_x, generator=gen, device=gen_device, dtype=torch.float32)
     gate_w = torch.randn(num_experts, hidden_dim, generator=gen, device=gen_device,
                          dtype=torch.float32) * router_std
-    es = torch.empty((), dtype=weight_dtype).element_size()
-    off = expert_layout(num_experts, hidden_dim, intermediate_dim, es)
+    off = weight_layout(num_experts, hidden_dim, intermediate_dim, weight_dtype)
+    es = off["elem_bytes"]
     stride_el = off["expert_stride"] // es
     n = intermediate_dim * hidden_dim
+    fp8 = weight_dtype == torch.float8_e4m3fn
     buf = torch.zeros(num_experts * stride_el, dtype=weight_dtype, device=device)
+    raw = buf.view(torch.uint8)
+    I = intermediate_dim
     for e in range(num_experts):
         base = e * stride_el
         for j in range(3):
             shape = (intermediate_dim, hidden_dim) if j < 2 else (hidden_dim, intermediate_dim)
             w = torch.randn(shape, generator=gen, device=gen_device, dtype=torch.float32)
             w.mul_(expert_std)
-            buf[base + j * n:base + (j + 1) * n].copy_(w.reshape(-1).to(weight_dtype))
+            if fp8:
+                # gate and up: a scale per row; down: a scale per column
+                q, sc = quantize_fp8(w, 1 if j < 2 else 0)
+                buf[base + j * n:base + (j + 1) * n].copy_(q.reshape(-1))
+                s0 = base + off["scale_offset"] + j * 4 * I
+                raw[s0:s0 + 4 * I].view(torch.float32).copy_(sc)
+                del q, sc
+            else:
+                buf[base + j * n:base + (j + 1) * n].copy_(w.reshape(-1).to(weight_dtype))
             del w
     return (x.to(device=device, dtype=x_dtype), gate_w.to(device), buf)
 
