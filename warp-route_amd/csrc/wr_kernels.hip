@@ -52,6 +52,19 @@
 #ifndef WR_WAVES_PER_CU
 #define WR_WAVES_PER_CU 8  // persistent waves per CU (upper bound)
 #endif
+// fp8 weights in the single-token fused kernel (16 weights per 128-bit load)
+#ifndef WR_F8_RPW
+#define WR_F8_RPW 4  // gate/up rows per wave (2 or 4)
+#endif
+#ifndef WR_F8_U1
+#define WR_F8_U1 2   // gate/up column chunks per row per iteration
+#endif
+#ifndef WR_F8_RPD
+#define WR_F8_RPD 8  // output rows per down block
+#endif
+#ifndef WR_F8_U2
+#define WR_F8_U2 2   // column chunks per down tile
+#endif
 
 namespace wr {
 
@@ -696,7 +709,8 @@ hipError_t logits_t(const Problem& p, float* logits, unsigned* zero, int nzero, 
 // values per lane would cost 64 VGPRs and a wave per SIMD.
 int fused_rpw(const Problem& p) {
   const int64_t row_bytes = (int64_t)p.h * weight_es(p.wdt);
-  return (p.vec > 1 && (row_bytes <= 4096 || p.wdt == WR_FP8_E4M3)) ? 4 : 2;
+  if (p.wdt == WR_FP8_E4M3) return p.vec > 1 ? WR_F8_RPW : 2;
+  return (p.vec > 1 && row_bytes <= 4096) ? 4 : 2;
 }
 
 // act chunks of the single-token fused kernel, and its gate/up blocks (the
@@ -723,8 +737,8 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   // fp8 down blocks take twice the rows and half the chunks in flight: the
   // same weight bytes per tile as fp16, and half the act reads per weight byte.
   constexpr bool kFp8 = std::is_same<WT, fp8w>::value;
-  constexpr int RPD = kFp8 ? 2 * WR_FU_RPD : WR_FU_RPD;
-  constexpr int U2 = kFp8 ? WR_FU_U / 2 : WR_FU_U;
+  constexpr int RPD = kFp8 ? WR_F8_RPD : WR_FU_RPD;
+  constexpr int U2 = kFp8 ? WR_F8_U2 : WR_FU_U;
   const int n2 = (p.h + RPD - 1) / RPD;
   hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2>),
                      dim3(hs.n1 + n2), dim3(kBlock), 0, s, static_cast<const WT*>(p.wbuf),
@@ -735,8 +749,9 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
 
 template <typename WT, typename XT, int VEC>
 hipError_t fused_t(const Problem& p, const FusedWs& w, hipStream_t s) {
-  if (fused_rpw(p) == 4) return fused_rpw_t<WT, XT, VEC, 4, WR_GU_U / 2>(p, w, s);
-  return fused_rpw_t<WT, XT, VEC, 2, WR_GU_U>(p, w, s);
+  constexpr bool kFp8 = std::is_same<WT, fp8w>::value;
+  if (fused_rpw(p) == 4) return fused_rpw_t<WT, XT, VEC, 4, kFp8 ? WR_F8_U1 : WR_GU_U / 2>(p, w, s);
+  return fused_rpw_t<WT, XT, VEC, 2, kFp8 ? WR_F8_U1 : WR_GU_U>(p, w, s);
 }
 
 template <typename WT, typename XT, int VEC>
