@@ -42,6 +42,15 @@ METRIC = ("µs per MoE layer at batch=1 (Mixtral shape); "
           "achieved HBM GB/s as % of peak")
 
 
+WLABEL = {"fp16": "f16", "bf16": "bf16", "fp8": "fp8 e4m3 (per-channel fp32 scales)"}
+
+
+def weight_dtype(name: str):
+    """torch dtype of a --weights choice."""
+    import torch
+    return {"fp16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn}[name]
+
+
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
@@ -125,8 +134,8 @@ def batched_bench(args) -> int:
     per call, averaged over the rotated layers."""
     import torch
     from warp_route import functional as F
-    from warp_route.synthetic import CONFIGS, clustered_batch, make_config_layer
-    cfg = CONFIGS["mixtral"]
+    from warp_route.synthetic import CONFIGS, clustered_batch, expert_weight_bytes, make_config_layer
+    cfg = CONFIGS["mixtral"].with_weights(weight_dtype(args.weights))
     E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
     dev = torch.device("cuda:0")
     layers = [make_config_layer(cfg, seed=s, device=dev, gen_device=dev)
@@ -143,20 +152,20 @@ def batched_bench(args) -> int:
         us = _timed(lambda i: F.batched_fused_moe(xs[i % L], layers[i % L][1], layers[i % L][2],
                                                   E, h, I, k, cfg.renormalize),
                     args.steps, args.warmup)
-        nbytes = sum(distinct) / L * 3 * h * I * 2
+        nbytes = sum(distinct) / L * expert_weight_bytes(h, I, cfg.weight_dtype)
         gbps = nbytes / us / 1e3
         print(json.dumps({
             "metric": "µs per batched MoE layer call (Mixtral shape, clustered routing)",
             "value": round(us, 2), "unit": "us/call", "higher_is_better": False,
             "tokens_per_s": round(B / us * 1e6, 1), "us_per_token": round(us / B, 3),
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-            "dtype": "f16 weights, f32 accumulate",
+            "dtype": f"{WLABEL[args.weights]} weights, f32 accumulate",
             "data": "synthetic (seeded random-init layers; clustered tokens, alpha 4)",
             "config": {"workload": "mixtral MoE layer, batched decode", "batch": B,
                        "distinct_experts_per_layer": distinct, "layers_rotated": L},
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
                          "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                         "bytes": "distinct selected experts' fp16 weights"},
+                         "bytes": f"distinct selected experts' {args.weights} weights"},
         }), flush=True)
     return 0
 
@@ -273,8 +282,7 @@ def main() -> int:
     from warp_route import functional as F
     from warp_route.synthetic import CONFIGS, make_config_layer
 
-    wdt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn}
-    cfg = CONFIGS[args.config].with_weights(wdt[args.weights])
+    cfg = CONFIGS[args.config].with_weights(weight_dtype(args.weights))
     E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
     dev = torch.device("cuda:0")
     log(f"[bench] generating {args.layers} {cfg.name} {args.weights} layers on the GPU")
@@ -337,8 +345,7 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"fp16": "f16", "bf16": "bf16", "fp8": "fp8 e4m3 (per-channel fp32 scales)"}[
-            args.weights] + " weights, f32 accumulate",
+        "dtype": WLABEL[args.weights] + " weights, f32 accumulate",
         "data": "synthetic (seeded random-init layers drawn on the GPU)",
         "config": {"workload": f"{cfg.name} MoE layer, decode batch 1", "hidden": h,
                    "intermediate": I, "experts": E, "top_k": k,

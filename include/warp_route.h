@@ -118,15 +118,14 @@ typedef struct wr_moe_args {
  * the offsets are those of wr_layout with elem_bytes 4, 2, 2 and
  * scale_offset is -1.  For WR_FP8_E4M3 the three matrices hold 1-byte codes
  * q at the same element offsets (gate 0, up I h, down 2 I h), followed at
- * scale_offset = 3 I h rounded up to 16 bytes by three fp32 arrays of I
- * values, s_gate, s_up and s_down, with
- *   gate[r][c] = fp8(q_gate[r][c]) * s_gate[r]    (per gate row)
- *   up[r][c]   = fp8(q_up[r][c])   * s_up[r]      (per up row)
- *   down[r][c] = fp8(q_down[r][c]) * s_down[c]    (per down column)
- * and expert_stride = scale_offset + 12 I rounded up to 128 bytes.  All three
- * scale arrays are indexed by the intermediate index, so a kernel applies
- * s_down to act (silu(gate x) * (up x)) instead of to the down rows.  Has no
- * counterpart in the reference, whose layout is fp32 only. */
+ * scale_offset = 3 I h rounded up to 16 bytes by one fp32 scale per output
+ * row: s_gate[I], s_up[I], then s_down[h], with
+ *   gate[r][c] = fp8(q_gate[r][c]) * s_gate[r]
+ *   up[r][c]   = fp8(q_up[r][c])   * s_up[r]
+ *   down[r][c] = fp8(q_down[r][c]) * s_down[r]
+ * and expert_stride = scale_offset + 4 (2 I + h) rounded up to 128 bytes.
+ * Kernels apply a row's scale to its dot product.  Has no counterpart in the
+ * reference, whose layout is fp32 only. */
 typedef struct wr_layout_info {
   int64_t gate_proj_offset;
   int64_t up_proj_offset;

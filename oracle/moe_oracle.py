@@ -148,8 +148,8 @@ def weight_layout(num_experts: int, hidden_dim: int, intermediate_dim: int,
     """Expert block layout per weight format (wr_layout_dtype).  f32, f16 and
     bf16: layout_offsets with 4, 2, 2 bytes per element and no scales.  fp8:
     1-byte codes at element offsets 0, I h, 2 I h; scales at 3 I h rounded up
-    to 16 bytes (fp32 s_gate[I], s_up[I], s_down[I]); stride rounded up to
-    128 bytes."""
+    to 16 bytes (fp32 s_gate[I], s_up[I], s_down[h], one per output row);
+    stride rounded up to 128 bytes."""
     if fmt not in WEIGHT_FORMATS:
         raise ValueError(f"unknown weight format {fmt!r}")
     if fmt != "fp8":
@@ -159,7 +159,8 @@ def weight_layout(num_experts: int, hidden_dim: int, intermediate_dim: int,
         return out
     n = intermediate_dim * hidden_dim
     sc = (3 * n + 15) // 16 * 16
-    stride = (sc + 12 * intermediate_dim + EXPERT_ALIGN - 1) // EXPERT_ALIGN * EXPERT_ALIGN
+    stride = ((sc + 4 * (2 * intermediate_dim + hidden_dim) + EXPERT_ALIGN - 1)
+              // EXPERT_ALIGN * EXPERT_ALIGN)
     return {"gate_proj_offset": 0, "up_proj_offset": n, "down_proj_offset": 2 * n,
             "scale_offset": sc, "expert_stride": stride, "elem_bytes": 1}
 
@@ -168,8 +169,7 @@ def expert_matrices(raw: np.ndarray, e: int, num_experts: int, hidden_dim: int,
                     intermediate_dim: int, fmt: str):
     """(gate [I,h], up [I,h], down [h,I]) of expert e as float64, decoded from
     the raw bytes (uint8) of a packed buffer in weight format ``fmt``.  fp8
-    matrices are dequantized: gate and up rows times their row scale, down
-    columns times their column scale."""
+    matrices are dequantized: every row times its row scale."""
     raw = np.asarray(raw, dtype=np.uint8)
     lo = weight_layout(num_experts, hidden_dim, intermediate_dim, fmt)
     h, I = hidden_dim, intermediate_dim
@@ -193,11 +193,12 @@ def expert_matrices(raw: np.ndarray, e: int, num_experts: int, hidden_dim: int,
     u = mat(lo["up_proj_offset"], I, h)
     d = mat(lo["down_proj_offset"], h, I)
     if fmt == "fp8":
-        sc = raw[base + lo["scale_offset"]:base + lo["scale_offset"] + 12 * I]
-        s = sc.view(np.float32).astype(np.float64).reshape(3, I)
-        g = g * s[0][:, None]
-        u = u * s[1][:, None]
-        d = d * s[2][None, :]
+        ns = 2 * I + h
+        sc = raw[base + lo["scale_offset"]:base + lo["scale_offset"] + 4 * ns]
+        s = sc.view(np.float32).astype(np.float64)
+        g = g * s[:I][:, None]
+        u = u * s[I:2 * I][:, None]
+        d = d * s[2 * I:][:, None]
     return g, u, d
 
 

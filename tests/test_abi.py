@@ -74,12 +74,12 @@ def test_layout_dtype_agrees_with_python_and_oracle(E, h, I, wdt):
 
 def test_fp8_layout_byte_table():
     """Hand-computed: E=8, h=4096, I=14336 (Mixtral): codes 3 I h =
-    176,160,768 bytes (a multiple of 16), then 12 I = 172,032 bytes of
-    scales; 176,332,800 is a multiple of 128.  h=3, I=5: codes 45 bytes,
-    scales at 48, 60 bytes of them, stride 128."""
+    176,160,768 bytes (a multiple of 16), then 4 (2 I + h) = 131,072 bytes of
+    row scales; 176,291,840 is a multiple of 128.  h=3, I=5: codes 45 bytes,
+    scales at 48, 52 bytes of them, stride 128."""
     assert capi.layout_dtype(8, 4096, 14336, capi.WR_FP8_E4M3) == {
         "gate_proj_offset": 0, "up_proj_offset": 58720256, "down_proj_offset": 117440512,
-        "scale_offset": 176160768, "expert_stride": 176332800, "elem_bytes": 1,
+        "scale_offset": 176160768, "expert_stride": 176291840, "elem_bytes": 1,
         "weight_dtype": capi.WR_FP8_E4M3}
     lo = capi.layout_dtype(2, 3, 5, capi.WR_FP8_E4M3)
     assert (lo["up_proj_offset"], lo["down_proj_offset"], lo["scale_offset"],

@@ -212,23 +212,25 @@ GROUPED = [(8, 256, 512, 2, False), (16, 512, 1024, 2, True), (64, 256, 512, 6, 
            (8, 384, 640, 1, True)]
 
 
+@pytest.mark.parametrize("wd", [F16, FP8], ids=["f16", "fp8"])
 @pytest.mark.parametrize("x_dtype", [F32, F16], ids=["xf32", "xf16"])
 @pytest.mark.parametrize("B", [2, 5, 33, 80])
 @pytest.mark.parametrize("cfg", GROUPED,
                          ids=lambda c: f"E{c[0]}-h{c[1]}-I{c[2]}-k{c[3]}" + ("-renorm" if c[4] else ""))
-def test_grouped_batched_parity(cuda, cfg, B, x_dtype):
-    """The grouped MFMA batched path (fp16 weights, h and I multiples of 128).
+def test_grouped_batched_parity(cuda, cfg, B, x_dtype, wd):
+    """The grouped MFMA batched path (fp16 or fp8 weights, h and I multiples
+    of 128; fp8 codes are staged as fp16 and scaled in the epilogue).
     Tokens cluster on one expert pair, so experts get anywhere from 1 to B
     tokens (B = 80 puts more than 64 on one expert: two token passes).  Every
     row's ids and weights are bit-identical to the single-token op and its
     output equals that op's up to summation order; a subset is checked against
     the oracle; two calls are bit-identical."""
     E, h, I, k, rn = cfg
-    _, gw, buf = make_layer(E, h, I, F16, router_std=h ** -0.5, expert_std=0.05, seed=3,
+    _, gw, buf = make_layer(E, h, I, wd, router_std=h ** -0.5, expert_std=0.05, seed=3,
                             device=cuda)
     pair = (1, 1) if k == 1 else (1, E - 1)  # k = 1: every token on one expert
     x = clustered_batch(gw, B, pair=pair, alpha=4.0, seed=B, device=cuda).to(x_dtype)
-    print(f"[gpu] grouped E{E}-h{h}-I{I}-k{k} B={B} {x_dtype}", flush=True)
+    print(f"[gpu] grouped E{E}-h{h}-I{I}-k{k} B={B} {x_dtype} {WNAME[wd]}", flush=True)
     ids = torch.empty(B, k, dtype=torch.int32, device=cuda)
     ws = torch.empty(B, k, dtype=torch.float32, device=cuda)
     out = F.batched_fused_moe(x, gw, buf, E, h, I, k, rn, ids, ws)

@@ -295,8 +295,7 @@ def _raw_block(layout, codes, scales=None):
 
 def test_fp8_expert_matrices_hand_computed():
     """E=1, h=2, I=2: gate codes 1, -1 / 2, 0.5; up 1.5, 2^-6 / 0, -2; down
-    1, 2 / -1, 0.5.  Scales: gate rows (2, 3), up rows (0.25, 4), down
-    columns (10, 100).  Down is scaled per column: down[r][c] * s_down[c]."""
+    1, 2 / -1, 0.5.  Row scales: gate (2, 3), up (0.25, 4), down (10, 100)."""
     lo = O.weight_layout(1, 2, 2, "fp8")
     assert (lo["up_proj_offset"], lo["down_proj_offset"], lo["scale_offset"],
             lo["expert_stride"]) == (4, 8, 16, 128)
@@ -307,7 +306,7 @@ def test_fp8_expert_matrices_hand_computed():
     g, u, d = O.expert_matrices(raw, 0, 1, 2, 2, "fp8")
     np.testing.assert_array_equal(g, [[2.0, -2.0], [6.0, 1.5]])
     np.testing.assert_array_equal(u, [[0.375, 0.25 * 2.0 ** -6], [0.0, -8.0]])
-    np.testing.assert_array_equal(d, [[10.0, 200.0], [-10.0, 50.0]])
+    np.testing.assert_array_equal(d, [[10.0, 20.0], [-100.0, 50.0]])
 
 
 def test_bf16_expert_matrices_hand_computed():

@@ -63,7 +63,7 @@ wr_layout_info layout_of(int64_t E, int64_t h, int64_t I, int wdt) {
   o.up_proj_offset = I * h;
   o.down_proj_offset = 2 * I * h;
   o.scale_offset = (3 * I * h + 15) / 16 * 16;
-  const int64_t raw = o.scale_offset + 3 * I * 4;
+  const int64_t raw = o.scale_offset + (2 * I + h) * 4;
   o.expert_stride = (raw + WR_EXPERT_ALIGN - 1) / WR_EXPERT_ALIGN * WR_EXPERT_ALIGN;
   return o;
 }

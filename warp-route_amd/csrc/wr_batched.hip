@@ -15,10 +15,11 @@
 //   3. k_gu_mfma: block (row tile, expert slot): 4 waves x 16 gate rows and
 //      the same 16 up rows each, all of the expert's tokens (up to 64 per
 //      pass); the token tile is staged in LDS and shared by the 4 waves.
-//      v_mfma_f32_16x16x32_f16 with A = weight rows (straight from HBM,
-//      exact fp16) and B = the hi and lo terms of x; products are exact and
-//      accumulate in fp32.  Epilogue: act[pair][row] = w * silu(g) * u
-//      (src/fused_moe.cu:192-201).
+//      v_mfma_f32_16x16x32_f16 with A = weight rows (fp16, or fp8 E4M3 codes
+//      converted exactly to fp16 while staging) and B = the hi and lo terms
+//      of x; products are exact and accumulate in fp32.  Epilogue:
+//      act[pair][row] = w * silu(g) * u (src/fused_moe.cu:192-201), with fp8
+//      row scales applied to g and u (and to the down sums in step 4).
 //   4. k_dn_mfma: block (row tile, K slice, expert slot): the same scheme on
 //      the down rows against act (split into hi/lo fp16 while staging), four
 //      K slices so that the grid has enough blocks; partial sums per slice.
@@ -28,9 +29,9 @@
 // is padded to 16 tokens per tile; at 2 MFMAs per product term it stays far
 // below the time the weight stream takes (the path is HBM-bound).
 //
-// Requirements (else the per-token kernels in wr_kernels.hip run): fp16
-// weights with 16-byte aligned rows, h and I multiples of 128, and the fp16
-// range for x and act (|v| < 65504).
+// Requirements (else the per-token kernels in wr_kernels.hip run): fp16 or
+// fp8 weights with 16-byte aligned rows, h and I multiples of 128, and the
+// fp16 range for x and act (|v| < 65504).
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -228,32 +229,77 @@ __device__ __forceinline__ void tile_store(TokTile& xs, const H8 (&hi)[kTilePiec
   }
 }
 
-// Weight tiles.  A wave's rows are loaded 4 rows x 256 bytes per instruction
-// (lane l: row 4 i + l / 16 of the instruction's group, 16 bytes at column
-// 8 (l % 16) of the K step): a streaming probe measured this pattern at 6.2
-// TB/s against 5.5 TB/s for MFMA fragments loaded straight from memory (16
-// rows x 64 bytes per instruction).  The wave stores its rows into its own LDS
-// tile (rows padded to 17 pieces, so the fragment reads below are free of bank
-// conflicts) and reads the MFMA A fragments from there: for MFMA j of the K
-// step, lane l takes row l % 16, columns 32 j + 8 (l / 16) .. + 8.
+// Weight tiles.  A wave's rows are loaded 16 bytes per lane, a K step of a
+// row (128 columns) per group of lanes: fp16 4 rows x 256 bytes per
+// instruction (lane l: row 4 i + l / 16 of group i, columns 8 (l % 16) ..
+// + 8), fp8 8 rows x 128 bytes (lane l: row 8 i + l / 8, columns 16 (l % 8)
+// .. + 16).  A streaming probe measured these patterns at 6.2 and 6.1 TB/s
+// against 5.5 TB/s for MFMA fragments loaded straight from memory (16 rows x
+// 64 bytes per instruction).  The wave stores its rows, as fp16, into its own
+// LDS tile (rows padded to 17 pieces, so the fragment reads below are free of
+// bank conflicts) and reads the MFMA A fragments from there: for MFMA j of
+// the K step, lane l takes row l % 16, columns 32 j + 8 (l / 16) .. + 8.
+// fp8 codes become fp16 with v_cvt_scalef32_pk_f16_fp8 (scale 1: every E4M3
+// value is an fp16 value), two per instruction.
 template <int ROWS>
 struct WTile {
   H8 w[ROWS][kLdsRow];
 };
 
-// Loads of one K step: ROWS / 4 instructions, group i = rows [4 i, 4 i + 4).
-// row_ptr(i) is this lane's address for group i at column 0 of the K step.
-template <int ROWS>
-__device__ __forceinline__ void w_load(H8 (&r)[ROWS / 4], const f16* const (&base)[ROWS / 4],
-                                       int kb) {
-#pragma unroll
-  for (int i = 0; i < ROWS / 4; ++i) r[i] = load_w<f16, 8>(base[i] + kb);
+template <typename WT>
+struct WGeo {
+  static constexpr int kLaneRow = 16 * (int)sizeof(WT) / 2;  // lanes per row: 16 (fp16), 8 (fp8)
+  static constexpr int kRowsPer = kWave / kLaneRow;            // rows per instruction: 4, 8
+  static constexpr int kElems = 16 / (int)sizeof(WT);          // elements per lane: 8, 16
+};
+
+// This lane's address of row group 0 at column 0 of the K loop, for the tile
+// whose first row is `row` of a matrix with row length ld.
+template <typename WT>
+__device__ __forceinline__ const WT* w_lane_base(const WT* mat, int row, int64_t ld, int lane) {
+  return mat + (int64_t)(row + lane / WGeo<WT>::kLaneRow) * ld +
+         (lane % WGeo<WT>::kLaneRow) * WGeo<WT>::kElems;
 }
 
-template <int ROWS>
-__device__ __forceinline__ void w_store(WTile<ROWS>& t, const H8 (&r)[ROWS / 4], int lane) {
+template <typename WT, int ROWS>
+struct WRegs {
+  static constexpr int N = ROWS / WGeo<WT>::kRowsPer;  // load instructions per K step
+  u32x4 v[N];
+};
+
+// Loads of one K step: base[i] is this lane's address for row group i at
+// column 0 of the K loop; kb is the step's first column.
+template <typename WT, int ROWS>
+__device__ __forceinline__ void w_load(WRegs<WT, ROWS>& r,
+                                       const WT* const (&base)[WRegs<WT, ROWS>::N], int kb) {
 #pragma unroll
-  for (int i = 0; i < ROWS / 4; ++i) t.w[4 * i + (lane >> 4)][lane & 15] = r[i];
+  for (int i = 0; i < WRegs<WT, ROWS>::N; ++i)
+    r.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base[i] + kb));
+}
+
+__device__ __forceinline__ H8 fp8x8_to_h8(uint32_t a, uint32_t b) {
+  typedef f16 h2 __attribute__((ext_vector_type(2)));
+  const h2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(a, 1.0f, false);
+  const h2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(a, 1.0f, true);
+  const h2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(b, 1.0f, false);
+  const h2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(b, 1.0f, true);
+  return H8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+template <typename WT, int ROWS>
+__device__ __forceinline__ void w_store(WTile<ROWS>& t, const WRegs<WT, ROWS>& r, int lane) {
+  constexpr int LR = WGeo<WT>::kLaneRow, RP = WGeo<WT>::kRowsPer;
+#pragma unroll
+  for (int i = 0; i < WRegs<WT, ROWS>::N; ++i) {
+    const int row = RP * i + lane / LR;
+    if constexpr (std::is_same<WT, fp8w>::value) {
+      const int c = 2 * (lane % LR);
+      t.w[row][c] = fp8x8_to_h8(r.v[i][0], r.v[i][1]);
+      t.w[row][c + 1] = fp8x8_to_h8(r.v[i][2], r.v[i][3]);
+    } else {
+      t.w[row][lane % LR] = __builtin_bit_cast(H8, r.v[i]);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -262,13 +308,13 @@ __device__ __forceinline__ void w_store(WTile<ROWS>& t, const H8 (&r)[ROWS / 4],
 // the K loop has no per-tile branches.  A wave's weight tile holds its 16 gate
 // rows (tile rows 0-15) and the same 16 up rows (tile rows 16-31).
 // ---------------------------------------------------------------------------
-template <bool LO, int NT>
+template <typename WT, bool LO, int NT>
 __device__ __forceinline__ void gu_pass(TokTile& xs, WTile<32>& wt,
-                                        const f16* const (&wbase)[8],
+                                        const WT* const (&wbase)[WRegs<WT, 32>::N],
                                         const f16* __restrict__ x_hi,
                                         const f16* __restrict__ x_lo, const BatchRoute& r,
                                         int p0, int mt, float* __restrict__ act, int row0,
-                                        const Geom& g, int lane) {
+                                        const float* __restrict__ sc, const Geom& g, int lane) {
   f32x4 ag[NT], au[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) ag[n] = au[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -278,16 +324,17 @@ __device__ __forceinline__ void gu_pass(TokTile& xs, WTile<32>& wt,
 
   // Software pipeline, one K step deep: step s+1's weight and token loads are
   // issued before step s's MFMAs.
-  H8 wr[8], th[kTilePieces], tl[kTilePieces];
-  w_load<32>(wr, wbase, 0);
+  WRegs<WT, 32> wr;
+  H8 th[kTilePieces], tl[kTilePieces];
+  w_load<WT, 32>(wr, wbase, 0);
   gu_tile_load(th, tl, x_hi, x_lo, off, 0, LO);
   for (int s = 0; s < ns; ++s) {
     __syncthreads();  // every wave is done reading the previous tiles
     tile_store(xs, th, tl, LO);
-    w_store<32>(wt, wr, lane);
+    w_store<WT, 32>(wt, wr, lane);
     __syncthreads();
     if (s + 1 < ns) {
-      w_load<32>(wr, wbase, (s + 1) * kBK);
+      w_load<WT, 32>(wr, wbase, (s + 1) * kBK);
       gu_tile_load(th, tl, x_hi, x_lo, off, (s + 1) * kBK, LO);
     }
 #pragma unroll
@@ -311,6 +358,13 @@ __device__ __forceinline__ void gu_pass(TokTile& xs, WTile<32>& wt,
   }
 
   // D layout: lane holds token n*16 + (lane % 16), rows 4 (lane / 16) .. +4.
+  // fp8: sc = the expert's row scales, gate rows at sc, up rows at sc + I.
+  const int rq = row0 + (lane >> 4) * 4;
+  f32x4 sg, su;
+  if constexpr (std::is_same<WT, fp8w>::value) {
+    sg = *reinterpret_cast<const f32x4*>(sc + rq);
+    su = *reinterpret_cast<const f32x4*>(sc + g.I + rq);
+  }
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     const int tn = n * 16 + (lane & 15);
@@ -319,14 +373,19 @@ __device__ __forceinline__ void gu_pass(TokTile& xs, WTile<32>& wt,
       const float w = r.pair_w[p];
       f32x4 v;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = w * (silu(ag[n][i]) * au[n][i]);
-      *reinterpret_cast<f32x4*>(act + (int64_t)p * g.I + row0 + (lane >> 4) * 4) = v;
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (std::is_same<WT, fp8w>::value)
+          v[i] = w * (silu(ag[n][i] * sg[i]) * (au[n][i] * su[i]));
+        else
+          v[i] = w * (silu(ag[n][i]) * au[n][i]);
+      }
+      *reinterpret_cast<f32x4*>(act + (int64_t)p * g.I + rq) = v;
     }
   }
 }
 
-template <bool LO>
-__global__ __launch_bounds__(kBlk) void k_gu_mfma(const f16* __restrict__ wbuf,
+template <typename WT, bool LO>
+__global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
                                                   const f16* __restrict__ x_hi,
                                                   const f16* __restrict__ x_lo, BatchRoute r,
                                                   float* __restrict__ act, Geom g) {
@@ -339,18 +398,25 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const f16* __restrict__ wbuf,
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int row0 = blockIdx.x * kBM + wave * 16;
-  const f16* G = wbuf + (int64_t)e * g.stride + (int64_t)(row0 + (lane >> 4)) * g.h + (lane & 15) * 8;
-  const f16* wbase[8];
+  const WT* blk = wbuf + (int64_t)e * g.stride;
+  const WT* G = w_lane_base(blk, row0, g.h, lane);
+  // Tile rows 0-15: gate rows row0 ..; rows 16-31: the same up rows.
+  constexpr int N = WRegs<WT, 32>::N, RP = WGeo<WT>::kRowsPer;
+  const WT* wbase[N];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) wbase[i] = G + (i < 4 ? 0 : g.off_up) + (int64_t)(4 * (i % 4)) * g.h;
+  for (int i = 0; i < N; ++i)
+    wbase[i] = G + (i < N / 2 ? 0 : g.off_up) + (int64_t)(RP * (i % (N / 2))) * g.h;
+  const float* sc = nullptr;
+  if constexpr (std::is_same<WT, fp8w>::value) sc = wscales(blk, g.off_scale);
   WTile<32>& wt = wts[wave];
   for (int m0 = 0; m0 < M; m0 += kMaxTok) {
     const int mt = min(kMaxTok, M - m0);
+    const int p0 = pbeg + m0;
     switch ((mt + 15) / 16) {
-      case 1: gu_pass<LO, 1>(xs, wt, wbase, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
-      case 2: gu_pass<LO, 2>(xs, wt, wbase, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
-      case 3: gu_pass<LO, 3>(xs, wt, wbase, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
-      default: gu_pass<LO, 4>(xs, wt, wbase, x_hi, x_lo, r, pbeg + m0, mt, act, row0, g, lane); break;
+      case 1: gu_pass<WT, LO, 1>(xs, wt, wbase, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
+      case 2: gu_pass<WT, LO, 2>(xs, wt, wbase, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
+      case 3: gu_pass<WT, LO, 3>(xs, wt, wbase, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
+      default: gu_pass<WT, LO, 4>(xs, wt, wbase, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
     }
   }
 }
@@ -359,10 +425,12 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const f16* __restrict__ wbuf,
 // Down.  grid (h / 64, kKSplit, expert slots).  K slice ks covers steps
 // [nsteps * ks / kKSplit, nsteps * (ks + 1) / kKSplit).
 // ---------------------------------------------------------------------------
-template <int NT>
-__device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt, const f16* const (&wbase)[4],
+template <typename WT, int NT>
+__device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt,
+                                        const WT* const (&wbase)[WRegs<WT, 16>::N],
                                         const float* __restrict__ act, int p0, int mt, int sb,
-                                        int se, float* __restrict__ y, int row0, const Geom& g,
+                                        int se, float* __restrict__ y, int row0,
+                                        const float* __restrict__ sdown, const Geom& g,
                                         int lane) {
   f32x4 acc[NT];
 #pragma unroll
@@ -370,16 +438,17 @@ __device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt, const f16* c
   if (sb < se) {
     int64_t off[kTilePieces];
     tile_rows(off, nullptr, p0, mt, g.I);
-    H8 wr[4], th[kTilePieces], tl[kTilePieces];
-    w_load<16>(wr, wbase, sb * kBK);
+    WRegs<WT, 16> wr;
+    H8 th[kTilePieces], tl[kTilePieces];
+    w_load<WT, 16>(wr, wbase, sb * kBK);
     dn_tile_load(th, tl, act, off, sb * kBK);
     for (int s = sb; s < se; ++s) {
       __syncthreads();
       tile_store(xs, th, tl, true);
-      w_store<16>(wt, wr, lane);
+      w_store<WT, 16>(wt, wr, lane);
       __syncthreads();
       if (s + 1 < se) {
-        w_load<16>(wr, wbase, (s + 1) * kBK);
+        w_load<WT, 16>(wr, wbase, (s + 1) * kBK);
         dn_tile_load(th, tl, act, off, (s + 1) * kBK);
       }
 #pragma unroll
@@ -395,15 +464,26 @@ __device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt, const f16* c
       }
     }
   }
+  // fp8: rows row0 + 4 (lane / 16) .. + 4 times their scales.
+  const int rq = row0 + (lane >> 4) * 4;
+  f32x4 sd;
+  if constexpr (std::is_same<WT, fp8w>::value) sd = *reinterpret_cast<const f32x4*>(sdown + rq);
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     const int tn = n * 16 + (lane & 15);
-    if (tn < mt)
-      *reinterpret_cast<f32x4*>(y + (int64_t)(p0 + tn) * g.h + row0 + (lane >> 4) * 4) = acc[n];
+    if (tn < mt) {
+      f32x4 v = acc[n];
+      if constexpr (std::is_same<WT, fp8w>::value) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] *= sd[i];
+      }
+      *reinterpret_cast<f32x4*>(y + (int64_t)(p0 + tn) * g.h + rq) = v;
+    }
   }
 }
 
-__global__ __launch_bounds__(kBlk) void k_dn_mfma(const f16* __restrict__ wbuf, BatchRoute r,
+template <typename WT>
+__global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, BatchRoute r,
                                                   const float* __restrict__ act,
                                                   float* __restrict__ ypart, Geom g, int P) {
   __shared__ TokTile xs;
@@ -419,20 +499,23 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const f16* __restrict__ wbuf, 
   const int nsteps = g.I / kBK;
   const int sb = nsteps * ks / BatchWs::kKSplit;
   const int se = nsteps * (ks + 1) / BatchWs::kKSplit;
-  const f16* D = wbuf + (int64_t)e * g.stride + g.off_down +
-                 (int64_t)(row0 + (lane >> 4)) * g.I + (lane & 15) * 8;
-  const f16* wbase[4];
+  const WT* blk = wbuf + (int64_t)e * g.stride;
+  const WT* D = w_lane_base(blk + g.off_down, row0, g.I, lane);
+  const float* sdown = nullptr;  // fp8: s_down[h] follows the I gate and I up scales
+  if constexpr (std::is_same<WT, fp8w>::value) sdown = wscales(blk, g.off_scale) + 2 * g.I;
+  constexpr int N = WRegs<WT, 16>::N;
+  const WT* wbase[N];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) wbase[i] = D + (int64_t)(4 * i) * g.I;
+  for (int i = 0; i < N; ++i) wbase[i] = D + (int64_t)(WGeo<WT>::kRowsPer * i) * g.I;
   float* y = ypart + (int64_t)ks * P * g.h;
   WTile<16>& wt = wts[wave];
   for (int m0 = 0; m0 < M; m0 += kMaxTok) {
     const int mt = min(kMaxTok, M - m0);
     switch ((mt + 15) / 16) {
-      case 1: dn_pass<1>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
-      case 2: dn_pass<2>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
-      case 3: dn_pass<3>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
-      default: dn_pass<4>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
+      case 1: dn_pass<WT, 1>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+      case 2: dn_pass<WT, 2>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+      case 3: dn_pass<WT, 3>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+      default: dn_pass<WT, 4>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
     }
   }
 }
@@ -453,8 +536,9 @@ __global__ __launch_bounds__(kBlk) void k_combine(const float* __restrict__ ypar
   out[(int64_t)t * h + row] = to_out<OT>(s);
 }
 
-template <typename XT>
+template <typename WT, typename XT>
 hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
+  constexpr int64_t es = sizeof(WT);
   Geom g;
   g.E = p.E;
   g.h = p.h;
@@ -462,23 +546,24 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
   g.k = p.k;
   g.renorm = p.renorm;
   g.B = p.B;
-  g.stride = p.stride_b / 2;
-  g.off_up = p.off_up_b / 2;
-  g.off_down = p.off_down_b / 2;
+  g.stride = p.stride_b / es;
+  g.off_up = p.off_up_b / es;
+  g.off_down = p.off_down_b / es;
+  g.off_scale = p.off_scale_b;
   const int P = p.B * p.k;
   const int slots = std::min(p.E, P);
-  const f16* wb = static_cast<const f16*>(p.wbuf);
+  const WT* wb = static_cast<const WT*>(p.wbuf);
 
   hipLaunchKernelGGL(k_route, dim3(1), dim3(1024), 0, s, w.logits, p.B, p.E, p.k, p.renorm,
                      p.topk_ids, p.topk_w, w.route);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   constexpr bool LO = std::is_same<XT, float>::value;
-  hipLaunchKernelGGL((k_gu_mfma<LO>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s, wb, w.x_hi,
+  hipLaunchKernelGGL((k_gu_mfma<WT, LO>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s, wb, w.x_hi,
                      w.x_lo, w.route, w.act, g);
   if ((err = hipGetLastError()) != hipSuccess) return err;
-  hipLaunchKernelGGL(k_dn_mfma, dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s, wb,
-                     w.route, w.act, w.ypart, g, P);
+  hipLaunchKernelGGL((k_dn_mfma<WT>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s,
+                     wb, w.route, w.act, w.ypart, g, P);
   if ((err = hipGetLastError()) != hipSuccess) return err;
   hipLaunchKernelGGL((k_combine<XT>), dim3((p.h + kBlk - 1) / kBlk, p.B), dim3(kBlk), 0, s,
                      w.ypart, w.route, static_cast<XT*>(p.out), p.h, p.k, P);
@@ -488,14 +573,17 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
 }  // namespace
 
 bool grouped_ok(const Problem& p) {
-  return p.B > 1 && p.wdt == WR_F16 && p.vec == 8 && p.h % kBK == 0 && p.I % kBK == 0;
+  const bool wt = (p.wdt == WR_F16 && p.vec == 8) || (p.wdt == WR_FP8_E4M3 && p.vec == 16);
+  return p.B > 1 && wt && p.h % kBK == 0 && p.I % kBK == 0;
 }
 
 hipError_t launch_grouped(const Problem& p, hipStream_t s) {
   const BatchWs w = BatchWs::carve(p.ws, p.E, p.h, p.I, p.k, p.B);
   hipError_t err = launch_logits_split(p, w.logits, w.x_hi, w.x_lo, s);
   if (err != hipSuccess) return err;
-  return p.adt == WR_F16 ? grouped_t<f16>(p, w, s) : grouped_t<float>(p, w, s);
+  if (p.wdt == WR_FP8_E4M3)
+    return p.adt == WR_F16 ? grouped_t<fp8w, f16>(p, w, s) : grouped_t<fp8w, float>(p, w, s);
+  return p.adt == WR_F16 ? grouped_t<f16, f16>(p, w, s) : grouped_t<f16, float>(p, w, s);
 }
 
 }  // namespace wr

@@ -182,18 +182,25 @@ __global__ __launch_bounds__(1024) void k_gate_topk(const float* __restrict__ ga
 
 // act for intermediate index r of the expert block at blk, from the gate and
 // up dot products gs and us and the gate weight wk:
-//   wk * silu(gs) * us                                   (unscaled types)
-//   wk * silu(gs * s_gate[r]) * (us * s_up[r]) * s_down[r]  (fp8: the per-row
-//     gate/up scales, and the down scale of column r folded into act)
+//   wk * silu(gs) * us                                  (unscaled types)
+//   wk * silu(gs * s_gate[r]) * (us * s_up[r])          (fp8 row scales)
 template <typename WT>
 __device__ __forceinline__ float act_value(const WT* blk, const Geom& g, int r, float wk,
                                            float gs, float us) {
   if constexpr (std::is_same<WT, fp8w>::value) {
     const float* sc = wscales(blk, g.off_scale);
-    return (wk * (silu(gs * sc[r]) * (us * sc[g.I + r]))) * sc[2 * g.I + r];
+    return wk * (silu(gs * sc[r]) * (us * sc[g.I + r]));
   } else {
     return wk * (silu(gs) * us);
   }
+}
+
+// fp8: scale of down row `row` of selected expert kk (s_down follows the I
+// gate and I up scales).
+template <typename WT>
+__device__ __forceinline__ float down_scale(const WT* wbuf, const Geom& g, const TopK& t, int kk,
+                                            int row) {
+  return wscales(wbuf + (int64_t)topk_id(t, kk) * g.stride, g.off_scale)[2 * g.I + row];
 }
 
 // ---------------------------------------------------------------------------
@@ -316,9 +323,15 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 #pragma unroll
     for (int j = 0; j < RPD; ++j) acc[j] = 0.0f;
 
+    constexpr bool kFp8 = std::is_same<WT, fp8w>::value;
     for (int kk = 0; kk < g.k; ++kk) {
       const WT* D = wbuf + (int64_t)topk_id(t, kk) * g.stride + g.off_down + (int64_t)r0 * g.I;
       const float* a = ab + (int64_t)kk * g.I;
+      // fp8: this expert's rows accumulate apart and are scaled per row below.
+      float ek[RPD];
+#pragma unroll
+      for (int j = 0; j < RPD; ++j) ek[j] = 0.0f;
+      float* const dst = kFp8 ? ek : acc;
       for (int c0 = lane * VEC; c0 < g.I; c0 += U * CH) {
         V wv[U][RPD];
         float av[U][VEC];
@@ -341,7 +354,12 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 #pragma unroll
           for (int j = 0; j < RPD; ++j)
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) acc[j] = fmaf(wdec<WT>(wv[u][j], i), av[u][i], acc[j]);
+            for (int i = 0; i < VEC; ++i) dst[j] = fmaf(wdec<WT>(wv[u][j], i), av[u][i], dst[j]);
+      }
+      if constexpr (kFp8) {
+#pragma unroll
+        for (int j = 0; j < RPD; ++j)
+          if (j < nrows) acc[j] = fmaf(down_scale(wbuf, g, t, kk, r0 + j), ek[j], acc[j]);
       }
     }
 
@@ -497,11 +515,13 @@ __device__ __forceinline__ void down_tile_load(typename WVec<WT, VEC>::type (&wv
 }
 
 // acc[j] += tile row j . act over the tile's chunks (act of expert kk at
-// act + kk * act_row).
+// act + kk * act_row).  fp8: each chunk's products are summed apart and
+// added times the row scale of the chunk's expert, sdn[kk * RPD + j].
 template <typename WT, typename V, int VEC, int RPD, int U>
 __device__ __forceinline__ void down_tile_fma(float (&acc)[RPD], const V (&wv)[U][RPD],
                                               const float* act, const Geom& g,
-                                              int64_t act_row, int q0, int nch, int lane) {
+                                              int64_t act_row, int q0, int nch, int lane,
+                                              const float* sdn) {
   const int C = g.k * nch;
   float av[U][VEC];
 #pragma unroll
@@ -516,12 +536,27 @@ __device__ __forceinline__ void down_tile_fma(float (&acc)[RPD], const V (&wv)[U
       for (int i = 0; i < VEC; ++i) av[u][i] = 0.0f;
     }
   }
+  if constexpr (std::is_same<WT, fp8w>::value) {
 #pragma unroll
-  for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u) {
+      const int q = q0 + u * kWavesPerBlock;
+      const int kk = q < C ? q / nch : 0;  // past the end: zero products, any valid scale
 #pragma unroll
-    for (int j = 0; j < RPD; ++j)
+      for (int j = 0; j < RPD; ++j) {
+        float d = 0.0f;
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) acc[j] = fmaf(wdec<WT>(wv[u][j], i), av[u][i], acc[j]);
+        for (int i = 0; i < VEC; ++i) d = fmaf(wdec<WT>(wv[u][j], i), av[u][i], d);
+        acc[j] = fmaf(sdn[kk * RPD + j], d, acc[j]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < RPD; ++j)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc[j] = fmaf(wdec<WT>(wv[u][j], i), av[u][i], acc[j]);
+  }
 }
 
 template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2>
@@ -574,7 +609,9 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   }
 
   // ---- down block ----
+  constexpr bool kFp8 = std::is_same<WT, fp8w>::value;
   __shared__ float part[kWavesPerBlock][RPD];
+  __shared__ float sdn[kFp8 ? WR_MAX_TOPK * RPD : 1];  // fp8 row scales [kk][j]
   const int r0 = ((int)blockIdx.x - hs.n1) * RPD;
   const int nrows = min(RPD, g.h - r0);
   const int nch = (g.I + kWave * VEC - 1) / (kWave * VEC);
@@ -582,6 +619,11 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
 
   V pre[U2][RPD];
   down_tile_load<WT, VEC, RPD, U2>(pre, wbuf, g, t, r0, nrows, wave, nch, lane);
+  if constexpr (kFp8) {
+    // Published to the block by the __syncthreads after the wait below.
+    const int i = threadIdx.x, kk = i / RPD, j = i % RPD;
+    if (kk < g.k) sdn[i] = j < nrows ? down_scale(wbuf, g, t, kk, r0 + j) : 0.0f;
+  }
 
   if (wave == 0) {
     // Lane c waits for the blocks counted by counter c: ids b < n1, b % 64 == c.
@@ -617,11 +659,11 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   float acc[RPD];
 #pragma unroll
   for (int j = 0; j < RPD; ++j) acc[j] = 0.0f;
-  down_tile_fma<WT, V, VEC, RPD, U2>(acc, pre, act, g, act_row, wave, nch, lane);
+  down_tile_fma<WT, V, VEC, RPD, U2>(acc, pre, act, g, act_row, wave, nch, lane, sdn);
   for (int q0 = wave + kWavesPerBlock * U2; q0 < C; q0 += kWavesPerBlock * U2) {
     V wv[U2][RPD];
     down_tile_load<WT, VEC, RPD, U2>(wv, wbuf, g, t, r0, nrows, q0, nch, lane);
-    down_tile_fma<WT, V, VEC, RPD, U2>(acc, wv, act, g, act_row, q0, nch, lane);
+    down_tile_fma<WT, V, VEC, RPD, U2>(acc, wv, act, g, act_row, q0, nch, lane, sdn);
   }
 #pragma unroll
   for (int j = 0; j < RPD; ++j) {

@@ -48,15 +48,11 @@ __global__ __launch_bounds__(kBlock) void k_matvec(const WT* __restrict__ W,
   if (lane == 0) y[r] = scale != nullptr ? acc * scale[r] : acc;
 }
 
-// act = silu(gate) * up (src/naive_moe.cu:117-128), times the fp8 down-column
-// scale when col_scale != nullptr.
+// act = silu(gate) * up (src/naive_moe.cu:117-128).
 __global__ void k_swiglu(const float* __restrict__ gate, const float* __restrict__ up,
-                         float* __restrict__ act, int n, const float* __restrict__ col_scale) {
+                         float* __restrict__ act, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) {
-    const float a = silu(gate[i]) * up[i];
-    act[i] = col_scale != nullptr ? a * col_scale[i] : a;
-  }
+  if (i < n) act[i] = silu(gate[i]) * up[i];
 }
 
 // accum = (first ? 0 : accum) + w * expert_out; the last expert also writes
@@ -132,7 +128,7 @@ hipError_t naive_t(const Problem& p, const NaiveWs& w, const HostTopK& t, hipStr
     const WT* G = reinterpret_cast<const WT*>(eb);
     const WT* U = reinterpret_cast<const WT*>(eb + p.off_up_b);
     const WT* D = reinterpret_cast<const WT*>(eb + p.off_down_b);
-    // fp8: s_gate, s_up, s_down, I floats each (per gate row, up row, down column)
+    // fp8 row scales: s_gate[I], s_up[I], s_down[h]
     const float* sc =
         p.off_scale_b >= 0 ? reinterpret_cast<const float*>(eb + p.off_scale_b) : nullptr;
     hipLaunchKernelGGL((k_matvec<WT, XT, VEC>), gI, dim3(kBlock), 0, s, G, x, w.gate_vec, p.I,
@@ -140,9 +136,9 @@ hipError_t naive_t(const Problem& p, const NaiveWs& w, const HostTopK& t, hipStr
     hipLaunchKernelGGL((k_matvec<WT, XT, VEC>), gI, dim3(kBlock), 0, s, U, x, w.up_vec, p.I,
                        p.h, sc != nullptr ? sc + p.I : nullptr);
     hipLaunchKernelGGL(k_swiglu, dim3((p.I + 255) / 256), dim3(256), 0, s, w.gate_vec, w.up_vec,
-                       w.act_vec, p.I, sc != nullptr ? sc + 2 * p.I : nullptr);
+                       w.act_vec, p.I);
     hipLaunchKernelGGL((k_matvec<WT, float, VEC>), gH, dim3(kBlock), 0, s, D, w.act_vec,
-                       w.expert_out, p.h, p.I, static_cast<const float*>(nullptr));
+                       w.expert_out, p.h, p.I, sc != nullptr ? sc + 2 * p.I : nullptr);
     hipLaunchKernelGGL((k_weighted_accum<XT>), dim3((p.h + 255) / 256), dim3(256), 0, s, w.accum,
                        w.expert_out, t.w[kk], p.h, kk == 0 ? 1 : 0,
                        kk == p.k - 1 ? out : static_cast<XT*>(nullptr));

@@ -66,10 +66,10 @@ def weight_layout(num_experts: int, hidden_dim: int, intermediate_dim: int,
 
     float32 / float16 / bfloat16: ``expert_layout`` with the element size, no
     scales.  float8_e4m3fn: 1-byte codes at the same element offsets, then at
-    ``scale_offset`` (3 I h rounded up to 16 bytes) three fp32 arrays of I
-    values: gate row scales, up row scales and down column scales, so that
-    gate[r][c] = q * s_gate[r], up[r][c] = q * s_up[r] and
-    down[r][c] = q * s_down[c]; the stride covers them, rounded up to 128."""
+    ``scale_offset`` (3 I h rounded up to 16 bytes) one fp32 scale per output
+    row, s_gate[I], s_up[I] and s_down[h], so that gate[r][c] = q * s_gate[r],
+    up[r][c] = q * s_up[r] and down[r][c] = q * s_down[r]; the stride covers
+    them, rounded up to 128."""
     if dtype not in WEIGHT_DTYPES:
         raise ValueError(f"weight dtype must be one of {WEIGHT_DTYPES}, got {dtype}")
     es = torch.empty((), dtype=dtype).element_size()
@@ -79,7 +79,8 @@ def weight_layout(num_experts: int, hidden_dim: int, intermediate_dim: int,
         return out
     n = intermediate_dim * hidden_dim
     sc = (3 * n + 15) // 16 * 16
-    stride = (sc + 12 * intermediate_dim + EXPERT_ALIGN - 1) // EXPERT_ALIGN * EXPERT_ALIGN
+    stride = ((sc + 4 * (2 * intermediate_dim + hidden_dim) + EXPERT_ALIGN - 1)
+              // EXPERT_ALIGN * EXPERT_ALIGN)
     return {"gate_proj_offset": 0, "up_proj_offset": n, "down_proj_offset": 2 * n,
             "scale_offset": sc, "expert_stride": stride, "elem_bytes": 1}
 
@@ -111,8 +112,8 @@ def _pack_expert_weights(
     Per expert, row-major: [gate_proj I x h][up_proj I x h][down_proj h x I],
     each expert block zero-padded to a 128-byte boundary.  ``dtype`` selects
     float32 (the reference's only layout, the default), float16, bfloat16, or
-    float8_e4m3fn, which quantizes with ``quantize_fp8`` (gate and up per row,
-    down per column) and stores the scales after the codes
+    float8_e4m3fn, which quantizes every matrix with ``quantize_fp8`` per row
+    (output channel) and stores the scales after the codes
     (``weight_layout``).  The buffer is created on the device of
     ``gate_proj[0]``.
     """
@@ -129,17 +130,17 @@ def _pack_expert_weights(
             buf[base + 2 * n:base + 3 * n] = down_proj[e].reshape(-1)
         return buf
     raw = buf.view(torch.uint8)
-    I = intermediate_dim
+    ns = 2 * intermediate_dim + hidden_dim
     for e in range(num_experts):
         base = e * stride_el
         qg, sg = quantize_fp8(gate_proj[e], 1)
         qu, su = quantize_fp8(up_proj[e], 1)
-        qd, sd = quantize_fp8(down_proj[e], 0)
+        qd, sd = quantize_fp8(down_proj[e], 1)
         buf[base:base + n] = qg.reshape(-1)
         buf[base + n:base + 2 * n] = qu.reshape(-1)
         buf[base + 2 * n:base + 3 * n] = qd.reshape(-1)
         sc = base + off["scale_offset"]
-        raw[sc:sc + 12 * I].view(torch.float32).copy_(torch.cat([sg, su, sd]))
+        raw[sc:sc + 4 * ns].view(torch.float32).copy_(torch.cat([sg, su, sd]))
     return buf
 
 

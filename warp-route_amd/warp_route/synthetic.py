@@ -95,11 +95,11 @@ def make_layer(num_experts: int, hidden_dim: int, intermediate_dim: int,
             w = torch.randn(shape, generator=gen, device=gen_device, dtype=torch.float32)
             w.mul_(expert_std)
             if fp8:
-                # gate and up: a scale per row; down: a scale per column
-                q, sc = quantize_fp8(w, 1 if j < 2 else 0)
+                # a scale per row: gate and up rows at j * I, down rows at 2 I
+                q, sc = quantize_fp8(w, 1)
                 buf[base + j * n:base + (j + 1) * n].copy_(q.reshape(-1))
                 s0 = base + off["scale_offset"] + j * 4 * I
-                raw[s0:s0 + 4 * I].view(torch.float32).copy_(sc)
+                raw[s0:s0 + 4 * sc.numel()].view(torch.float32).copy_(sc)
                 del q, sc
             else:
                 buf[base + j * n:base + (j + 1) * n].copy_(w.reshape(-1).to(weight_dtype))
