@@ -10,7 +10,9 @@ resident in HBM.  Layers rotate over --layers independent random layers
 calls.
 
 Prints one JSON line: value = microseconds per layer (lower is better),
-roofline = selected-expert weight bytes / layer time against 8 TB/s HBM3E,
+roofline = selected-expert weight bytes / the FFN kernel's average duration
+(HIP events around k_fused_ffn alone, through the C-ABI's split entry points)
+against 8 TB/s HBM3E, with the whole layer's rate beside it,
 cpu_baseline = the reference's pure-torch MoE (fp32, host cores) timed on a
 bounded sample of the same layer.
 
@@ -109,6 +111,56 @@ def cpu_baseline(x, gw, buf, cfg, seconds: float):
                    f"median), after 2 warm-ups; {fp32_bytes / med_us / 1e3:.1f} GB/s on the "
                    f"{fp32_bytes / 1e6:.0f} MB of fp32 selected weights; CPU: {cpu_model()}"),
     }
+
+
+def ffn_kernel_us(layers, cfg, steps: int, warmup: int) -> float:
+    """Average duration of the expert-FFN kernel alone (k_fused_ffn): each
+    call goes through the C-ABI's two halves of wr_fused_moe, with HIP events
+    recorded on the current stream between wr_fused_moe_route and
+    wr_fused_moe_ffn and after the latter, so each pair brackets exactly the
+    FFN launch."""
+    import torch
+    from warp_route import capi
+    E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+    lib = capi.lib()
+    nws = lib.wr_workspace_bytes(capi.WR_KIND_FUSED, E, h, I, k, 1)
+    wtag = {torch.float32: capi.WR_F32, torch.float16: capi.WR_F16, torch.bfloat16: capi.WR_BF16,
+            torch.float8_e4m3fn: capi.WR_FP8_E4M3}
+    keep, calls = [], []
+    for x, gw, buf in layers:
+        out = torch.empty_like(x)
+        ws = torch.empty(nws, dtype=torch.uint8, device=x.device)
+        a = capi.WrMoeArgs()
+        a.gate_w, a.weight_buf = gw.data_ptr(), buf.data_ptr()
+        a.weight_bytes = buf.numel() * buf.element_size()
+        a.weight_dtype = wtag[buf.dtype]
+        a.act_dtype = capi.WR_F16 if x.dtype == torch.float16 else capi.WR_F32
+        a.num_experts, a.hidden_dim, a.intermediate_dim, a.top_k = E, h, I, k
+        a.renormalize, a.batch_size = int(cfg.renormalize), 1
+        a.x, a.out = x.data_ptr(), out.data_ptr()
+        a.workspace, a.workspace_bytes = ws.data_ptr(), nws
+        keep.append((out, ws))
+        calls.append(a)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call(name, a):
+        st = capi.call(name, a, stream)
+        if st != capi.WR_OK:
+            raise RuntimeError(f"{name}: {capi.status_str(st)}")
+
+    for i in range(warmup):
+        call("wr_fused_moe", calls[i % len(calls)])
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i, (e0, e1) in enumerate(evs):
+        a = calls[i % len(calls)]
+        call("wr_fused_moe_route", a)
+        e0.record()
+        call("wr_fused_moe_ffn", a)
+        e1.record()
+    torch.cuda.synchronize()
+    return statistics.fmean(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3
 
 
 def _timed(step, steps: int, warmup: int) -> float:
@@ -327,7 +379,9 @@ def main() -> int:
     per = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
     p10, p50, p90 = (per[int(q * (len(per) - 1))] for q in (0.1, 0.5, 0.9))
 
-    achieved = sel_bytes / (us * 1e-6) / 1e9
+    # The dominant kernel alone, for the roofline (same layers, same stream).
+    kern_us = ffn_kernel_us(layers, cfg, args.steps, args.warmup)
+    achieved = sel_bytes / (kern_us * 1e-6) / 1e9
     traffic = None
     suffix = "" if args.weights == "fp16" else f"_{args.weights}"
     tfile = os.path.join(ROOT, "profiles", f"traffic_{cfg.name}{suffix}.json")
@@ -354,7 +408,10 @@ def main() -> int:
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic},
+                     "traffic": traffic, "kernel": "k_fused_ffn",
+                     "kernel_us": round(kern_us, 2),
+                     "layer_GBps": round(sel_bytes / us / 1e3, 1),
+                     "layer_frac": round(sel_bytes / us / 1e3 / HBM_PEAK_GBPS, 4)},
         "per_call_us": {"p10": round(p10, 2), "p50": round(p50, 2), "p90": round(p90, 2)},
         "selected_bytes_per_call": sel_bytes,
     }

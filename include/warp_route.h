@@ -178,6 +178,19 @@ WR_API int wr_gate_topk(const wr_moe_args *args, void *stream);
  * (src/fused_moe.cu:233-263, declared at src/fused_moe.cuh:29-32). */
 WR_API int wr_fused_moe(const wr_moe_args *args, void *stream);
 
+/* The two launches of wr_fused_moe, for callers that issue them separately
+ * (to overlap the router with other work on the stream's timeline, or to time
+ * the expert FFN alone).  wr_fused_moe_route computes the router logits into
+ * the workspace and resets its control block; wr_fused_moe_ffn selects the
+ * experts from those logits and runs the FFN.  Both take the arguments of
+ * wr_fused_moe and validate them the same way.  Call them in this order, on
+ * one stream, with one workspace and nothing else using that workspace in
+ * between; together they do exactly what wr_fused_moe does.  The reference
+ * has no split (fused_moe_forward, src/fused_moe.cu:233-263, computes the
+ * router inside its one kernel). */
+WR_API int wr_fused_moe_route(const wr_moe_args *args, void *stream);
+WR_API int wr_fused_moe_ffn(const wr_moe_args *args, void *stream);
+
 /* B-token fused MoE (batch_size >= 0; 0 is a no-op as in
  * src/fused_moe_batched.cu:201).  Tokens that share an expert share its weight
  * reads.  Replaces batched_fused_moe_forward (src/fused_moe_batched.cu:186-214,

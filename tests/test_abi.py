@@ -24,7 +24,7 @@ def test_header_declares_the_expected_entry_points():
     assert sorted(declared_symbols()) == sorted([
         "wr_status_str", "wr_layout", "wr_total_weight_bytes", "wr_layout_dtype",
         "wr_weight_bytes", "wr_workspace_bytes", "wr_gate_topk", "wr_fused_moe",
-        "wr_batched_fused_moe", "wr_naive_moe"])
+        "wr_fused_moe_route", "wr_fused_moe_ffn", "wr_batched_fused_moe", "wr_naive_moe"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -191,7 +191,8 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("entry", ["wr_fused_moe", "wr_batched_fused_moe", "wr_naive_moe"])
+@pytest.mark.parametrize("entry", ["wr_fused_moe", "wr_fused_moe_route", "wr_fused_moe_ffn",
+                                   "wr_batched_fused_moe", "wr_naive_moe"])
 @pytest.mark.parametrize("field,value,want", CASES)
 def test_validation_codes(entry, field, value, want):
     a = valid_args()
@@ -224,6 +225,8 @@ def test_batch_rules():
     a = valid_args(B=2)
     a.weight_bytes = 10  # would fail later; batch is checked first
     assert capi.call("wr_fused_moe", a) == capi.WR_EINVAL_BATCH
+    assert capi.call("wr_fused_moe_route", a) == capi.WR_EINVAL_BATCH
+    assert capi.call("wr_fused_moe_ffn", a) == capi.WR_EINVAL_BATCH
     assert capi.call("wr_naive_moe", a) == capi.WR_EINVAL_BATCH
     a.batch_size = -1
     assert capi.call("wr_batched_fused_moe", a) == capi.WR_EINVAL_BATCH

@@ -337,6 +337,30 @@ def test_c_abi_direct_call_matches_extension(cuda):
     assert torch.equal(out, want)
 
 
+@pytest.mark.parametrize("wd", [F16, FP8], ids=["f16", "fp8"])
+def test_split_route_ffn_matches_fused(cuda, wd):
+    """wr_fused_moe_route then wr_fused_moe_ffn on one stream and workspace is
+    bit-identical to wr_fused_moe, on a workspace that starts as junk and is
+    reused for a second layer."""
+    E, h, I, k = 8, 1024, 2048, 2
+    stream = torch.cuda.current_stream().cuda_stream
+    nws = capi.lib().wr_workspace_bytes(capi.WR_KIND_FUSED, E, h, I, k, 1)
+    work = torch.full((nws,), 0x5A, dtype=torch.uint8, device=cuda)
+    for seed in (4, 5):
+        x, gw, buf, _ = robust_layer(E, h, I, wd, k, cuda, seed0=seed)
+        want = torch.empty_like(x)
+        got = torch.full_like(x, float("nan"))
+        a = _fused_args(x, gw, buf, E, h, I, k, want, work, renorm=1)
+        assert capi.call("wr_fused_moe", a, stream) == capi.WR_OK
+        a = _fused_args(x, gw, buf, E, h, I, k, got, work, renorm=1)
+        assert capi.call("wr_fused_moe_route", a, stream) == capi.WR_OK
+        assert capi.call("wr_fused_moe_ffn", a, stream) == capi.WR_OK
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"seed {seed}"
+        ref = oracle_token(x, gw, buf, E, h, I, k, True)
+        assert_parity(got, None, None, ref, label=f"split {WNAME[wd]}")
+
+
 def _fused_args(x, gw, buf, E, h, I, k, out, work, renorm=0):
     a = capi.WrMoeArgs()
     a.gate_w, a.weight_buf = gw.data_ptr(), buf.data_ptr()

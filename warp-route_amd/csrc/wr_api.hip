@@ -226,6 +226,20 @@ WR_API int wr_fused_moe(const wr_moe_args* args, void* stream) {
   return hip_status(wr::launch_fused(p, static_cast<hipStream_t>(stream)));
 }
 
+WR_API int wr_fused_moe_route(const wr_moe_args* args, void* stream) {
+  Problem p{};
+  const int st = validate(args, WR_KIND_FUSED, &p);
+  if (st != WR_OK) return st;
+  return hip_status(wr::launch_fused_route(p, static_cast<hipStream_t>(stream)));
+}
+
+WR_API int wr_fused_moe_ffn(const wr_moe_args* args, void* stream) {
+  Problem p{};
+  const int st = validate(args, WR_KIND_FUSED, &p);
+  if (st != WR_OK) return st;
+  return hip_status(wr::launch_fused_ffn(p, static_cast<hipStream_t>(stream)));
+}
+
 WR_API int wr_batched_fused_moe(const wr_moe_args* args, void* stream) {
   Problem p{};
   const int st = validate(args, WR_KIND_BATCHED, &p);

@@ -170,6 +170,9 @@ bool grouped_ok(const Problem& p);
 hipError_t launch_grouped(const Problem& p, hipStream_t s);
 hipError_t launch_gate_topk(const Problem& p, hipStream_t s);
 hipError_t launch_fused(const Problem& p, hipStream_t s);
+// The two launches of launch_fused, for callers that issue them separately.
+hipError_t launch_fused_route(const Problem& p, hipStream_t s);
+hipError_t launch_fused_ffn(const Problem& p, hipStream_t s);
 hipError_t launch_batched(const Problem& p, hipStream_t s);
 hipError_t run_naive(const Problem& p, hipStream_t s);
 

@@ -833,16 +833,27 @@ hipError_t ffn_x(const Problem& p, const FusedWs& w, hipStream_t s) {
   }
 }
 
-hipError_t run_ffn(const Problem& p, hipStream_t s) {
+// Router logits into the workspace; for one token also the reset of the
+// single-token kernel's control words, which start each call at zero.
+hipError_t run_route(const Problem& p, hipStream_t s) {
   const FusedWs w = FusedWs::carve(p.ws, p.E, p.I, p.k, p.B);
-  // The single-token kernel's control words start each call at zero.
   static_assert(FusedWs::kCtrlWords <= kBlock, "one router thread zeroes each control word");
   unsigned* zero = p.B == 1 ? w.ctrl : nullptr;
   const int nz = FusedWs::kCtrlWords, zs = FusedWs::kCounterStride;
-  hipError_t err = p.adt == WR_F16 ? logits_t<f16>(p, w.logits, zero, nz, zs, s)
-                                   : logits_t<float>(p, w.logits, zero, nz, zs, s);
-  if (err != hipSuccess) return err;
+  return p.adt == WR_F16 ? logits_t<f16>(p, w.logits, zero, nz, zs, s)
+                         : logits_t<float>(p, w.logits, zero, nz, zs, s);
+}
+
+// The expert FFN from the logits run_route left in the workspace.
+hipError_t run_ffn_only(const Problem& p, hipStream_t s) {
+  const FusedWs w = FusedWs::carve(p.ws, p.E, p.I, p.k, p.B);
   return p.adt == WR_F16 ? ffn_x<f16>(p, w, s) : ffn_x<float>(p, w, s);
+}
+
+hipError_t run_ffn(const Problem& p, hipStream_t s) {
+  const hipError_t err = run_route(p, s);
+  if (err != hipSuccess) return err;
+  return run_ffn_only(p, s);
 }
 
 template <typename XT>
@@ -869,6 +880,10 @@ hipError_t launch_gate_topk(const Problem& p, hipStream_t s) {
 }
 
 hipError_t launch_fused(const Problem& p, hipStream_t s) { return run_ffn(p, s); }
+
+hipError_t launch_fused_route(const Problem& p, hipStream_t s) { return run_route(p, s); }
+
+hipError_t launch_fused_ffn(const Problem& p, hipStream_t s) { return run_ffn_only(p, s); }
 
 hipError_t launch_logits_split(const Problem& p, float* logits, f16* x_hi, f16* x_lo,
                                hipStream_t s) {

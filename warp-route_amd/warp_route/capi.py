@@ -93,7 +93,8 @@ def lib() -> ctypes.CDLL:
         l.wr_weight_bytes.restype = ctypes.c_int64
         l.wr_workspace_bytes.argtypes = [ctypes.c_int] * 6
         l.wr_workspace_bytes.restype = ctypes.c_size_t
-        for name in ("wr_gate_topk", "wr_fused_moe", "wr_batched_fused_moe", "wr_naive_moe"):
+        for name in ("wr_gate_topk", "wr_fused_moe", "wr_fused_moe_route", "wr_fused_moe_ffn",
+                     "wr_batched_fused_moe", "wr_naive_moe"):
             f = getattr(l, name)
             f.argtypes = [ctypes.POINTER(WrMoeArgs), ctypes.c_void_p]
             f.restype = ctypes.c_int
