@@ -17,7 +17,9 @@
 //      pass); the token tile is staged in LDS and shared by the 4 waves.
 //      v_mfma_f32_16x16x32_f16 with A = weight rows (fp16, or fp8 E4M3 codes
 //      converted exactly to fp16 while staging) and B = the hi and lo terms
-//      of x; products are exact and accumulate in fp32.  Epilogue:
+//      of x; products are exact and accumulate in fp32.  bf16 weights use
+//      v_mfma_f32_16x16x32_bf16 with x in two bf16 terms instead
+//      (|x - (hi + lo)| <= 2^-18 |x|, with fp32's exponent range).  Epilogue:
 //      act[pair][row] = w * silu(g) * u (src/fused_moe.cu:192-201), with fp8
 //      row scales applied to g and u (and to the down sums in step 4).
 //   4. k_dn_mfma: block (row tile, K slice, expert slot): the same scheme on
@@ -29,9 +31,9 @@
 // is padded to 16 tokens per tile; at 2 MFMAs per product term it stays far
 // below the time the weight stream takes (the path is HBM-bound).
 //
-// Requirements (else the per-token kernels in wr_kernels.hip run): fp16 or
-// fp8 weights with 16-byte aligned rows, h and I multiples of 128, and the
-// fp16 range for x and act (|v| < 65504).
+// Requirements (else the per-token kernels in wr_kernels.hip run): fp16, bf16
+// or fp8 weights with 16-byte aligned rows, h and I multiples of 128, and,
+// for fp16 and fp8, the fp16 range for x and act (|v| < 65504).
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -50,10 +52,23 @@ constexpr int kMaxTok = 64;     // tokens per pass: 4 MFMA N tiles
 constexpr int kPieces = kBK / 8;        // 16-byte pieces per token row of a tile
 constexpr int kLdsRow = kPieces + 1;    // padded row: spreads lanes over the LDS banks
 
-typedef f16x8 H8;
+typedef f16x8 H8;  // eight 16-bit operands: fp16, or bf16 bit patterns
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+// MFMA operand type of a weight type: bf16 for bf16 weights, fp16 otherwise
+// (fp8 codes are staged as fp16).
+template <typename WT>
+constexpr bool bf16_ops() {
+  return std::is_same<WT, bf16w>::value;
+}
+
+template <bool BF>
 __device__ __forceinline__ f32x4 mfma(const H8& a, const H8& b, const f32x4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  if constexpr (BF)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ H8 h8zero() {
@@ -196,7 +211,8 @@ __device__ __forceinline__ void gu_tile_load(H8 (&hi)[kTilePieces], H8 (&lo)[kTi
   }
 }
 
-// Down: act rows, fp32, split into two fp16 terms.
+// Down: act rows, fp32, split into two fp16 (or, BF, bf16) terms.
+template <bool BF>
 __device__ __forceinline__ void dn_tile_load(H8 (&hi)[kTilePieces], H8 (&lo)[kTilePieces],
                                              const float* __restrict__ act,
                                              const int64_t (&off)[kTilePieces], int kb) {
@@ -210,9 +226,15 @@ __device__ __forceinline__ void dn_tile_load(H8 (&hi)[kTilePieces], H8 (&lo)[kTi
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         const float v = t < 4 ? v0[t] : v1[t - 4];
-        const f16 vh = (f16)v;
-        hi[q][t] = vh;
-        lo[q][t] = (f16)(v - (float)vh);
+        if constexpr (BF) {
+          const __bf16 vh = (__bf16)v;
+          hi[q][t] = __builtin_bit_cast(f16, vh);
+          lo[q][t] = __builtin_bit_cast(f16, (__bf16)(v - (float)vh));
+        } else {
+          const f16 vh = (f16)v;
+          hi[q][t] = vh;
+          lo[q][t] = (f16)(v - (float)vh);
+        }
       }
     }
   }
@@ -345,13 +367,14 @@ __device__ __forceinline__ void gu_pass(TokTile& xs, WTile<32>& wt,
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
         const int tn = n * 16 + (lane & 15);
+        constexpr bool BF = bf16_ops<WT>();
         const H8 bh = xs.hi[tn][c];
-        ag[n] = mfma(ga, bh, ag[n]);
-        au[n] = mfma(ua, bh, au[n]);
+        ag[n] = mfma<BF>(ga, bh, ag[n]);
+        au[n] = mfma<BF>(ua, bh, au[n]);
         if (LO) {
           const H8 bl = xs.lo[tn][c];
-          ag[n] = mfma(ga, bl, ag[n]);
-          au[n] = mfma(ua, bl, au[n]);
+          ag[n] = mfma<BF>(ga, bl, ag[n]);
+          au[n] = mfma<BF>(ua, bl, au[n]);
         }
       }
     }
@@ -441,7 +464,7 @@ __device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt,
     WRegs<WT, 16> wr;
     H8 th[kTilePieces], tl[kTilePieces];
     w_load<WT, 16>(wr, wbase, sb * kBK);
-    dn_tile_load(th, tl, act, off, sb * kBK);
+    dn_tile_load<bf16_ops<WT>()>(th, tl, act, off, sb * kBK);
     for (int s = sb; s < se; ++s) {
       __syncthreads();
       tile_store(xs, th, tl, true);
@@ -449,7 +472,7 @@ __device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt,
       __syncthreads();
       if (s + 1 < se) {
         w_load<WT, 16>(wr, wbase, (s + 1) * kBK);
-        dn_tile_load(th, tl, act, off, (s + 1) * kBK);
+        dn_tile_load<bf16_ops<WT>()>(th, tl, act, off, (s + 1) * kBK);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -458,8 +481,8 @@ __device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt,
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
           const int tn = n * 16 + (lane & 15);
-          acc[n] = mfma(da, xs.hi[tn][c], acc[n]);
-          acc[n] = mfma(da, xs.lo[tn][c], acc[n]);
+          acc[n] = mfma<bf16_ops<WT>()>(da, xs.hi[tn][c], acc[n]);
+          acc[n] = mfma<bf16_ops<WT>()>(da, xs.lo[tn][c], acc[n]);
         }
       }
     }
@@ -558,7 +581,8 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
                      p.topk_ids, p.topk_w, w.route);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  constexpr bool LO = std::is_same<XT, float>::value;
+  // The lo term of x: fp32 x, or any x against bf16 (8-bit mantissa) terms.
+  constexpr bool LO = std::is_same<XT, float>::value || bf16_ops<WT>();
   hipLaunchKernelGGL((k_gu_mfma<WT, LO>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s, wb, w.x_hi,
                      w.x_lo, w.route, w.act, g);
   if ((err = hipGetLastError()) != hipSuccess) return err;
@@ -573,16 +597,19 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
 }  // namespace
 
 bool grouped_ok(const Problem& p) {
-  const bool wt = (p.wdt == WR_F16 && p.vec == 8) || (p.wdt == WR_FP8_E4M3 && p.vec == 16);
+  const bool wt = ((p.wdt == WR_F16 || p.wdt == WR_BF16) && p.vec == 8) ||
+                  (p.wdt == WR_FP8_E4M3 && p.vec == 16);
   return p.B > 1 && wt && p.h % kBK == 0 && p.I % kBK == 0;
 }
 
 hipError_t launch_grouped(const Problem& p, hipStream_t s) {
   const BatchWs w = BatchWs::carve(p.ws, p.E, p.h, p.I, p.k, p.B);
-  hipError_t err = launch_logits_split(p, w.logits, w.x_hi, w.x_lo, s);
+  hipError_t err = launch_logits_split(p, w.logits, w.x_hi, w.x_lo, p.wdt == WR_BF16 ? 1 : 0, s);
   if (err != hipSuccess) return err;
   if (p.wdt == WR_FP8_E4M3)
     return p.adt == WR_F16 ? grouped_t<fp8w, f16>(p, w, s) : grouped_t<fp8w, float>(p, w, s);
+  if (p.wdt == WR_BF16)
+    return p.adt == WR_F16 ? grouped_t<bf16w, f16>(p, w, s) : grouped_t<bf16w, float>(p, w, s);
   return p.adt == WR_F16 ? grouped_t<f16, f16>(p, w, s) : grouped_t<f16, float>(p, w, s);
 }
 

@@ -93,7 +93,7 @@ struct BatchRoute {
 struct BatchWs {
   static constexpr int kKSplit = 4;  // K slices of the down GEMM
   float* logits;  // [B][WR_MAX_EXPERTS]
-  _Float16* x_hi;  // [B][h]: x = hi + lo
+  _Float16* x_hi;  // [B][h]: x = hi + lo (fp16 terms, or bf16 bit patterns for bf16 weights)
   _Float16* x_lo;  // [B][h]
   BatchRoute route;
   float* act;    // [P][I], grouped pair order, scaled by the gate weight
@@ -162,9 +162,10 @@ struct NaiveWs {
 // Launchers (wr_kernels.hip, wr_naive.hip).  Each returns the first HIP
 // error it meets.
 hipError_t launch_logits(const Problem& p, float* logits, hipStream_t s);
-// Logits, plus x split into two fp16 terms x = hi + lo (lo = 0 for fp16 x).
+// Logits, plus x split into two 16-bit terms x = hi + lo: fp16 (lo = 0 for
+// fp16 x), or bf16 when split_bf16.
 hipError_t launch_logits_split(const Problem& p, float* logits, _Float16* x_hi, _Float16* x_lo,
-                               hipStream_t s);
+                               int split_bf16, hipStream_t s);
 // Grouped batched path: usable when grouped_ok(p).
 bool grouped_ok(const Problem& p);
 hipError_t launch_grouped(const Problem& p, hipStream_t s);

@@ -117,6 +117,8 @@ __device__ __forceinline__ float router_combine(const float* p) {
 // arrival counters, timeout flag and rotation masks), which the next kernel on
 // the stream reads.
 // With x_hi != nullptr, block (e, b) also writes its 1/E share of token b's x
+// as two 16-bit terms x = hi + lo: fp16 terms, or bf16 terms when split_bf16
+// (bit patterns in the same buffers),
 // as two fp16 terms, hi = fp16(x) and lo = fp16(x - hi) (lo = 0 for fp16 x),
 // for the batched MFMA path.
 template <typename XT, int VEC>
@@ -126,7 +128,8 @@ __global__ __launch_bounds__(kBlock) void k_router_logits(const float* __restric
                                                           int h, unsigned* __restrict__ zero,
                                                           int nzero, int zstride,
                                                           f16* __restrict__ x_hi,
-                                                          f16* __restrict__ x_lo) {
+                                                          f16* __restrict__ x_lo,
+                                                          int split_bf16) {
   __shared__ float part[4];
   const int q = threadIdx.x / kWave;
   const int e = blockIdx.x, b = blockIdx.y;
@@ -136,8 +139,16 @@ __global__ __launch_bounds__(kBlock) void k_router_logits(const float* __restric
     for (int i = e * cs + (int)threadIdx.x; i < end; i += kBlock) {
       const float v = (float)x[(int64_t)b * h + i];
       const f16 vh = (f16)v;
-      x_hi[(int64_t)b * h + i] = vh;
-      x_lo[(int64_t)b * h + i] = std::is_same<XT, float>::value ? (f16)(v - (float)vh) : (f16)0.0f;
+      if (split_bf16) {
+        const __bf16 bh = (__bf16)v;
+        const __bf16 bl = (__bf16)(v - (float)bh);
+        x_hi[(int64_t)b * h + i] = __builtin_bit_cast(f16, bh);
+        x_lo[(int64_t)b * h + i] = __builtin_bit_cast(f16, bl);
+      } else {
+        x_hi[(int64_t)b * h + i] = vh;
+        x_lo[(int64_t)b * h + i] =
+            std::is_same<XT, float>::value ? (f16)(v - (float)vh) : (f16)0.0f;
+      }
     }
   }
   if (zero != nullptr && e == 0 && b == 0 && (int)threadIdx.x < nzero)
@@ -732,15 +743,16 @@ bool router_vec4(const Problem& p) {
 
 template <typename XT>
 hipError_t logits_t(const Problem& p, float* logits, unsigned* zero, int nzero, int zstride,
-                    hipStream_t s, f16* x_hi = nullptr, f16* x_lo = nullptr) {
+                    hipStream_t s, f16* x_hi = nullptr, f16* x_lo = nullptr,
+                    int split_bf16 = 0) {
   const dim3 grid(p.E, p.B);
   const XT* x = static_cast<const XT*>(p.x);
   if (router_vec4(p))
     hipLaunchKernelGGL((k_router_logits<XT, 4>), grid, dim3(kBlock), 0, s, p.gate_w, x, logits,
-                       p.E, p.h, zero, nzero, zstride, x_hi, x_lo);
+                       p.E, p.h, zero, nzero, zstride, x_hi, x_lo, split_bf16);
   else
     hipLaunchKernelGGL((k_router_logits<XT, 1>), grid, dim3(kBlock), 0, s, p.gate_w, x, logits,
-                       p.E, p.h, zero, nzero, zstride, x_hi, x_lo);
+                       p.E, p.h, zero, nzero, zstride, x_hi, x_lo, split_bf16);
   return hipGetLastError();
 }
 
@@ -886,9 +898,9 @@ hipError_t launch_fused_route(const Problem& p, hipStream_t s) { return run_rout
 hipError_t launch_fused_ffn(const Problem& p, hipStream_t s) { return run_ffn_only(p, s); }
 
 hipError_t launch_logits_split(const Problem& p, float* logits, f16* x_hi, f16* x_lo,
-                               hipStream_t s) {
-  return p.adt == WR_F16 ? logits_t<f16>(p, logits, nullptr, 0, 0, s, x_hi, x_lo)
-                         : logits_t<float>(p, logits, nullptr, 0, 0, s, x_hi, x_lo);
+                               int split_bf16, hipStream_t s) {
+  return p.adt == WR_F16 ? logits_t<f16>(p, logits, nullptr, 0, 0, s, x_hi, x_lo, split_bf16)
+                         : logits_t<float>(p, logits, nullptr, 0, 0, s, x_hi, x_lo, split_bf16);
 }
 
 hipError_t launch_batched(const Problem& p, hipStream_t s) {
