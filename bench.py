@@ -44,13 +44,15 @@ METRIC = ("µs per MoE layer at batch=1 (Mixtral shape); "
           "achieved HBM GB/s as % of peak")
 
 
-WLABEL = {"fp16": "f16", "bf16": "bf16", "fp8": "fp8 e4m3 (per-channel fp32 scales)"}
+WLABEL = {"fp16": "f16", "bf16": "bf16", "fp8": "fp8 e4m3 (per-row fp32 scales)",
+          "mxfp4": "mxfp4 (e2m1, e8m0 scale per 32)"}
 
 
 def weight_dtype(name: str):
     """torch dtype of a --weights choice."""
     import torch
-    return {"fp16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn}[name]
+    return {"fp16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn,
+            "mxfp4": torch.float4_e2m1fn_x2}[name]
 
 
 def log(msg: str) -> None:
@@ -84,7 +86,7 @@ def cpu_baseline(x, gw, buf, cfg, seconds: float):
     logits = gwc @ xc
     sel = torch.topk(torch.softmax(logits, 0), k).indices.tolist()
     fmt = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16",
-           torch.float8_e4m3fn: "fp8"}[buf.dtype]
+           torch.float8_e4m3fn: "fp8", torch.float4_e2m1fn_x2: "mxfp4"}[buf.dtype]
     stride = O.weight_layout(E, h, I, fmt)["expert_stride"]
     raw = buf.view(torch.uint8)
     gp, up, dp = [None] * E, [None] * E, [None] * E
@@ -125,7 +127,7 @@ def ffn_kernel_us(layers, cfg, steps: int, warmup: int) -> float:
     lib = capi.lib()
     nws = lib.wr_workspace_bytes(capi.WR_KIND_FUSED, E, h, I, k, 1)
     wtag = {torch.float32: capi.WR_F32, torch.float16: capi.WR_F16, torch.bfloat16: capi.WR_BF16,
-            torch.float8_e4m3fn: capi.WR_FP8_E4M3}
+            torch.float8_e4m3fn: capi.WR_FP8_E4M3, torch.float4_e2m1fn_x2: capi.WR_MXFP4}
     keep, calls = [], []
     for x, gw, buf in layers:
         out = torch.empty_like(x)
@@ -298,7 +300,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--config", default="mixtral", choices=["mixtral", "deepseek", "dbrx"])
-    ap.add_argument("--weights", default="fp16", choices=["fp16", "bf16", "fp8"],
+    ap.add_argument("--weights", default="fp16", choices=["fp16", "bf16", "fp8", "mxfp4"],
                     help="expert weight format (the headline is fp16)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -67,6 +67,7 @@ typedef enum wr_status {
   WR_EINVAL_WORKSPACE = 7,    /* workspace NULL or smaller than required       */
   WR_EINVAL_BATCH = 8,        /* batch_size < 0, or != 1 for a single-token op */
   WR_EINVAL_KIND = 9,         /* unknown wr_kind                               */
+  WR_EINVAL_BLOCK = 10,       /* MXFP4 weights need h and I multiples of 32    */
   WR_EHIP = 100               /* a HIP runtime call failed                     */
 } wr_status;
 
@@ -74,8 +75,17 @@ typedef enum wr_status {
  * WR_F32 or WR_F16.  WR_BF16 is bfloat16 (the top 16 bits of an fp32).
  * WR_FP8_E4M3 is the OCP 8-bit float E4M3: sign, 4 exponent bits (bias 7),
  * 3 mantissa bits, subnormals, no infinities, NaN = S.1111.111, largest
- * finite value 448.  The reference stores fp32 only. */
-typedef enum wr_dtype { WR_F32 = 0, WR_F16 = 1, WR_BF16 = 2, WR_FP8_E4M3 = 3 } wr_dtype;
+ * finite value 448.  WR_MXFP4 is OCP Microscaling FP4: E2M1 elements (sign,
+ * 2 exponent bits with bias 1, 1 mantissa bit: 0, 0.5, 1, 1.5, 2, 3, 4, 6),
+ * two per byte (element 2i in bits 0-3), with one E8M0 scale 2^(s - 127) per
+ * 32 consecutive elements of a row.  The reference stores fp32 only. */
+typedef enum wr_dtype {
+  WR_F32 = 0,
+  WR_F16 = 1,
+  WR_BF16 = 2,
+  WR_FP8_E4M3 = 3,
+  WR_MXFP4 = 4
+} wr_dtype;
 
 /* Which entry point a workspace is sized for. */
 typedef enum wr_kind { WR_KIND_FUSED = 0, WR_KIND_BATCHED = 1, WR_KIND_NAIVE = 2 } wr_kind;
@@ -116,7 +126,12 @@ typedef struct wr_moe_args {
 
 /* Expert block layout for a weight dtype.  For WR_F32, WR_F16 and WR_BF16
  * the offsets are those of wr_layout with elem_bytes 4, 2, 2 and
- * scale_offset is -1.  For WR_FP8_E4M3 the three matrices hold 1-byte codes
+ * scale_offset is -1.  For WR_MXFP4 (h and I multiples of 32) the codes take
+ * half a byte per element: gate [I][h/2] bytes at 0, up at I h / 2, down
+ * [h][I/2] at I h; then at scale_offset = 3 I h / 2 rounded up to 16 bytes
+ * the E8M0 block scales, one byte per 32 elements of a row: gate [I][h/32],
+ * up [I][h/32], down [h][I/32]; expert_stride = scale_offset + 3 I h / 32
+ * rounded up to 128 bytes; elem_bytes is 0 (half a byte).  For WR_FP8_E4M3 the three matrices hold 1-byte codes
  * q at the same element offsets (gate 0, up I h, down 2 I h), followed at
  * scale_offset = 3 I h rounded up to 16 bytes by one fp32 scale per output
  * row: s_gate[I], s_up[I], then s_down[h], with
@@ -132,7 +147,7 @@ typedef struct wr_layout_info {
   int64_t down_proj_offset;
   int64_t scale_offset;   /* -1: no scales                                  */
   int64_t expert_stride;
-  int32_t elem_bytes;     /* bytes per matrix element: 4, 2 or 1            */
+  int32_t elem_bytes;     /* bytes per matrix element: 4, 2 or 1; 0 for MXFP4 */
   int32_t weight_dtype;   /* wr_dtype                                       */
 } wr_layout_info;
 

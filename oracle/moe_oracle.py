@@ -118,7 +118,8 @@ def expert_views(buf: np.ndarray, e: int, num_experts: int, hidden_dim: int,
 # ----------------------------------------------------------------------------
 # Reduced-precision weight formats (no reference counterpart)
 # ----------------------------------------------------------------------------
-WEIGHT_FORMATS = ("f32", "f16", "bf16", "fp8")
+WEIGHT_FORMATS = ("f32", "f16", "bf16", "fp8", "mxfp4")
+MX_BLOCK = 32
 
 
 def decode_bf16(bits: np.ndarray) -> np.ndarray:
@@ -143,6 +144,24 @@ def decode_e4m3(codes: np.ndarray) -> np.ndarray:
     return sign * mag
 
 
+def decode_e2m1(codes: np.ndarray) -> np.ndarray:
+    """OCP FP4 E2M1 codes (0..15) -> float64.  Bits s.ee.m, exponent bias 1:
+    e = 0 is subnormal, (-1)^s * m/2; otherwise (-1)^s * (1 + m/2) * 2^(e-1).
+    Magnitudes 0, 0.5, 1, 1.5, 2, 3, 4, 6; no infinities or NaN."""
+    c = np.asarray(codes).astype(np.int64) & 0xF
+    sign = np.where(c & 0x8, -1.0, 1.0)
+    e = (c >> 1) & 0x3
+    m = (c & 0x1).astype(np.float64)
+    mag = np.where(e == 0, m / 2.0, (1.0 + m / 2.0) * np.exp2(e - 1.0))
+    return sign * mag
+
+
+def decode_e8m0(codes: np.ndarray) -> np.ndarray:
+    """OCP E8M0 scale bytes -> float64 2^(e - 127); 255 is NaN."""
+    e = np.asarray(codes, dtype=np.uint8).astype(np.float64)
+    return np.where(e == 255, np.nan, np.exp2(e - 127.0))
+
+
 def weight_layout(num_experts: int, hidden_dim: int, intermediate_dim: int,
                   fmt: str) -> Dict[str, int]:
     """Expert block layout per weight format (wr_layout_dtype).  f32, f16 and
@@ -152,6 +171,14 @@ def weight_layout(num_experts: int, hidden_dim: int, intermediate_dim: int,
     stride rounded up to 128 bytes."""
     if fmt not in WEIGHT_FORMATS:
         raise ValueError(f"unknown weight format {fmt!r}")
+    if fmt == "mxfp4":
+        # codes half a byte per element; then E8M0 bytes, one per 32 elements
+        # of a row: gate [I][h/32], up [I][h/32], down [h][I/32]
+        n = intermediate_dim * hidden_dim
+        sc = (3 * n // 2 + 15) // 16 * 16
+        stride = (sc + 3 * n // MX_BLOCK + EXPERT_ALIGN - 1) // EXPERT_ALIGN * EXPERT_ALIGN
+        return {"gate_proj_offset": 0, "up_proj_offset": n // 2, "down_proj_offset": n,
+                "scale_offset": sc, "expert_stride": stride, "elem_bytes": 0}
     if fmt != "fp8":
         es = {"f32": 4, "f16": 2, "bf16": 2}[fmt]
         out = layout_offsets(num_experts, hidden_dim, intermediate_dim, es)
@@ -176,6 +203,18 @@ def expert_matrices(raw: np.ndarray, e: int, num_experts: int, hidden_dim: int,
     n = I * h
     base = e * lo["expert_stride"]
     es = lo["elem_bytes"]
+
+    if fmt == "mxfp4":
+        def mxmat(j, off, rows, cols):
+            b = raw[base + off:base + off + n // 2]
+            codes = np.empty(n, dtype=np.uint8)
+            codes[0::2] = b & 0xF
+            codes[1::2] = b >> 4
+            s0 = base + lo["scale_offset"] + j * (n // MX_BLOCK)
+            sc = decode_e8m0(raw[s0:s0 + n // MX_BLOCK]).reshape(rows, cols // MX_BLOCK)
+            return decode_e2m1(codes).reshape(rows, cols) * np.repeat(sc, MX_BLOCK, axis=1)
+        return (mxmat(0, lo["gate_proj_offset"], I, h), mxmat(1, lo["up_proj_offset"], I, h),
+                mxmat(2, lo["down_proj_offset"], h, I))
 
     def mat(off, rows, cols):
         b = raw[base + off:base + off + n * es]

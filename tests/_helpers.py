@@ -13,14 +13,14 @@ def f64(t: torch.Tensor) -> np.ndarray:
 
 
 FORMATS = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16",
-           torch.float8_e4m3fn: "fp8"}
+           torch.float8_e4m3fn: "fp8", torch.float4_e2m1fn_x2: "mxfp4"}
 
 
 def expert_mats(buf: torch.Tensor, e: int, E: int, h: int, I: int):
     """(gate, up, down) of expert e from a packed buffer on any device, as fp64
     numpy arrays (expert_views on the flat layout, src/expert_layout.cuh:50-71;
     bf16 and fp8 buffers are decoded by the oracle from their raw bytes)."""
-    if buf.dtype in (torch.bfloat16, torch.float8_e4m3fn):
+    if buf.dtype in (torch.bfloat16, torch.float8_e4m3fn, torch.float4_e2m1fn_x2):
         lo = O.weight_layout(E, h, I, FORMATS[buf.dtype])
         blk = buf.view(torch.uint8)[e * lo["expert_stride"]:(e + 1) * lo["expert_stride"]]
         return O.expert_matrices(blk.cpu().numpy(), 0, E, h, I, FORMATS[buf.dtype])

@@ -41,7 +41,8 @@ def test_header_constants_match_binding():
     for name in ("WR_OK", "WR_EINVAL_NULL", "WR_EINVAL_SHAPE", "WR_EINVAL_TOPK",
                  "WR_EINVAL_EXPERTS", "WR_EINVAL_DTYPE", "WR_EINVAL_WEIGHT_SIZE",
                  "WR_EINVAL_WORKSPACE", "WR_EINVAL_BATCH", "WR_EINVAL_KIND", "WR_EHIP",
-                 "WR_F32", "WR_F16", "WR_BF16", "WR_FP8_E4M3", "WR_KIND_FUSED",
+                 "WR_F32", "WR_F16", "WR_BF16", "WR_FP8_E4M3", "WR_MXFP4", "WR_EINVAL_BLOCK",
+                 "WR_KIND_FUSED",
                  "WR_KIND_BATCHED", "WR_KIND_NAIVE"):
         m = re.search(rf"\b{name} = (\d+)", text)
         assert m and int(m.group(1)) == getattr(capi, name), name
@@ -55,14 +56,22 @@ def test_struct_layout_matches_header_order():
     assert ctypes.sizeof(capi.WrLayoutInfo) == 48
 
 
-FMT = {capi.WR_F32: "f32", capi.WR_F16: "f16", capi.WR_BF16: "bf16", capi.WR_FP8_E4M3: "fp8"}
+FMT = {capi.WR_F32: "f32", capi.WR_F16: "f16", capi.WR_BF16: "bf16", capi.WR_FP8_E4M3: "fp8",
+       capi.WR_MXFP4: "mxfp4"}
 TDT = {capi.WR_F32: "float32", capi.WR_F16: "float16", capi.WR_BF16: "bfloat16",
-       capi.WR_FP8_E4M3: "float8_e4m3fn"}
+       capi.WR_FP8_E4M3: "float8_e4m3fn", capi.WR_MXFP4: "float4_e2m1fn_x2"}
 
 
 @pytest.mark.parametrize("wdt", sorted(FMT))
-@pytest.mark.parametrize("E,h,I", [(8, 4096, 14336), (64, 2048, 1408), (2, 3, 5), (3, 7, 1)])
+@pytest.mark.parametrize("E,h,I", [(8, 4096, 14336), (64, 2048, 1408), (2, 3, 5), (3, 7, 1),
+                                   (3, 96, 32)])
 def test_layout_dtype_agrees_with_python_and_oracle(E, h, I, wdt):
+    if wdt == capi.WR_MXFP4 and (h % 32 or I % 32):
+        info = capi.WrLayoutInfo()
+        st = capi.lib().wr_layout_dtype(E, h, I, wdt, ctypes.byref(info))
+        assert st == capi.WR_EINVAL_BLOCK
+        assert capi.lib().wr_weight_bytes(E, h, I, wdt) == -1
+        return
     import torch
     from oracle import moe_oracle as O
     got = capi.layout_dtype(E, h, I, wdt)
@@ -81,6 +90,12 @@ def test_fp8_layout_byte_table():
         "gate_proj_offset": 0, "up_proj_offset": 58720256, "down_proj_offset": 117440512,
         "scale_offset": 176160768, "expert_stride": 176291840, "elem_bytes": 1,
         "weight_dtype": capi.WR_FP8_E4M3}
+    # MXFP4, Mixtral: codes 3 I h / 2 = 88,080,384 bytes, then 3 I h / 32 =
+    # 5,505,024 bytes of E8M0 scales; 93,585,408 is a multiple of 128.
+    assert capi.layout_dtype(8, 4096, 14336, capi.WR_MXFP4) == {
+        "gate_proj_offset": 0, "up_proj_offset": 29360128, "down_proj_offset": 58720256,
+        "scale_offset": 88080384, "expert_stride": 93585408, "elem_bytes": 0,
+        "weight_dtype": capi.WR_MXFP4}
     lo = capi.layout_dtype(2, 3, 5, capi.WR_FP8_E4M3)
     assert (lo["up_proj_offset"], lo["down_proj_offset"], lo["scale_offset"],
             lo["expert_stride"]) == (15, 30, 48, 128)
@@ -105,7 +120,7 @@ def test_layout_rejects_bad_arguments():
     assert lib.wr_layout(1, 4, 4, 2, None) == capi.WR_EINVAL_NULL
     assert lib.wr_total_weight_bytes(1, 0, 4, 2) == -1
     info = capi.WrLayoutInfo()
-    assert lib.wr_layout_dtype(1, 4, 4, 4, ctypes.byref(info)) == capi.WR_EINVAL_DTYPE
+    assert lib.wr_layout_dtype(1, 4, 4, 5, ctypes.byref(info)) == capi.WR_EINVAL_DTYPE
     assert lib.wr_layout_dtype(1, 4, 0, 1, ctypes.byref(info)) == capi.WR_EINVAL_SHAPE
     assert lib.wr_layout_dtype(1, 4, 4, 1, None) == capi.WR_EINVAL_NULL
     assert lib.wr_weight_bytes(1, 4, 4, -1) == -1
@@ -178,7 +193,7 @@ CASES = [
     ("num_experts", 65, capi.WR_EINVAL_EXPERTS),
     ("top_k", 0, capi.WR_EINVAL_TOPK),
     ("top_k", 7, capi.WR_EINVAL_TOPK),
-    ("weight_dtype", 4, capi.WR_EINVAL_DTYPE),
+    ("weight_dtype", 5, capi.WR_EINVAL_DTYPE),
     ("act_dtype", -1, capi.WR_EINVAL_DTYPE),
     ("act_dtype", capi.WR_BF16, capi.WR_EINVAL_DTYPE),
     ("gate_w", None, capi.WR_EINVAL_NULL),
@@ -200,7 +215,15 @@ def test_validation_codes(entry, field, value, want):
     assert capi.call(entry, a) == want
 
 
-@pytest.mark.parametrize("wdt", [capi.WR_BF16, capi.WR_FP8_E4M3])
+def test_mxfp4_needs_blocks_of_32():
+    a = valid_args()  # h = 64, I = 32
+    a.weight_dtype = capi.WR_MXFP4
+    a.intermediate_dim = 48
+    assert capi.call("wr_fused_moe", a) == capi.WR_EINVAL_BLOCK
+    assert capi.status_str(capi.WR_EINVAL_BLOCK).startswith("MXFP4")
+
+
+@pytest.mark.parametrize("wdt", [capi.WR_BF16, capi.WR_FP8_E4M3, capi.WR_MXFP4])
 def test_weight_size_is_checked_per_format(wdt):
     """One byte short of wr_weight_bytes is rejected for every format (the
     fp8 layout is smaller than fp16's, and holds its scales)."""

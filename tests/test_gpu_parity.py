@@ -23,8 +23,8 @@ from warp_route.synthetic import CONFIGS, clustered_batch, make_config_layer, ma
 pytestmark = pytest.mark.gpu
 
 F32, F16 = torch.float32, torch.float16
-BF16, FP8 = torch.bfloat16, torch.float8_e4m3fn
-WNAME = {F32: "f32", F16: "f16", BF16: "bf16", FP8: "fp8"}
+BF16, FP8, MX4 = torch.bfloat16, torch.float8_e4m3fn, torch.float4_e2m1fn_x2
+WNAME = {F32: "f32", F16: "f16", BF16: "bf16", FP8: "fp8", MX4: "mxfp4"}
 
 # (E, h, I, k, weight dtype, renormalize)
 SMALL = [
@@ -95,6 +95,11 @@ LOWP = [
     (5, 100, 36, 2, BF16, False),     # h % 8 != 0: scalar path
     (5, 100, 36, 2, FP8, True),       # h % 16 != 0: scalar path
     (3, 48, 40, 3, FP8, False),       # I % 16 != 0: scalar path, k == E
+    (8, 256, 512, 2, MX4, True),      # MXFP4: blocks of 32 along rows
+    (64, 256, 512, 6, MX4, False),
+    (16, 512, 1024, 4, MX4, True),
+    (8, 4096, 1024, 2, MX4, True),    # 2 KB code rows
+    (5, 96, 64, 2, MX4, False),       # three and two blocks per row, k == 2 of 5
 ]
 
 
@@ -127,6 +132,32 @@ def test_low_precision_weight_parity(cuda, op, cfg, x_dtype):
     assert out.dtype == x_dtype and out.shape == (h,)
     ref = oracle_token(x, gw, buf, E, h, I, k, rn)
     assert_parity(out, ids, ws, ref, rel_tol=out_tol(x_dtype), label=f"{op} {ids_of(cfg)}")
+
+
+@pytest.mark.parametrize("op", ["fused", "naive", "batched"])
+def test_mxfp4_unaligned_x_takes_the_byte_path(cuda, op):
+    """x that is not 16-byte aligned (a view one element into a larger
+    tensor) makes MXFP4 take its byte-at-a-time path (two codes per load)."""
+    E, h, I, k = 8, 256, 512, 2
+    B = 2 if op == "batched" else None
+    xa, gw, buf, seed = robust_layer(E, h, I, MX4, k, cuda, batch=B)
+    big = torch.empty(xa.numel() + 1, dtype=xa.dtype, device=cuda)
+    big[1:] = xa.reshape(-1)
+    x = big[1:].view(xa.shape)
+    assert x.data_ptr() % 16 != 0
+    print(f"[gpu] mxfp4 unaligned {op} seed={seed}", flush=True)
+    if op == "batched":
+        out = F.batched_fused_moe(x, gw, buf, E, h, I, k, True)
+        torch.cuda.synchronize()
+        for b in range(B):
+            assert_parity(out[b], None, None, oracle_token(xa[b], gw, buf, E, h, I, k, True),
+                          label=f"unaligned batched b={b}")
+        return
+    fn = F.fused_moe if op == "fused" else F.naive_moe
+    out = fn(x, gw, buf, E, h, I, k, True)
+    torch.cuda.synchronize()
+    assert_parity(out, None, None, oracle_token(xa, gw, buf, E, h, I, k, True),
+                  label=f"unaligned {op}")
 
 
 @pytest.mark.parametrize("cfg", SMALL, ids=ids_of)
@@ -212,14 +243,15 @@ GROUPED = [(8, 256, 512, 2, False), (16, 512, 1024, 2, True), (64, 256, 512, 6, 
            (8, 384, 640, 1, True)]
 
 
-@pytest.mark.parametrize("wd", [F16, FP8, BF16], ids=["f16", "fp8", "bf16"])
+@pytest.mark.parametrize("wd", [F16, FP8, BF16, MX4], ids=["f16", "fp8", "bf16", "mxfp4"])
 @pytest.mark.parametrize("x_dtype", [F32, F16], ids=["xf32", "xf16"])
 @pytest.mark.parametrize("B", [2, 5, 33, 80])
 @pytest.mark.parametrize("cfg", GROUPED,
                          ids=lambda c: f"E{c[0]}-h{c[1]}-I{c[2]}-k{c[3]}" + ("-renorm" if c[4] else ""))
 def test_grouped_batched_parity(cuda, cfg, B, x_dtype, wd):
-    """The grouped MFMA batched path (fp16, fp8 or bf16 weights, h and I
-    multiples of 128; fp8 codes are staged as fp16 and scaled in the epilogue;
+    """The grouped MFMA batched path (fp16, fp8, bf16 or MXFP4 weights, h and
+    I multiples of 128; fp8 codes are staged as fp16 and scaled in the
+    epilogue, MXFP4 codes staged as fp16 times their block scale;
     bf16 weights take x and act as two bf16 terms, within 2^-18 of them, so
     their rows are compared with the single-token op at 5e-5 of max|out|
     instead of 1e-5).
@@ -370,7 +402,7 @@ def _fused_args(x, gw, buf, E, h, I, k, out, work, renorm=0):
     a.gate_w, a.weight_buf = gw.data_ptr(), buf.data_ptr()
     a.weight_bytes = buf.numel() * buf.element_size()
     a.weight_dtype = {F32: capi.WR_F32, F16: capi.WR_F16, BF16: capi.WR_BF16,
-                      FP8: capi.WR_FP8_E4M3}[buf.dtype]
+                      FP8: capi.WR_FP8_E4M3, MX4: capi.WR_MXFP4}[buf.dtype]
     a.act_dtype = capi.WR_F16 if x.dtype == torch.float16 else capi.WR_F32
     a.num_experts, a.hidden_dim, a.intermediate_dim, a.top_k = E, h, I, k
     a.renormalize, a.batch_size = renorm, 1
@@ -381,9 +413,10 @@ def _fused_args(x, gw, buf, E, h, I, k, out, work, renorm=0):
 
 @pytest.mark.parametrize("shape", [(16, 512, 256, 4, F16), (8, 4096, 14336, 2, F16),
                                    (64, 2048, 1408, 6, F16), (8, 192, 100, 3, F16),
-                                   (8, 4096, 14336, 2, FP8), (16, 6144, 10752, 4, FP8)],
+                                   (8, 4096, 14336, 2, FP8), (16, 6144, 10752, 4, FP8),
+                                   (8, 4096, 14336, 2, MX4)],
                          ids=["small", "mixtral", "deepseek", "ragged", "mixtral-fp8",
-                              "dbrx-fp8"])
+                              "dbrx-fp8", "mixtral-mxfp4"])
 def test_fused_handoff_never_times_out(cuda, shape):
     """Single-token fused kernel: every gate/up block incremented its arrival
     counter (64 counters, 256 bytes apart) and no down block's bounded wait
@@ -406,6 +439,8 @@ def test_fused_handoff_never_times_out(cuda, shape):
     a = _fused_args(x, gw, buf, E, h, I, k, out, work)
     if wd == FP8:
         rpw = 4 if (h % 16 == 0 and I % 16 == 0) else 2
+    elif wd == MX4:
+        rpw = 4  # 16-byte aligned buffers
     else:
         rpw = 4 if (h % 8 == 0 and I % 8 == 0 and h * 2 <= 4096) else 2
     group = 8 * (32 // (4 * rpw))
@@ -500,7 +535,7 @@ def test_moelayer(cuda):
 FULL = ["mixtral", "deepseek", "dbrx"]
 
 
-@pytest.mark.parametrize("wd", [F16, FP8, BF16], ids=["f16", "fp8", "bf16"])
+@pytest.mark.parametrize("wd", [F16, FP8, BF16, MX4], ids=["f16", "fp8", "bf16", "mxfp4"])
 @pytest.mark.parametrize("name", FULL)
 @pytest.mark.parametrize("op", ["fused", "naive"])
 def test_full_size_configs(cuda, name, op, wd):

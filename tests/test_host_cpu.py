@@ -205,3 +205,51 @@ def test_synthetic_fp8_layer_is_the_quantized_fp32_layer():
 def test_moelayer_rejects_unknown_weight_dtype():
     with pytest.raises(ValueError, match="weight_dtype"):
         warp_route.MoELayer(4, 32, 32, 2, weight_dtype=torch.int8)
+
+
+def test_mxfp4_quantizer_rules():
+    """Shared exponent floor(log2 max|block|) - 2; round to nearest E2M1 value
+    with ties to the even code; saturation at 6.  One block with max 1.0:
+    scale 2^-2, so the values below are x4 on the E2M1 grid."""
+    v = torch.zeros(1, 32)
+    vals = [1.0, 0.0625, 0.1875, 0.3125, 0.4375, 0.625, 0.875, 1.25, -0.3125, 0.999]
+    #  /0.25:  4,   0.25,   0.75,   1.25,   1.75,   2.5,   3.5,   5,    -1.25,  3.996
+    # codes:   6(4)  0(0)   2(1)    2(1)    4(2)    4(2)   6(4)   6(4)  10(-1)  6(4)
+    v[0, :len(vals)] = torch.tensor(vals)
+    q, s = F.quantize_mxfp4(v)
+    assert s.tolist() == [[127 - 2]]
+    codes = torch.stack([q[0] & 15, q[0] >> 4], dim=1).reshape(-1)[:len(vals)].tolist()
+    assert codes == [6, 0, 2, 2, 4, 4, 6, 6, 10, 6]
+    # saturation: max 7.9 -> exponent floor(log2 7.9) - 2 = 0, 7.9 -> 6
+    q, s = F.quantize_mxfp4(torch.full((1, 32), 7.9))
+    assert s.item() == 127 and (q == 0x77).all()
+    # an all-zero block: scale byte 0, codes 0
+    q, s = F.quantize_mxfp4(torch.zeros(2, 64))
+    assert (s == 0).all() and (q == 0).all()
+    with pytest.raises(ValueError, match="multiple of 32"):
+        F.quantize_mxfp4(torch.zeros(2, 48))
+
+
+def test_mxfp4_packer_error_bound():
+    """_pack_expert_weights(float4_e2m1fn_x2), decoded by the oracle: every
+    element is within half an E2M1 step of w / scale (0.25 below 2, 0.5 below
+    4, 1 up to 6) or saturated at 6, in units of its block's scale, which is
+    2^(floor(log2 max|block|) - 2)."""
+    E, h, I = 2, 64, 96
+    g = torch.Generator().manual_seed(2)
+    mats = [[torch.randn(s, generator=g) * 0.05 for s in ((I, h), (I, h), (h, I))]
+            for _ in range(E)]
+    buf = F._pack_expert_weights([m[0] for m in mats], [m[1] for m in mats],
+                                 [m[2] for m in mats], E, h, I, dtype=torch.float4_e2m1fn_x2)
+    raw = buf.view(torch.uint8).numpy()
+    for e in range(E):
+        for w, d in zip(mats[e], O.expert_matrices(raw, e, E, h, I, "mxfp4")):
+            w = w.double().numpy()
+            rows, cols = w.shape
+            blk = np.abs(w).reshape(rows, cols // 32, 32).max(axis=2)
+            scale = np.exp2(np.floor(np.log2(blk)) - 2)
+            sc = np.repeat(scale, 32, axis=1)
+            a = np.abs(w) / sc
+            half = np.where(a < 2, 0.25, np.where(a < 4, 0.5, 1.0))
+            bound = np.maximum(half, a - 6.0) * sc * (1 + 1e-9)
+            assert np.all(np.abs(d - w) <= bound)

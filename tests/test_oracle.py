@@ -333,3 +333,46 @@ def test_expert_matrices_agree_with_expert_views(fmt, np_dt):
         b = O.expert_views(buf, e, E, h, I)
         for x, y in zip(a, b):
             np.testing.assert_array_equal(x, y.astype(np.float64))
+
+
+def test_decode_e2m1_table():
+    """The OCP FP4 E2M1 value table, written out: codes 0-7 are 0, 0.5, 1,
+    1.5, 2, 3, 4, 6 and codes 8-15 their negatives."""
+    want = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
+    got = O.decode_e2m1(np.arange(16))
+    np.testing.assert_array_equal(got, want)
+    assert np.signbit(got[8])
+
+
+def test_decode_e8m0_matches_torch_for_every_code():
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e8m0fnu).to(torch.float64).numpy()
+    got = O.decode_e8m0(codes)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(got)
+    np.testing.assert_array_equal(got[ok], want[ok])
+    assert O.decode_e8m0(np.array([127, 0, 254], np.uint8)).tolist() == [1.0, 2.0 ** -127, 2.0 ** 127]
+
+
+def test_mxfp4_expert_matrices_hand_computed():
+    """E=1, h=32, I=32 (one block per row).  Gate row 0: codes 1 (0.5) and 15
+    (-6) in its first byte (element 0 in the low nibble), scale byte 129 (x4);
+    down row 31: element 31 code 7 (6), scale 120 (2^-7).  Everything else is
+    code 0 with scale 127."""
+    lo = O.weight_layout(1, 32, 32, "mxfp4")
+    assert (lo["up_proj_offset"], lo["down_proj_offset"], lo["scale_offset"],
+            lo["expert_stride"]) == (512, 1024, 1536, 1664)
+    raw = np.zeros(lo["expert_stride"], np.uint8)
+    raw[lo["scale_offset"]:lo["scale_offset"] + 96] = 127
+    raw[0] = 0xF1                                    # gate[0][0] = 0.5, gate[0][1] = -6
+    raw[lo["scale_offset"] + 0] = 129               # gate row 0 scale 4
+    raw[lo["down_proj_offset"] + 31 * 16 + 15] = 0x70  # down[31][31] = 6 (high nibble)
+    raw[lo["scale_offset"] + 64 + 31] = 120         # down row 31 scale 2^-7
+    g, u, d = O.expert_matrices(raw, 0, 1, 32, 32, "mxfp4")
+    want_g = np.zeros((32, 32))
+    want_g[0, 0], want_g[0, 1] = 2.0, -24.0
+    want_d = np.zeros((32, 32))
+    want_d[31, 31] = 6.0 * 2.0 ** -7
+    np.testing.assert_array_equal(g, want_g)
+    np.testing.assert_array_equal(u, np.zeros((32, 32)))
+    np.testing.assert_array_equal(d, want_d)

@@ -8,9 +8,11 @@
 //   topk_ids=None      optional int32 [k] / [B,k] output of selected experts
 //   topk_weights=None  optional fp32 [k] / [B,k] output of their weights
 // Differences from the reference, all compatible with its call forms:
-//   * weight_buf may be float32 (the reference layout), float16, bfloat16 or
-//     float8_e4m3fn (codes plus fp32 scales, wr_layout_dtype); hidden may be
-//     float32 or float16 and the output takes its dtype; gate_w is float32.
+//   * weight_buf may be float32 (the reference layout), float16, bfloat16,
+//     float8_e4m3fn (codes plus fp32 row scales) or float4_e2m1fn_x2 (MXFP4
+//     codes plus E8M0 block scales), laid out as wr_layout_dtype says; hidden
+//     may be float32 or float16 and the output takes its dtype; gate_w is
+//     float32.
 //   * top_k may be 1..min(6, num_experts) on every op (the reference's fused
 //     and batched ops accepted only 1 or 2, src/bindings.cpp:75,117).
 //   * work is enqueued on the current HIP stream of hidden's device and the
@@ -46,8 +48,11 @@ int weight_dtype_tag(const torch::Tensor& t) {
     case torch::kFloat16: return WR_F16;
     case torch::kBFloat16: return WR_BF16;
     case torch::kFloat8_e4m3fn: return WR_FP8_E4M3;
+    case torch::kFloat4_e2m1fn_x2: return WR_MXFP4;
     default:
-      TORCH_CHECK(false, "weight_buf must be float32, float16, bfloat16 or float8_e4m3fn, got ",
+      TORCH_CHECK(false,
+                  "weight_buf must be float32, float16, bfloat16, float8_e4m3fn or "
+                  "float4_e2m1fn_x2, got ",
                   t.scalar_type());
   }
   return -1;
@@ -74,6 +79,9 @@ void check_common(const torch::Tensor& gate_w, const torch::Tensor& weight_buf, 
   TORCH_CHECK(top_k >= 1 && top_k <= WR_MAX_TOPK && top_k <= num_experts,
               "top_k must be in [1, min(", WR_MAX_TOPK, ", num_experts)], got ", top_k);
   const int64_t es = weight_buf.element_size();
+  TORCH_CHECK(wdt != WR_MXFP4 || (hidden_dim % 32 == 0 && intermediate_dim % 32 == 0),
+              "MXFP4 weights need hidden_dim and intermediate_dim to be multiples of 32, got ",
+              hidden_dim, " and ", intermediate_dim);
   const int64_t need = wr_weight_bytes(num_experts, hidden_dim, intermediate_dim, wdt);
   TORCH_CHECK(weight_buf.numel() * es >= need, "weight_buf too small: need ", need,
               " bytes, got ", weight_buf.numel() * es);

@@ -38,7 +38,9 @@ int check_dims(int E, int h, int I, int k) {
 
 bool act_dtype_ok(int d) { return d == WR_F32 || d == WR_F16; }
 
-// Bytes per matrix element of a weight dtype, 0 if unknown.
+bool weight_dtype_ok(int d) { return d >= WR_F32 && d <= WR_MXFP4; }
+
+// Bytes per matrix element of a weight dtype (0 for MXFP4: half a byte).
 int weight_es(int d) {
   switch (d) {
     case WR_F32: return 4;
@@ -56,6 +58,14 @@ wr_layout_info layout_of(int64_t E, int64_t h, int64_t I, int wdt) {
   o.elem_bytes = weight_es(wdt);
   o.gate_proj_offset = 0;
   o.scale_offset = -1;
+  if (wdt == WR_MXFP4) {
+    o.up_proj_offset = I * h / 2;
+    o.down_proj_offset = I * h;
+    o.scale_offset = (3 * I * h / 2 + 15) / 16 * 16;
+    const int64_t raw = o.scale_offset + 3 * I * h / 32;
+    o.expert_stride = (raw + WR_EXPERT_ALIGN - 1) / WR_EXPERT_ALIGN * WR_EXPERT_ALIGN;
+    return o;
+  }
   if (wdt != WR_FP8_E4M3) {
     o.expert_stride = stride_bytes(E, h, I, o.elem_bytes, &o.up_proj_offset, &o.down_proj_offset);
     return o;
@@ -89,6 +99,11 @@ size_t ws_bytes(int kind, int E, int h, int I, int k, int B) {
 // 16-byte aligned weight and activation pointers); anything else takes the
 // scalar path.
 int choose_vec(const wr_moe_args* a) {
+  if (a->weight_dtype == WR_MXFP4) {  // h, I multiples of 32: 32 elements per 16 bytes, else 2
+    const bool al = reinterpret_cast<uintptr_t>(a->weight_buf) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(a->x) % 16 == 0;
+    return al ? 32 : 2;
+  }
   const int v = 16 / weight_es(a->weight_dtype);
   if (a->hidden_dim % v != 0 || a->intermediate_dim % v != 0) return 1;
   if (reinterpret_cast<uintptr_t>(a->weight_buf) % 16 != 0) return 1;
@@ -101,7 +116,10 @@ int validate(const wr_moe_args* a, int kind, Problem* p) {
   if (a == nullptr) return WR_EINVAL_NULL;
   int st = check_dims(a->num_experts, a->hidden_dim, a->intermediate_dim, a->top_k);
   if (st != WR_OK) return st;
-  if (weight_es(a->weight_dtype) == 0 || !act_dtype_ok(a->act_dtype)) return WR_EINVAL_DTYPE;
+  if (!weight_dtype_ok(a->weight_dtype) || !act_dtype_ok(a->act_dtype)) return WR_EINVAL_DTYPE;
+  if (a->weight_dtype == WR_MXFP4 && kind >= 0 &&
+      (a->hidden_dim % 32 != 0 || a->intermediate_dim % 32 != 0))
+    return WR_EINVAL_BLOCK;
   const bool single = kind == WR_KIND_FUSED || kind == WR_KIND_NAIVE;
   if (single ? a->batch_size != 1 : a->batch_size < 0) return WR_EINVAL_BATCH;
   if (a->batch_size == 0) {
@@ -158,11 +176,14 @@ WR_API const char* wr_status_str(int status) {
     case WR_EINVAL_TOPK: return "top_k must be in [1, min(6, num_experts)]";
     case WR_EINVAL_EXPERTS: return "num_experts exceeds WR_MAX_EXPERTS (64)";
     case WR_EINVAL_DTYPE:
-      return "unsupported dtype (weights: fp32, fp16, bf16 or fp8 e4m3; activations: fp32 or fp16)";
+      return "unsupported dtype (weights: fp32, fp16, bf16, fp8 e4m3 or mxfp4; activations: fp32 or "
+             "fp16)";
     case WR_EINVAL_WEIGHT_SIZE: return "weight_buf is smaller than the packed expert layout";
     case WR_EINVAL_WORKSPACE: return "workspace is NULL or smaller than wr_workspace_bytes()";
     case WR_EINVAL_BATCH: return "invalid batch_size";
     case WR_EINVAL_KIND: return "unknown workspace kind";
+    case WR_EINVAL_BLOCK:
+      return "MXFP4 weights need hidden_dim and intermediate_dim to be multiples of 32";
     case WR_EHIP: return "HIP runtime error";
     default: return "unknown status";
   }
@@ -192,7 +213,9 @@ WR_API int wr_layout_dtype(int num_experts, int hidden_dim, int intermediate_dim
                            int weight_dtype, wr_layout_info* out) {
   if (out == nullptr) return WR_EINVAL_NULL;
   if (num_experts < 1 || hidden_dim < 1 || intermediate_dim < 1) return WR_EINVAL_SHAPE;
-  if (weight_es(weight_dtype) == 0) return WR_EINVAL_DTYPE;
+  if (!weight_dtype_ok(weight_dtype)) return WR_EINVAL_DTYPE;
+  if (weight_dtype == WR_MXFP4 && (hidden_dim % 32 != 0 || intermediate_dim % 32 != 0))
+    return WR_EINVAL_BLOCK;
   *out = layout_of(num_experts, hidden_dim, intermediate_dim, weight_dtype);
   return WR_OK;
 }

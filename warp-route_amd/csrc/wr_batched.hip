@@ -270,33 +270,47 @@ struct WTile {
 
 template <typename WT>
 struct WGeo {
-  static constexpr int kLaneRow = 16 * (int)sizeof(WT) / 2;  // lanes per row: 16 (fp16), 8 (fp8)
-  static constexpr int kRowsPer = kWave / kLaneRow;            // rows per instruction: 4, 8
-  static constexpr int kElems = 16 / (int)sizeof(WT);          // elements per lane: 8, 16
+  static constexpr int kElems = 16 / (int)sizeof(WT) * epu<WT>();  // per lane: 8, 16, 32 (mxfp4)
+  static constexpr int kLaneRow = kBK / kElems;                     // lanes per row: 16, 8, 4
+  static constexpr int kRowsPer = kWave / kLaneRow;                 // rows per instruction: 4, 8, 16
 };
 
 // This lane's address of row group 0 at column 0 of the K loop, for the tile
-// whose first row is `row` of a matrix with row length ld.
+// whose first row is `row` of a matrix with row length ld (elements).
 template <typename WT>
 __device__ __forceinline__ const WT* w_lane_base(const WT* mat, int row, int64_t ld, int lane) {
-  return mat + (int64_t)(row + lane / WGeo<WT>::kLaneRow) * ld +
-         (lane % WGeo<WT>::kLaneRow) * WGeo<WT>::kElems;
+  return mat + eoff<WT>((int64_t)(row + lane / WGeo<WT>::kLaneRow) * ld +
+                        (lane % WGeo<WT>::kLaneRow) * WGeo<WT>::kElems);
+}
+
+// MXFP4: this lane's E8M0 byte of the same block at column 0 of the K loop,
+// for a matrix whose block scales start at sc ([rows][ld / 32] bytes).
+template <typename WT>
+__device__ __forceinline__ const uint8_t* w_lane_scale(const uint8_t* sc, int row, int64_t ld,
+                                                       int lane) {
+  return sc + (int64_t)(row + lane / WGeo<WT>::kLaneRow) * (ld / 32) +
+         (lane % WGeo<WT>::kLaneRow) * WGeo<WT>::kElems / 32;
 }
 
 template <typename WT, int ROWS>
 struct WRegs {
   static constexpr int N = ROWS / WGeo<WT>::kRowsPer;  // load instructions per K step
   u32x4 v[N];
+  float s[std::is_same<WT, fp4x2>::value ? N : 1];     // MXFP4 block scales
 };
 
 // Loads of one K step: base[i] is this lane's address for row group i at
-// column 0 of the K loop; kb is the step's first column.
+// column 0 of the K loop (sc[i] its MXFP4 scale byte); kb is the step's
+// first column.
 template <typename WT, int ROWS>
 __device__ __forceinline__ void w_load(WRegs<WT, ROWS>& r,
-                                       const WT* const (&base)[WRegs<WT, ROWS>::N], int kb) {
+                                       const WT* const (&base)[WRegs<WT, ROWS>::N],
+                                       const uint8_t* const (&sc)[WRegs<WT, ROWS>::N], int kb) {
 #pragma unroll
-  for (int i = 0; i < WRegs<WT, ROWS>::N; ++i)
-    r.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base[i] + kb));
+  for (int i = 0; i < WRegs<WT, ROWS>::N; ++i) {
+    r.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base[i] + eoff<WT>(kb)));
+    if constexpr (std::is_same<WT, fp4x2>::value) r.s[i] = e8m0_value(sc[i][kb / 32]);
+  }
 }
 
 __device__ __forceinline__ H8 fp8x8_to_h8(uint32_t a, uint32_t b) {
@@ -308,13 +322,29 @@ __device__ __forceinline__ H8 fp8x8_to_h8(uint32_t a, uint32_t b) {
   return H8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
+// MXFP4: eight codes (one 32-bit word) -> eight fp16 values times the block
+// scale (v_cvt_scalef32_pk_f16_fp4, checked against the E2M1 table; exact
+// while the scaled values are fp16 normals, i.e. scales of 2^-15 and up).
+__device__ __forceinline__ H8 fp4x8_to_h8(uint32_t w, float s) {
+  typedef f16 h2 __attribute__((ext_vector_type(2)));
+  const h2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 0);
+  const h2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 1);
+  const h2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 2);
+  const h2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 3);
+  return H8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
 template <typename WT, int ROWS>
 __device__ __forceinline__ void w_store(WTile<ROWS>& t, const WRegs<WT, ROWS>& r, int lane) {
   constexpr int LR = WGeo<WT>::kLaneRow, RP = WGeo<WT>::kRowsPer;
 #pragma unroll
   for (int i = 0; i < WRegs<WT, ROWS>::N; ++i) {
     const int row = RP * i + lane / LR;
-    if constexpr (std::is_same<WT, fp8w>::value) {
+    if constexpr (std::is_same<WT, fp4x2>::value) {
+      const int c = 4 * (lane % LR);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) t.w[row][c + p] = fp4x8_to_h8(r.v[i][p], r.s[i]);
+    } else if constexpr (std::is_same<WT, fp8w>::value) {
       const int c = 2 * (lane % LR);
       t.w[row][c] = fp8x8_to_h8(r.v[i][0], r.v[i][1]);
       t.w[row][c + 1] = fp8x8_to_h8(r.v[i][2], r.v[i][3]);
@@ -333,6 +363,7 @@ __device__ __forceinline__ void w_store(WTile<ROWS>& t, const WRegs<WT, ROWS>& r
 template <typename WT, bool LO, int NT>
 __device__ __forceinline__ void gu_pass(TokTile& xs, WTile<32>& wt,
                                         const WT* const (&wbase)[WRegs<WT, 32>::N],
+                                        const uint8_t* const (&wsc)[WRegs<WT, 32>::N],
                                         const f16* __restrict__ x_hi,
                                         const f16* __restrict__ x_lo, const BatchRoute& r,
                                         int p0, int mt, float* __restrict__ act, int row0,
@@ -348,7 +379,7 @@ __device__ __forceinline__ void gu_pass(TokTile& xs, WTile<32>& wt,
   // issued before step s's MFMAs.
   WRegs<WT, 32> wr;
   H8 th[kTilePieces], tl[kTilePieces];
-  w_load<WT, 32>(wr, wbase, 0);
+  w_load<WT, 32>(wr, wbase, wsc, 0);
   gu_tile_load(th, tl, x_hi, x_lo, off, 0, LO);
   for (int s = 0; s < ns; ++s) {
     __syncthreads();  // every wave is done reading the previous tiles
@@ -356,7 +387,7 @@ __device__ __forceinline__ void gu_pass(TokTile& xs, WTile<32>& wt,
     w_store<WT, 32>(wt, wr, lane);
     __syncthreads();
     if (s + 1 < ns) {
-      w_load<WT, 32>(wr, wbase, (s + 1) * kBK);
+      w_load<WT, 32>(wr, wbase, wsc, (s + 1) * kBK);
       gu_tile_load(th, tl, x_hi, x_lo, off, (s + 1) * kBK, LO);
     }
 #pragma unroll
@@ -426,9 +457,15 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
   // Tile rows 0-15: gate rows row0 ..; rows 16-31: the same up rows.
   constexpr int N = WRegs<WT, 32>::N, RP = WGeo<WT>::kRowsPer;
   const WT* wbase[N];
+  const uint8_t* wsc[N];
+  // MXFP4 block scales: gate [I][h/32], then up [I][h/32]
+  const uint8_t* mxs = reinterpret_cast<const uint8_t*>(blk) + g.off_scale;
 #pragma unroll
-  for (int i = 0; i < N; ++i)
-    wbase[i] = G + (i < N / 2 ? 0 : g.off_up) + (int64_t)(RP * (i % (N / 2))) * g.h;
+  for (int i = 0; i < N; ++i) {
+    wbase[i] = G + (i < N / 2 ? 0 : g.off_up) + eoff<WT>((int64_t)(RP * (i % (N / 2))) * g.h);
+    wsc[i] = w_lane_scale<WT>(mxs + (i < N / 2 ? 0 : (int64_t)g.I * g.h / 32), row0, g.h, lane) +
+             (int64_t)(RP * (i % (N / 2))) * (g.h / 32);
+  }
   const float* sc = nullptr;
   if constexpr (std::is_same<WT, fp8w>::value) sc = wscales(blk, g.off_scale);
   WTile<32>& wt = wts[wave];
@@ -436,10 +473,10 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
     const int mt = min(kMaxTok, M - m0);
     const int p0 = pbeg + m0;
     switch ((mt + 15) / 16) {
-      case 1: gu_pass<WT, LO, 1>(xs, wt, wbase, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
-      case 2: gu_pass<WT, LO, 2>(xs, wt, wbase, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
-      case 3: gu_pass<WT, LO, 3>(xs, wt, wbase, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
-      default: gu_pass<WT, LO, 4>(xs, wt, wbase, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
+      case 1: gu_pass<WT, LO, 1>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
+      case 2: gu_pass<WT, LO, 2>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
+      case 3: gu_pass<WT, LO, 3>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
+      default: gu_pass<WT, LO, 4>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
     }
   }
 }
@@ -451,6 +488,7 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
 template <typename WT, int NT>
 __device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt,
                                         const WT* const (&wbase)[WRegs<WT, 16>::N],
+                                        const uint8_t* const (&wsc)[WRegs<WT, 16>::N],
                                         const float* __restrict__ act, int p0, int mt, int sb,
                                         int se, float* __restrict__ y, int row0,
                                         const float* __restrict__ sdown, const Geom& g,
@@ -463,7 +501,7 @@ __device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt,
     tile_rows(off, nullptr, p0, mt, g.I);
     WRegs<WT, 16> wr;
     H8 th[kTilePieces], tl[kTilePieces];
-    w_load<WT, 16>(wr, wbase, sb * kBK);
+    w_load<WT, 16>(wr, wbase, wsc, sb * kBK);
     dn_tile_load<bf16_ops<WT>()>(th, tl, act, off, sb * kBK);
     for (int s = sb; s < se; ++s) {
       __syncthreads();
@@ -471,7 +509,7 @@ __device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt,
       w_store<WT, 16>(wt, wr, lane);
       __syncthreads();
       if (s + 1 < se) {
-        w_load<WT, 16>(wr, wbase, (s + 1) * kBK);
+        w_load<WT, 16>(wr, wbase, wsc, (s + 1) * kBK);
         dn_tile_load<bf16_ops<WT>()>(th, tl, act, off, (s + 1) * kBK);
       }
 #pragma unroll
@@ -528,17 +566,25 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, B
   if constexpr (std::is_same<WT, fp8w>::value) sdown = wscales(blk, g.off_scale) + 2 * g.I;
   constexpr int N = WRegs<WT, 16>::N;
   const WT* wbase[N];
+  const uint8_t* wsc[N];
+  // MXFP4 down block scales [h][I/32], after the gate and up scales
+  const uint8_t* mxs =
+      reinterpret_cast<const uint8_t*>(blk) + g.off_scale + 2 * ((int64_t)g.I * g.h / 32);
 #pragma unroll
-  for (int i = 0; i < N; ++i) wbase[i] = D + (int64_t)(WGeo<WT>::kRowsPer * i) * g.I;
+  for (int i = 0; i < N; ++i) {
+    wbase[i] = D + eoff<WT>((int64_t)(WGeo<WT>::kRowsPer * i) * g.I);
+    wsc[i] = w_lane_scale<WT>(mxs, row0, g.I, lane) +
+             (int64_t)(WGeo<WT>::kRowsPer * i) * (g.I / 32);
+  }
   float* y = ypart + (int64_t)ks * P * g.h;
   WTile<16>& wt = wts[wave];
   for (int m0 = 0; m0 < M; m0 += kMaxTok) {
     const int mt = min(kMaxTok, M - m0);
     switch ((mt + 15) / 16) {
-      case 1: dn_pass<WT, 1>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-      case 2: dn_pass<WT, 2>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-      case 3: dn_pass<WT, 3>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-      default: dn_pass<WT, 4>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+      case 1: dn_pass<WT, 1>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+      case 2: dn_pass<WT, 2>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+      case 3: dn_pass<WT, 3>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+      default: dn_pass<WT, 4>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
     }
   }
 }
@@ -561,7 +607,7 @@ __global__ __launch_bounds__(kBlk) void k_combine(const float* __restrict__ ypar
 
 template <typename WT, typename XT>
 hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
-  constexpr int64_t es = sizeof(WT);
+  constexpr int64_t es = sizeof(WT);  // bytes per storage unit (two MXFP4 codes per byte)
   Geom g;
   g.E = p.E;
   g.h = p.h;
@@ -598,7 +644,7 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
 
 bool grouped_ok(const Problem& p) {
   const bool wt = ((p.wdt == WR_F16 || p.wdt == WR_BF16) && p.vec == 8) ||
-                  (p.wdt == WR_FP8_E4M3 && p.vec == 16);
+                  (p.wdt == WR_FP8_E4M3 && p.vec == 16) || (p.wdt == WR_MXFP4 && p.vec == 32);
   return p.B > 1 && wt && p.h % kBK == 0 && p.I % kBK == 0;
 }
 
@@ -610,6 +656,8 @@ hipError_t launch_grouped(const Problem& p, hipStream_t s) {
     return p.adt == WR_F16 ? grouped_t<fp8w, f16>(p, w, s) : grouped_t<fp8w, float>(p, w, s);
   if (p.wdt == WR_BF16)
     return p.adt == WR_F16 ? grouped_t<bf16w, f16>(p, w, s) : grouped_t<bf16w, float>(p, w, s);
+  if (p.wdt == WR_MXFP4)
+    return p.adt == WR_F16 ? grouped_t<fp4x2, f16>(p, w, s) : grouped_t<fp4x2, float>(p, w, s);
   return p.adt == WR_F16 ? grouped_t<f16, f16>(p, w, s) : grouped_t<f16, float>(p, w, s);
 }
 

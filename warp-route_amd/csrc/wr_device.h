@@ -30,7 +30,42 @@ struct bf16w {
 struct fp8w {
   uint8_t bits;
 };
-static_assert(sizeof(bf16w) == 2 && sizeof(fp8w) == 1, "weight tags must be packed");
+// MXFP4: two E2M1 codes per byte (element 2i in bits 0-3), one E8M0 scale
+// per 32 elements of a row, stored apart from the codes.
+struct fp4x2 {
+  uint8_t bits;
+};
+static_assert(sizeof(bf16w) == 2 && sizeof(fp8w) == 1 && sizeof(fp4x2) == 1,
+              "weight tags must be packed");
+
+// Matrix elements per storage unit of WT (two for MXFP4, else one); element
+// offsets within a matrix become unit offsets with eoff.
+template <typename WT>
+constexpr int epu() {
+  return std::is_same<WT, fp4x2>::value ? 2 : 1;
+}
+template <typename WT>
+__host__ __device__ constexpr int64_t eoff(int64_t elems) {
+  return elems / epu<WT>();
+}
+
+// A loaded MXFP4 vector: its codes and the fp32 value of its block scale.
+// Vectors never straddle a 32-element block (32 elements per 16 bytes, or
+// 2 per byte on the unaligned path).
+struct fp4v32 {
+  u32x4 q;
+  float s;
+};
+struct fp4v2 {
+  uint8_t q;
+  float s;
+};
+
+// E8M0 scale byte -> 2^(e - 127) as fp32 (e = 0 is the subnormal 2^-127;
+// 255, NaN in the format, is never written by the packer).
+__device__ __forceinline__ float e8m0_value(uint32_t e) {
+  return e == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(e << 23);
+}
 
 // Shape and layout of one MoE problem, passed to kernels by value.  Offsets
 // and the expert stride are in elements of the weight type: the stride is a
@@ -244,17 +279,44 @@ template <>
 struct WVec<fp8w, 16> { typedef u32x4 type; };
 template <>
 struct WVec<fp8w, 1> { typedef uint8_t type; };
+template <>
+struct WVec<fp4x2, 32> { typedef fp4v32 type; };
+template <>
+struct WVec<fp4x2, 2> { typedef fp4v2 type; };
 
 // Natural vector width of a weight type: elements per 128-bit access.
 template <typename WT>
 constexpr int wvec_width() {
-  return 16 / (int)sizeof(WT);
+  return 16 / (int)sizeof(WT) * epu<WT>();
+}
+// Elements per access on the unaligned path.
+template <typename WT>
+constexpr int wvec_scalar() {
+  return epu<WT>();
 }
 
 // Streaming weight load: read once per call, so mark it non-temporal.
 template <typename T, int VEC>
 __device__ __forceinline__ typename WVec<T, VEC>::type load_w(const T* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const typename WVec<T, VEC>::type*>(p));
+}
+
+// Weight load with its block scale: for MXFP4, `sc` is the E8M0 byte of the
+// block holding the first element; other types ignore it.
+template <typename T, int VEC>
+__device__ __forceinline__ typename WVec<T, VEC>::type load_wq(const T* p, const uint8_t* sc) {
+  if constexpr (std::is_same<T, fp4x2>::value) {
+    typename WVec<T, VEC>::type v;
+    if constexpr (VEC == 32)
+      v.q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    else
+      v.q = __builtin_nontemporal_load(reinterpret_cast<const uint8_t*>(p));
+    v.s = e8m0_value(*sc);
+    return v;
+  } else {
+    (void)sc;
+    return load_w<T, VEC>(p);
+  }
 }
 
 template <typename V>
@@ -272,7 +334,23 @@ __device__ __forceinline__ float velem(const V& v, int i) {
 // converts two bytes per instruction (the pair is shared by i and i ^ 1).
 template <typename WT, typename V>
 __device__ __forceinline__ float wdec(const V& v, int i) {
-  if constexpr (std::is_same<WT, bf16w>::value) {
+  if constexpr (std::is_same<WT, fp4x2>::value) {
+    // v_cvt_scalef32_pk_f32_fp4: the two codes of one byte, times the scale
+    // (checked against the E2M1 table for every byte on gfx950).
+    if constexpr (std::is_same<V, fp4v2>::value) {
+      return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((uint32_t)v.q, v.s, 0)[i & 1];
+    } else {
+      const uint32_t w = v.q[i >> 3];
+      f32x2 pr;
+      switch ((i >> 1) & 3) {
+        case 0: pr = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, v.s, 0); break;
+        case 1: pr = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, v.s, 1); break;
+        case 2: pr = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, v.s, 2); break;
+        default: pr = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, v.s, 3); break;
+      }
+      return pr[i & 1];
+    }
+  } else if constexpr (std::is_same<WT, bf16w>::value) {
     if constexpr (std::is_same<V, uint16_t>::value) {
       return __uint_as_float((uint32_t)v << 16);
     } else {
@@ -302,8 +380,12 @@ __device__ __forceinline__ const float* wscales(const WT* blk, int64_t off_scale
 
 template <typename V>
 __device__ __forceinline__ V vzero() {
-  if constexpr (std::is_same<V, f16>::value || std::is_same<V, float>::value ||
-                std::is_integral<V>::value) {
+  if constexpr (std::is_same<V, fp4v32>::value) {
+    return fp4v32{u32x4{0u, 0u, 0u, 0u}, 1.0f};
+  } else if constexpr (std::is_same<V, fp4v2>::value) {
+    return fp4v2{0, 1.0f};
+  } else if constexpr (std::is_same<V, f16>::value || std::is_same<V, float>::value ||
+                       std::is_integral<V>::value) {
     return V(0);
   } else {
     V z;

@@ -65,6 +65,16 @@
 #ifndef WR_F8_U2
 #define WR_F8_U2 2   // column chunks per down tile
 #endif
+// MXFP4 weights in the single-token fused kernel (32 weights per 128-bit load)
+#ifndef WR_F4_U1
+#define WR_F4_U1 1   // gate/up column chunks per row per iteration (4 rows per wave)
+#endif
+#ifndef WR_F4_RPD
+#define WR_F4_RPD 8  // output rows per down block
+#endif
+#ifndef WR_F4_U2
+#define WR_F4_U2 1   // column chunks per down tile
+#endif
 
 namespace wr {
 
@@ -191,6 +201,28 @@ __global__ __launch_bounds__(1024) void k_gate_topk(const float* __restrict__ ga
   }
 }
 
+// MXFP4: the block-scale bytes of row r of matrix m (0 gate, 1 up, 2 down)
+// of the expert block at blk ([I][h/32], [I][h/32], [h][I/32] after the
+// codes); the scale of element c of the row is at [c / 32].  nullptr for the
+// other types.
+template <typename WT>
+__device__ __forceinline__ const uint8_t* mx_row(const WT* blk, const Geom& g, int m, int64_t r) {
+  if constexpr (std::is_same<WT, fp4x2>::value) {
+    const int64_t per = (int64_t)g.I * g.h / 32;
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(blk) + g.off_scale + m * per;
+    return base + r * ((m == 2 ? g.I : g.h) / 32);
+  } else {
+    (void)blk; (void)g; (void)m; (void)r;
+    return nullptr;
+  }
+}
+
+template <typename WT>
+__device__ __forceinline__ const uint8_t* mx_at(const uint8_t* row, int64_t c) {
+  if constexpr (std::is_same<WT, fp4x2>::value) return row + c / 32;
+  else return nullptr;
+}
+
 // act for intermediate index r of the expert block at blk, from the gate and
 // up dot products gs and us and the gate weight wk:
 //   wk * silu(gs) * us                                  (unscaled types)
@@ -253,7 +285,8 @@ __global__ __launch_bounds__(kBlock) void k_gateup(const WT* __restrict__ wbuf,
     const int kk = it / items;
     const int r0 = (it - kk * items) * RPW;
     const int e = topk_id(t, kk);
-    const WT* G = wbuf + (int64_t)e * g.stride + (int64_t)r0 * g.h;
+    const WT* blk = wbuf + (int64_t)e * g.stride;
+    const WT* G = blk + eoff<WT>((int64_t)r0 * g.h);
     const WT* Up = G + g.off_up;
     const int nrows = min(RPW, g.I - r0);
 
@@ -271,8 +304,12 @@ __global__ __launch_bounds__(kBlock) void k_gateup(const WT* __restrict__ wbuf,
 #pragma unroll
         for (int j = 0; j < RPW; ++j) {
           const bool okj = ok && j < nrows;
-          wg[u][j] = okj ? load_w<WT, VEC>(G + (int64_t)j * g.h + c) : vzero<V>();
-          wu[u][j] = okj ? load_w<WT, VEC>(Up + (int64_t)j * g.h + c) : vzero<V>();
+          wg[u][j] = okj ? load_wq<WT, VEC>(G + eoff<WT>((int64_t)j * g.h + c),
+                                            mx_at<WT>(mx_row(blk, g, 0, r0 + j), c))
+                         : vzero<V>();
+          wu[u][j] = okj ? load_wq<WT, VEC>(Up + eoff<WT>((int64_t)j * g.h + c),
+                                            mx_at<WT>(mx_row(blk, g, 1, r0 + j), c))
+                         : vzero<V>();
         }
         if (ok) {
           load_x<XT, VEC>(xb + c, xv[u]);
@@ -336,7 +373,8 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 
     constexpr bool kFp8 = std::is_same<WT, fp8w>::value;
     for (int kk = 0; kk < g.k; ++kk) {
-      const WT* D = wbuf + (int64_t)topk_id(t, kk) * g.stride + g.off_down + (int64_t)r0 * g.I;
+      const WT* blk = wbuf + (int64_t)topk_id(t, kk) * g.stride;
+      const WT* D = blk + g.off_down + eoff<WT>((int64_t)r0 * g.I);
       const float* a = ab + (int64_t)kk * g.I;
       // fp8: this expert's rows accumulate apart and are scaled per row below.
       float ek[RPD];
@@ -352,7 +390,10 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
           const bool ok = c < g.I;
 #pragma unroll
           for (int j = 0; j < RPD; ++j)
-            wv[u][j] = (ok && j < nrows) ? load_w<WT, VEC>(D + (int64_t)j * g.I + c) : vzero<V>();
+            wv[u][j] = (ok && j < nrows)
+                           ? load_wq<WT, VEC>(D + eoff<WT>((int64_t)j * g.I + c),
+                                              mx_at<WT>(mx_row(blk, g, 2, r0 + j), c))
+                           : vzero<V>();
           if (ok) {
             load_x<float, VEC>(a + c, av[u]);
           } else {
@@ -453,7 +494,8 @@ __device__ __forceinline__ void gateup_item(const WT* __restrict__ wbuf, const X
                                             int r0, int lane) {
   typedef typename WVec<WT, VEC>::type V;
   constexpr int CH = kWave * VEC;
-  const WT* G = wbuf + (int64_t)topk_id(t, kk) * g.stride + (int64_t)r0 * g.h;
+  const WT* blk = wbuf + (int64_t)topk_id(t, kk) * g.stride;
+  const WT* G = blk + eoff<WT>((int64_t)r0 * g.h);
   const WT* Up = G + g.off_up;
   const int nrows = min(RPW, g.I - r0);
   float ag[RPW], au[RPW];
@@ -469,8 +511,12 @@ __device__ __forceinline__ void gateup_item(const WT* __restrict__ wbuf, const X
 #pragma unroll
       for (int j = 0; j < RPW; ++j) {
         const bool okj = ok && j < nrows;
-        wg[u][j] = okj ? load_w<WT, VEC>(G + (int64_t)j * g.h + c) : vzero<V>();
-        wu[u][j] = okj ? load_w<WT, VEC>(Up + (int64_t)j * g.h + c) : vzero<V>();
+        wg[u][j] = okj ? load_wq<WT, VEC>(G + eoff<WT>((int64_t)j * g.h + c),
+                                          mx_at<WT>(mx_row(blk, g, 0, r0 + j), c))
+                       : vzero<V>();
+        wu[u][j] = okj ? load_wq<WT, VEC>(Up + eoff<WT>((int64_t)j * g.h + c),
+                                          mx_at<WT>(mx_row(blk, g, 1, r0 + j), c))
+                       : vzero<V>();
       }
       if (ok) {
         load_x<XT, VEC>(xb + c, xv[u]);
@@ -490,7 +536,6 @@ __device__ __forceinline__ void gateup_item(const WT* __restrict__ wbuf, const X
         }
   }
   const float wk = topk_w(t, kk);
-  const WT* blk = wbuf + (int64_t)topk_id(t, kk) * g.stride;
 #pragma unroll
   for (int j = 0; j < RPW; ++j) {
     const float gs = wave_sum(ag[j]);
@@ -517,11 +562,13 @@ __device__ __forceinline__ void down_tile_load(typename WVec<WT, VEC>::type (&wv
     const int kk = q / nch;
     const int c = (q - kk * nch) * kWave * VEC + lane * VEC;
     const bool ok = q < C && c < g.I;
-    const WT* D = wbuf + (int64_t)topk_id(t, ok ? kk : 0) * g.stride + g.off_down +
-                  (int64_t)r0 * g.I + c;
+    const WT* blk = wbuf + (int64_t)topk_id(t, ok ? kk : 0) * g.stride;
+    const WT* D = blk + g.off_down + eoff<WT>((int64_t)r0 * g.I + c);
 #pragma unroll
     for (int j = 0; j < RPD; ++j)
-      wv[u][j] = (ok && j < nrows) ? load_w<WT, VEC>(D + (int64_t)j * g.I) : vzero<V>();
+      wv[u][j] = (ok && j < nrows) ? load_wq<WT, VEC>(D + eoff<WT>((int64_t)j * g.I),
+                                                      mx_at<WT>(mx_row(blk, g, 2, r0 + j), c))
+                                   : vzero<V>();
   }
 }
 
@@ -691,8 +738,9 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
 // ---------------------------------------------------------------------------
 namespace {
 
+// Bytes per storage unit of a weight type (an MXFP4 unit is a byte of two codes).
 int64_t weight_es(int wdt) {
-  return wdt == WR_F32 ? 4 : (wdt == WR_FP8_E4M3 ? 1 : 2);
+  return wdt == WR_F32 ? 4 : ((wdt == WR_FP8_E4M3 || wdt == WR_MXFP4) ? 1 : 2);
 }
 
 Geom make_geom(const Problem& p) {
@@ -764,6 +812,7 @@ hipError_t logits_t(const Problem& p, float* logits, unsigned* zero, int nzero, 
 int fused_rpw(const Problem& p) {
   const int64_t row_bytes = (int64_t)p.h * weight_es(p.wdt);
   if (p.wdt == WR_FP8_E4M3) return p.vec > 1 ? WR_F8_RPW : 2;
+  if (p.wdt == WR_MXFP4) return p.vec == 32 ? 4 : 2;
   return (p.vec > 1 && row_bytes <= 4096) ? 4 : 2;
 }
 
@@ -790,9 +839,11 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   hs.spin_limit = 1u << 20;
   // fp8 down blocks take twice the rows and half the chunks in flight: the
   // same weight bytes per tile as fp16, and half the act reads per weight byte.
+  // MXFP4 (32 act values per lane and chunk): 8 rows, one chunk in flight.
   constexpr bool kFp8 = std::is_same<WT, fp8w>::value;
-  constexpr int RPD = kFp8 ? WR_F8_RPD : WR_FU_RPD;
-  constexpr int U2 = kFp8 ? WR_F8_U2 : WR_FU_U;
+  constexpr bool kFp4 = std::is_same<WT, fp4x2>::value;
+  constexpr int RPD = kFp4 ? WR_F4_RPD : (kFp8 ? WR_F8_RPD : WR_FU_RPD);
+  constexpr int U2 = kFp4 ? WR_F4_U2 : (kFp8 ? WR_F8_U2 : WR_FU_U);
   const int n2 = (p.h + RPD - 1) / RPD;
   hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2>),
                      dim3(hs.n1 + n2), dim3(kBlock), 0, s, static_cast<const WT*>(p.wbuf),
@@ -801,18 +852,29 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Column chunks in flight per gate/up row: fp8 WR_F8_U1, MXFP4 one (32 x
+// values per lane and chunk), else WR_GU_U (halved for 4 rows per wave).
+template <typename WT, int RPW>
+constexpr int fused_u1() {
+  if constexpr (std::is_same<WT, fp4x2>::value) return WR_F4_U1;
+  if constexpr (std::is_same<WT, fp8w>::value) return WR_F8_U1;
+  return RPW == 4 ? WR_GU_U / 2 : WR_GU_U;
+}
+
 template <typename WT, typename XT, int VEC>
 hipError_t fused_t(const Problem& p, const FusedWs& w, hipStream_t s) {
-  constexpr bool kFp8 = std::is_same<WT, fp8w>::value;
-  if (fused_rpw(p) == 4) return fused_rpw_t<WT, XT, VEC, 4, kFp8 ? WR_F8_U1 : WR_GU_U / 2>(p, w, s);
-  return fused_rpw_t<WT, XT, VEC, 2, kFp8 ? WR_F8_U1 : WR_GU_U>(p, w, s);
+  if (fused_rpw(p) == 4) return fused_rpw_t<WT, XT, VEC, 4, fused_u1<WT, 4>()>(p, w, s);
+  return fused_rpw_t<WT, XT, VEC, 2, fused_u1<WT, 2>()>(p, w, s);
 }
 
 template <typename WT, typename XT, int VEC>
 hipError_t ffn_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   constexpr int RPW = WR_GU_RPW, RPD = WR_DN_RPD;
-  // fp8: half the chunks in flight (16 fp32 x values per chunk and lane).
-  constexpr int U1 = std::is_same<WT, fp8w>::value ? WR_GU_U / 2 : WR_GU_U;
+  // fp8: half the chunks in flight (16 fp32 x values per chunk and lane);
+  // MXFP4: one chunk (32 values), and one chunk per down tile.
+  constexpr bool kFp4 = std::is_same<WT, fp4x2>::value;
+  constexpr int U1 = kFp4 ? 1 : (std::is_same<WT, fp8w>::value ? WR_GU_U / 2 : WR_GU_U);
+  constexpr int UD = kFp4 ? 1 : WR_DN_U;
   if (p.B == 1) return fused_t<WT, XT, VEC>(p, w, s);
   const Geom g = make_geom(p);
   const WT* wb = static_cast<const WT*>(p.wbuf);
@@ -824,15 +886,15 @@ hipError_t ffn_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   if (err != hipSuccess) return err;
   const int nw2 = waves_for((p.h + RPD - 1) / RPD, p.B);
   const dim3 g2((nw2 + kWavesPerBlock - 1) / kWavesPerBlock, p.B);
-  hipLaunchKernelGGL((k_down<WT, XT, VEC, RPD, WR_DN_U>), g2, dim3(kBlock), 0, s, wb, w.logits,
+  hipLaunchKernelGGL((k_down<WT, XT, VEC, RPD, UD>), g2, dim3(kBlock), 0, s, wb, w.logits,
                      w.act, static_cast<XT*>(p.out), g, nw2);
   return hipGetLastError();
 }
 
 template <typename WT, typename XT>
 hipError_t ffn_w(const Problem& p, const FusedWs& w, hipStream_t s) {
-  constexpr int V = wvec_width<WT>();
-  return p.vec == V ? ffn_t<WT, XT, V>(p, w, s) : ffn_t<WT, XT, 1>(p, w, s);
+  constexpr int V = wvec_width<WT>(), V1 = wvec_scalar<WT>();
+  return p.vec == V ? ffn_t<WT, XT, V>(p, w, s) : ffn_t<WT, XT, V1>(p, w, s);
 }
 
 template <typename XT>
@@ -841,6 +903,7 @@ hipError_t ffn_x(const Problem& p, const FusedWs& w, hipStream_t s) {
     case WR_F16: return ffn_w<f16, XT>(p, w, s);
     case WR_BF16: return ffn_w<bf16w, XT>(p, w, s);
     case WR_FP8_E4M3: return ffn_w<fp8w, XT>(p, w, s);
+    case WR_MXFP4: return ffn_w<fp4x2, XT>(p, w, s);
     default: return ffn_w<float, XT>(p, w, s);
   }
 }

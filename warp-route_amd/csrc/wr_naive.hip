@@ -25,20 +25,23 @@ constexpr int kWpb = kBlock / kWave;
 
 // y[r] = W[r, :] . v (times scale[r] when scale != nullptr: fp8 row scales)
 // for r < rows; one wave per row (src/naive_moe.cu:79-111 computes the same
-// product on one 256-thread block).
+// product on one 256-thread block).  MXFP4: mx holds the matrix's block
+// scales, [rows][cols / 32] bytes.
 template <typename WT, typename VT, int VEC>
 __global__ __launch_bounds__(kBlock) void k_matvec(const WT* __restrict__ W,
                                                    const VT* __restrict__ v,
                                                    float* __restrict__ y, int rows, int cols,
-                                                   const float* __restrict__ scale) {
+                                                   const float* __restrict__ scale,
+                                                   const uint8_t* __restrict__ mx) {
   typedef typename WVec<WT, VEC>::type V;
   const int lane = threadIdx.x & (kWave - 1);
   const int r = blockIdx.x * kWpb + threadIdx.x / kWave;
   if (r >= rows) return;
-  const WT* w = W + (int64_t)r * cols;
+  const WT* w = W + eoff<WT>((int64_t)r * cols);
+  const uint8_t* mxr = mx != nullptr ? mx + (int64_t)r * (cols / 32) : nullptr;
   float acc = 0.0f;
   for (int c = lane * VEC; c < cols; c += kWave * VEC) {
-    const V wv = load_w<WT, VEC>(w + c);
+    const V wv = load_wq<WT, VEC>(w + eoff<WT>(c), mxr != nullptr ? mxr + c / 32 : nullptr);
     float xv[VEC];
     load_x<VT, VEC>(v + c, xv);
 #pragma unroll
@@ -129,16 +132,23 @@ hipError_t naive_t(const Problem& p, const NaiveWs& w, const HostTopK& t, hipStr
     const WT* U = reinterpret_cast<const WT*>(eb + p.off_up_b);
     const WT* D = reinterpret_cast<const WT*>(eb + p.off_down_b);
     // fp8 row scales: s_gate[I], s_up[I], s_down[h]
-    const float* sc =
-        p.off_scale_b >= 0 ? reinterpret_cast<const float*>(eb + p.off_scale_b) : nullptr;
+    const float* sc = p.wdt == WR_FP8_E4M3
+                          ? reinterpret_cast<const float*>(eb + p.off_scale_b)
+                          : nullptr;
+    // MXFP4 block scales: gate [I][h/32], up [I][h/32], down [h][I/32]
+    const uint8_t* mx = p.wdt == WR_MXFP4
+                            ? reinterpret_cast<const uint8_t*>(eb + p.off_scale_b)
+                            : nullptr;
+    const int64_t mxm = (int64_t)p.I * p.h / 32;
     hipLaunchKernelGGL((k_matvec<WT, XT, VEC>), gI, dim3(kBlock), 0, s, G, x, w.gate_vec, p.I,
-                       p.h, sc);
+                       p.h, sc, mx);
     hipLaunchKernelGGL((k_matvec<WT, XT, VEC>), gI, dim3(kBlock), 0, s, U, x, w.up_vec, p.I,
-                       p.h, sc != nullptr ? sc + p.I : nullptr);
+                       p.h, sc != nullptr ? sc + p.I : nullptr, mx != nullptr ? mx + mxm : nullptr);
     hipLaunchKernelGGL(k_swiglu, dim3((p.I + 255) / 256), dim3(256), 0, s, w.gate_vec, w.up_vec,
                        w.act_vec, p.I);
     hipLaunchKernelGGL((k_matvec<WT, float, VEC>), gH, dim3(kBlock), 0, s, D, w.act_vec,
-                       w.expert_out, p.h, p.I, sc != nullptr ? sc + 2 * p.I : nullptr);
+                       w.expert_out, p.h, p.I, sc != nullptr ? sc + 2 * p.I : nullptr,
+                       mx != nullptr ? mx + 2 * mxm : nullptr);
     hipLaunchKernelGGL((k_weighted_accum<XT>), dim3((p.h + 255) / 256), dim3(256), 0, s, w.accum,
                        w.expert_out, t.w[kk], p.h, kk == 0 ? 1 : 0,
                        kk == p.k - 1 ? out : static_cast<XT*>(nullptr));
@@ -150,8 +160,8 @@ hipError_t naive_t(const Problem& p, const NaiveWs& w, const HostTopK& t, hipStr
 
 template <typename WT, typename XT>
 hipError_t naive_w(const Problem& p, const NaiveWs& w, const HostTopK& t, hipStream_t s) {
-  constexpr int V = wvec_width<WT>();
-  return p.vec == V ? naive_t<WT, XT, V>(p, w, t, s) : naive_t<WT, XT, 1>(p, w, t, s);
+  constexpr int V = wvec_width<WT>(), V1 = wvec_scalar<WT>();
+  return p.vec == V ? naive_t<WT, XT, V>(p, w, t, s) : naive_t<WT, XT, V1>(p, w, t, s);
 }
 
 template <typename XT>
@@ -160,6 +170,7 @@ hipError_t naive_x(const Problem& p, const NaiveWs& w, const HostTopK& t, hipStr
     case WR_F16: return naive_w<f16, XT>(p, w, t, s);
     case WR_BF16: return naive_w<bf16w, XT>(p, w, t, s);
     case WR_FP8_E4M3: return naive_w<fp8w, XT>(p, w, t, s);
+    case WR_MXFP4: return naive_w<fp4x2, XT>(p, w, t, s);
     default: return naive_w<float, XT>(p, w, t, s);
   }
 }

@@ -17,10 +17,11 @@ import torch.nn as nn
 
 from .functional import (MAX_EXPERTS, MAX_TOPK, WEIGHT_DTYPES, _pack_expert_weights,
                          batched_fused_moe, expert_layout, fused_moe, gate_topk, naive_moe,
-                         quantize_fp8, weight_layout)
+                         quantize_fp8, quantize_mxfp4, weight_layout)
 
 __all__ = ["MoELayer", "fused_moe", "naive_moe", "batched_fused_moe", "gate_topk",
-           "expert_layout", "weight_layout", "quantize_fp8", "_pack_expert_weights"]
+           "expert_layout", "weight_layout", "quantize_fp8", "quantize_mxfp4",
+           "_pack_expert_weights"]
 
 
 class MoELayer(nn.Module):
@@ -35,7 +36,8 @@ class MoELayer(nn.Module):
         renormalize: divide the selected weights by their sum.
         weight_dtype: dtype of the packed expert buffer the kernels read
             (torch.float32 as in the reference, torch.float16, torch.bfloat16,
-            or torch.float8_e4m3fn with per-channel fp32 scales).
+            torch.float8_e4m3fn with per-row fp32 scales, or
+            torch.float4_e2m1fn_x2 for MXFP4).
     """
 
     def __init__(self, num_experts: int, hidden_dim: int, intermediate_dim: int,

@@ -27,12 +27,14 @@ WR_EINVAL_WEIGHT_SIZE = 6
 WR_EINVAL_WORKSPACE = 7
 WR_EINVAL_BATCH = 8
 WR_EINVAL_KIND = 9
+WR_EINVAL_BLOCK = 10
 WR_EHIP = 100
 
 WR_F32 = 0
 WR_F16 = 1
 WR_BF16 = 2
 WR_FP8_E4M3 = 3
+WR_MXFP4 = 4
 
 WR_KIND_FUSED = 0
 WR_KIND_BATCHED = 1

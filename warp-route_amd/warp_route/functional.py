@@ -13,9 +13,11 @@ trailing keyword arguments add:
   topk_weights  optional preallocated float32 tensor of the same shape that
                 receives their gate weights
 
-``weight_buf`` may be float32 (the reference layout), float16, bfloat16 or
-float8_e4m3fn (codes plus fp32 scales, see ``weight_layout``); ``x`` may be
-float32 or float16 and the output has x's dtype.  Work runs on the current
+``weight_buf`` may be float32 (the reference layout), float16, bfloat16,
+float8_e4m3fn (codes plus fp32 row scales) or float4_e2m1fn_x2 (MXFP4: two
+E2M1 codes per byte plus an E8M0 scale per 32 elements), see
+``weight_layout``; ``x`` may be float32 or float16 and the output has x's
+dtype.  Work runs on the current
 HIP stream without a device synchronisation.  There is no CPU fallback: the
 ops raise if the HIP extension is missing.
 """
@@ -30,7 +32,10 @@ MAX_EXPERTS = 64  # src/gate.cuh:5
 MAX_TOPK = 6      # src/gate.cuh:7
 EXPERT_ALIGN = 128
 FP8_MAX = 448.0   # largest finite OCP E4M3 value
-WEIGHT_DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.float8_e4m3fn)
+WEIGHT_DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.float8_e4m3fn,
+                 torch.float4_e2m1fn_x2)
+MX_BLOCK = 32     # MXFP4 elements per E8M0 scale
+E2M1_GRID = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)  # magnitudes of codes 0..7
 
 
 @functools.lru_cache(maxsize=1)
@@ -72,6 +77,15 @@ def weight_layout(num_experts: int, hidden_dim: int, intermediate_dim: int,
     them, rounded up to 128."""
     if dtype not in WEIGHT_DTYPES:
         raise ValueError(f"weight dtype must be one of {WEIGHT_DTYPES}, got {dtype}")
+    if dtype == torch.float4_e2m1fn_x2:
+        if hidden_dim % MX_BLOCK or intermediate_dim % MX_BLOCK:
+            raise ValueError(f"MXFP4 weights need hidden_dim and intermediate_dim to be multiples "
+                             f"of {MX_BLOCK}, got {hidden_dim}, {intermediate_dim}")
+        n = intermediate_dim * hidden_dim
+        sc = (3 * n // 2 + 15) // 16 * 16
+        stride = (sc + 3 * n // MX_BLOCK + EXPERT_ALIGN - 1) // EXPERT_ALIGN * EXPERT_ALIGN
+        return {"gate_proj_offset": 0, "up_proj_offset": n // 2, "down_proj_offset": n,
+                "scale_offset": sc, "expert_stride": stride, "elem_bytes": 0}
     es = torch.empty((), dtype=dtype).element_size()
     if dtype != torch.float8_e4m3fn:
         out = expert_layout(num_experts, hidden_dim, intermediate_dim, es)
@@ -85,6 +99,14 @@ def weight_layout(num_experts: int, hidden_dim: int, intermediate_dim: int,
             "scale_offset": sc, "expert_stride": stride, "elem_bytes": 1}
 
 
+def zeros_weights(n: int, dtype: torch.dtype, device) -> torch.Tensor:
+    """A zeroed 1-D weight buffer of n elements (torch has no fill kernel for
+    float4_e2m1fn_x2, so its bytes are zeroed as uint8)."""
+    if dtype == torch.float4_e2m1fn_x2:
+        return torch.zeros(n, dtype=torch.uint8, device=device).view(dtype)
+    return torch.zeros(n, dtype=dtype, device=device)
+
+
 def quantize_fp8(w: torch.Tensor, dim: int):
     """(codes, scales) of ``w`` in OCP E4M3 with one fp32 scale per slice
     along ``dim`` (dim=1: per row, dim=0: per column):
@@ -95,6 +117,39 @@ def quantize_fp8(w: torch.Tensor, dim: int):
     scale = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
     q = (wf / scale).clamp_(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
     return q, scale.reshape(-1)
+
+
+def quantize_mxfp4(w: torch.Tensor):
+    """(codes, scales) of a [rows, cols] matrix in OCP MXFP4 (cols a multiple
+    of 32): per block of 32 elements of a row, the shared E8M0 exponent is
+    floor(log2(max|block|)) - 2 (E2M1's largest exponent; 0 for an all-zero
+    block) plus the bias 127, and each element is w / 2^(exponent) rounded to
+    the nearest E2M1 value, ties to an even code, saturating at 6.
+    Returns codes as uint8 [rows, cols / 2] (element 2i in the low nibble) and
+    scales as uint8 [rows, cols / 32]."""
+    rows, cols = w.shape
+    if cols % MX_BLOCK:
+        raise ValueError(f"MXFP4 rows need a multiple of {MX_BLOCK} elements, got {cols}")
+    wf = w.to(torch.float32).reshape(rows, cols // MX_BLOCK, MX_BLOCK)
+    amax = wf.abs().amax(dim=-1)
+    _, ex = torch.frexp(amax)  # amax = m * 2^ex, m in [0.5, 1): floor(log2(amax)) = ex - 1
+    e8 = torch.where(amax > 0, (ex.to(torch.int32) - 1 - 2 + 127).clamp(0, 254),
+                     torch.zeros_like(ex, dtype=torch.int32))
+    scale = torch.ldexp(torch.ones_like(amax), (e8 - 127).to(torch.float32))
+    v = wf / scale.unsqueeze(-1)
+    a = v.abs().clamp(max=6.0)
+    grid = torch.tensor(E2M1_GRID, dtype=torch.float32, device=w.device)
+    dist = (a.unsqueeze(-1) - grid).abs()
+    code = dist.argmin(dim=-1)  # the lower code on a tie
+    # a tie between an odd code and the next one goes to the even code
+    nxt = (code + 1).clamp(max=7)
+    tie = (code % 2 == 1) & (dist.gather(-1, nxt.unsqueeze(-1)).squeeze(-1) ==
+                             dist.gather(-1, code.unsqueeze(-1)).squeeze(-1))
+    code = torch.where(tie, nxt, code)
+    code = code | ((v < 0).to(code.dtype) << 3)
+    code = code.to(torch.uint8).reshape(rows, cols)
+    packed = code[:, 0::2] | (code[:, 1::2] << 4)
+    return packed.contiguous(), e8.to(torch.uint8).contiguous()
 
 
 def _pack_expert_weights(
@@ -118,10 +173,21 @@ def _pack_expert_weights(
     ``gate_proj[0]``.
     """
     off = weight_layout(num_experts, hidden_dim, intermediate_dim, dtype)
-    es = off["elem_bytes"]
+    es = torch.empty((), dtype=dtype).element_size()  # bytes per buffer element
     stride_el = off["expert_stride"] // es
     n = intermediate_dim * hidden_dim
-    buf = torch.zeros(num_experts * stride_el, dtype=dtype, device=gate_proj[0].device)
+    buf = zeros_weights(num_experts * stride_el, dtype, gate_proj[0].device)
+    raw = buf.view(torch.uint8)
+    if dtype == torch.float4_e2m1fn_x2:
+        gs = n // MX_BLOCK  # scale bytes per matrix
+        for e in range(num_experts):
+            base = e * stride_el
+            for j, m in enumerate((gate_proj[e], up_proj[e], down_proj[e])):
+                q, sc = quantize_mxfp4(m)
+                raw[base + j * n // 2:base + (j + 1) * n // 2] = q.reshape(-1)
+                s0 = base + off["scale_offset"] + j * gs
+                raw[s0:s0 + gs] = sc.reshape(-1)
+        return buf
     if dtype != torch.float8_e4m3fn:
         for e in range(num_experts):
             base = e * stride_el
@@ -129,7 +195,6 @@ def _pack_expert_weights(
             buf[base + n:base + 2 * n] = up_proj[e].reshape(-1)
             buf[base + 2 * n:base + 3 * n] = down_proj[e].reshape(-1)
         return buf
-    raw = buf.view(torch.uint8)
     ns = 2 * intermediate_dim + hidden_dim
     for e in range(num_experts):
         base = e * stride_el

@@ -18,7 +18,7 @@ from typing import Optional
 
 import torch
 
-from .functional import quantize_fp8, weight_layout
+from .functional import MX_BLOCK, quantize_fp8, quantize_mxfp4, weight_layout, zeros_weights
 
 
 @dataclass(frozen=True)
@@ -47,10 +47,13 @@ class MoEConfig:
 
 def expert_weight_bytes(hidden_dim: int, intermediate_dim: int, dtype: torch.dtype) -> int:
     """Bytes a kernel must read for one selected expert: its three matrices,
-    and for fp8 its three scale arrays."""
+    and for fp8 and MXFP4 their scales."""
+    n = 3 * hidden_dim * intermediate_dim
+    if dtype == torch.float4_e2m1fn_x2:
+        return n // 2 + n // MX_BLOCK
     es = torch.empty((), dtype=dtype).element_size()
-    n = 3 * hidden_dim * intermediate_dim * es
-    return n + (12 * intermediate_dim if dtype == torch.float8_e4m3fn else 0)
+    return n * es + (4 * (2 * intermediate_dim + hidden_dim) if dtype == torch.float8_e4m3fn
+                     else 0)
 
 
 CONFIGS = {
@@ -81,11 +84,12 @@ def make_layer(num_experts: int, hidden_dim: int, intermediate_dim: int,
     gate_w = torch.randn(num_experts, hidden_dim, generator=gen, device=gen_device,
                          dtype=torch.float32) * router_std
     off = weight_layout(num_experts, hidden_dim, intermediate_dim, weight_dtype)
-    es = off["elem_bytes"]
+    es = torch.empty((), dtype=weight_dtype).element_size()
     stride_el = off["expert_stride"] // es
     n = intermediate_dim * hidden_dim
     fp8 = weight_dtype == torch.float8_e4m3fn
-    buf = torch.zeros(num_experts * stride_el, dtype=weight_dtype, device=device)
+    fp4 = weight_dtype == torch.float4_e2m1fn_x2
+    buf = zeros_weights(num_experts * stride_el, weight_dtype, device)
     raw = buf.view(torch.uint8)
     I = intermediate_dim
     for e in range(num_experts):
@@ -94,7 +98,13 @@ def make_layer(num_experts: int, hidden_dim: int, intermediate_dim: int,
             shape = (intermediate_dim, hidden_dim) if j < 2 else (hidden_dim, intermediate_dim)
             w = torch.randn(shape, generator=gen, device=gen_device, dtype=torch.float32)
             w.mul_(expert_std)
-            if fp8:
+            if fp4:
+                q, sc = quantize_mxfp4(w)
+                raw[base + j * n // 2:base + (j + 1) * n // 2].copy_(q.reshape(-1))
+                s0 = base + off["scale_offset"] + j * (n // MX_BLOCK)
+                raw[s0:s0 + n // MX_BLOCK].copy_(sc.reshape(-1))
+                del q, sc
+            elif fp8:
                 # a scale per row: gate and up rows at j * I, down rows at 2 I
                 q, sc = quantize_fp8(w, 1)
                 buf[base + j * n:base + (j + 1) * n].copy_(q.reshape(-1))
