@@ -29,6 +29,7 @@ per token), launched op by op and, with --graph, from one captured HIP graph.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import statistics
@@ -311,6 +312,9 @@ def main() -> int:
                     help="time one token through this many layers instead")
     ap.add_argument("--graph", action="store_true",
                     help="with --stack: also replay the step from a captured HIP graph")
+    ap.add_argument("--tp-shard", type=int, default=1, metavar="G",
+                    help="time one GPU's share of a G-way tensor-parallel split over the "
+                         "intermediate dimension (I/G rows of gate/up, I/G columns of down)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -337,6 +341,17 @@ def main() -> int:
     from warp_route.synthetic import CONFIGS, make_config_layer
 
     cfg = CONFIGS[args.config].with_weights(weight_dtype(args.weights))
+    G = args.tp_shard
+    if G > 1:
+        # The shard is the same packed layout with I' = I / G; the router is
+        # replicated, so every shard routes as the whole layer does.
+        if cfg.intermediate_dim % G or (args.weights == "mxfp4"
+                                        and (cfg.intermediate_dim // G) % 32):
+            print(f"--tp-shard {G} does not divide I = {cfg.intermediate_dim} "
+                  f"into whole rows for {args.weights}", file=sys.stderr)
+            return 2
+        cfg = dataclasses.replace(cfg, intermediate_dim=cfg.intermediate_dim // G,
+                                  name=f"{cfg.name}_tp{G}")
     E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
     dev = torch.device("cuda:0")
     log(f"[bench] generating {args.layers} {cfg.name} {args.weights} layers on the GPU")
@@ -403,11 +418,13 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": WLABEL[args.weights] + " weights, f32 accumulate",
         "data": "synthetic (seeded random-init layers drawn on the GPU)",
-        "config": {"workload": f"{cfg.name} MoE layer, decode batch 1", "hidden": h,
+        "config": {"workload": f"{cfg.name} MoE layer, decode batch 1"
+                   + (f", one of {G} tensor-parallel shards over I" if G > 1 else ""),
+                   "hidden": h,
                    "intermediate": I, "experts": E, "top_k": k,
                    "renormalize": cfg.renormalize, "weight_dtype": args.weights,
                    "x_dtype": "fp32", "layers_rotated": args.layers,
-                   "parallelism": "single GPU"},
+                   "parallelism": "single GPU" if G == 1 else f"tp{G} shard, one GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic, "kernel": "k_fused_ffn",

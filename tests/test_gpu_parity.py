@@ -580,3 +580,42 @@ def test_full_size_batched_clustered(cuda, B):
         assert_parity(out[b], ids[b], None, ref, label=f"clustered b={b}")
     del buf
     torch.cuda.empty_cache()
+
+
+TP = [("mixtral", F16, 2), ("mixtral", F16, 8), ("mixtral", FP8, 4), ("mixtral", MX4, 4),
+      ("deepseek", F16, 2), ("dbrx", F16, 4)]
+
+
+@pytest.mark.parametrize("name,wd,G", TP, ids=[f"{n}-{WNAME[w]}-tp{g}" for n, w, g in TP])
+def test_tp_shards_sum_to_the_full_layer(cuda, name, wd, G):
+    """A G-way tensor-parallel split over I on one GPU: each shard (the same
+    kernels at I' = I/G) selects the full layer's experts and matches the
+    oracle on its own weights, and the shards' outputs sum to the full
+    layer's output up to fp32 summation order (the all-reduce a multi-GPU
+    run would do)."""
+    cfg = CONFIGS[name].with_weights(wd)
+    E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+    for seed in range(20):
+        x, gw, buf = make_config_layer(cfg, seed=seed, device=cuda, gen_device=cuda)
+        if O.selection_is_robust(f64(gw), f64(x), k):
+            break
+        del buf
+    print(f"[gpu] tp {name} {WNAME[wd]} G={G} seed={seed}", flush=True)
+    ids = torch.empty(k, dtype=torch.int32, device=cuda)
+    full = F.fused_moe(x, gw, buf, E, h, I, k, cfg.renormalize, ids)
+    total = torch.zeros_like(full)
+    Is = I // G
+    for s in range(G):
+        part = F.shard_expert_weights(buf, E, h, I, G, s)
+        sids = torch.empty(k, dtype=torch.int32, device=cuda)
+        out = F.fused_moe(x, gw, part, E, h, Is, k, cfg.renormalize, sids)
+        torch.cuda.synchronize()
+        assert torch.equal(sids, ids), f"shard {s}: {sids.tolist()} != {ids.tolist()}"
+        if s in (0, G - 1):
+            ref = oracle_token(x, gw, part, E, h, Is, k, cfg.renormalize)
+            assert_parity(out, sids, None, ref, label=f"{name} tp{G} shard {s}")
+        total += out
+        del part
+    assert_same_up_to_order(total, full, label=f"{name} tp{G} sum of shards")
+    del buf
+    torch.cuda.empty_cache()

@@ -253,3 +253,63 @@ def test_mxfp4_packer_error_bound():
             half = np.where(a < 2, 0.25, np.where(a < 4, 0.5, 1.0))
             bound = np.maximum(half, a - 6.0) * sc * (1 + 1e-9)
             assert np.all(np.abs(d - w) <= bound)
+
+
+SHARD_FMTS = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16",
+              torch.float8_e4m3fn: "fp8", torch.float4_e2m1fn_x2: "mxfp4"}
+
+
+def _decoded(buf, E, h, I, fmt):
+    raw = buf.view(torch.uint8).numpy()
+    return [O.expert_matrices(raw, e, E, h, I, fmt) for e in range(E)]
+
+
+@pytest.mark.parametrize("dtype", list(SHARD_FMTS), ids=list(SHARD_FMTS.values()))
+def test_shard_expert_weights_slices_every_format(dtype):
+    """shard_expert_weights, decoded by the oracle (scales included), holds
+    exactly rows [s I', (s+1) I') of the full layer's gate and up and the same
+    columns of its down, for every shard; shards of shards compose."""
+    E, h, I = 3, 64, 256
+    fmt = SHARD_FMTS[dtype]
+    g = torch.Generator().manual_seed(5)
+    mats = [[torch.randn(s, generator=g) * 0.05 for s in ((I, h), (I, h), (h, I))]
+            for _ in range(E)]
+    buf = F._pack_expert_weights([m[0] for m in mats], [m[1] for m in mats],
+                                 [m[2] for m in mats], E, h, I, dtype=dtype)
+    full = _decoded(buf, E, h, I, fmt)
+    for G in (2, 4, 8):
+        Is = I // G
+        for s in range(G):
+            part = F.shard_expert_weights(buf, E, h, I, G, s)
+            assert part.dtype == dtype
+            lo = F.weight_layout(E, h, Is, dtype)
+            assert part.numel() * part.element_size() == E * lo["expert_stride"]
+            for e, (gf, uf, df) in enumerate(full):
+                gs, us, ds = _decoded(part, E, h, Is, fmt)[e]
+                rs = slice(s * Is, (s + 1) * Is)
+                np.testing.assert_array_equal(gs, gf[rs])
+                np.testing.assert_array_equal(us, uf[rs])
+                np.testing.assert_array_equal(ds, df[:, rs])
+    # shard 3 of 4 == shard 1 of 2 of shard 1 of 2, byte for byte
+    a = F.shard_expert_weights(buf, E, h, I, 4, 3).view(torch.uint8)
+    b = F.shard_expert_weights(F.shard_expert_weights(buf, E, h, I, 2, 1), E, h, I // 2, 2, 1)
+    assert torch.equal(a, b.view(torch.uint8))
+    # one shard is the whole layer
+    assert torch.equal(F.shard_expert_weights(buf, E, h, I, 1, 0).view(torch.uint8),
+                       buf.view(torch.uint8))
+
+
+def test_shard_expert_weights_argument_checks():
+    E, h, I = 2, 64, 96
+    buf = F.zeros_weights(E * F.weight_layout(E, h, I, torch.float16)["expert_stride"] // 2,
+                          torch.float16, "cpu")
+    with pytest.raises(ValueError):
+        F.shard_expert_weights(buf, E, h, I, 5, 0)      # 96 % 5 != 0
+    with pytest.raises(ValueError):
+        F.shard_expert_weights(buf, E, h, I, 2, 2)      # no shard 2 of 2
+    with pytest.raises(ValueError):
+        F.shard_expert_weights(buf[:-1], E, h, I, 2, 0)  # buffer too small
+    b4 = F.zeros_weights(E * F.weight_layout(E, h, I, torch.float4_e2m1fn_x2)["expert_stride"],
+                         torch.float4_e2m1fn_x2, "cpu")
+    with pytest.raises(ValueError):
+        F.shard_expert_weights(b4, E, h, I, 2, 0)       # I' = 48 is not a multiple of 32

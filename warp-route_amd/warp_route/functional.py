@@ -209,6 +209,70 @@ def _pack_expert_weights(
     return buf
 
 
+_CODE_BITS = {torch.float32: 32, torch.float16: 16, torch.bfloat16: 16,
+              torch.float8_e4m3fn: 8, torch.float4_e2m1fn_x2: 4}
+
+
+def shard_expert_weights(weight_buf: torch.Tensor, num_experts: int, hidden_dim: int,
+                         intermediate_dim: int, num_shards: int, shard: int) -> torch.Tensor:
+    """One GPU's share of a tensor-parallel split over the intermediate
+    dimension: a packed buffer (same dtype, same device) of the layer with
+    I' = I / num_shards, holding rows [s I', (s+1) I') of every expert's gate
+    and up matrices and the same columns of its down matrix.
+
+    The codes are copied, not requantized: fp8 gate/up row scales are sliced
+    with their rows and the down row scales kept whole; MXFP4 block scales
+    move with their 32-element blocks (I' must be a multiple of 32).  So the
+    shard holds exactly the original weights, each shard routes as the whole
+    layer does (the router is replicated), and the whole layer's output is
+    the sum of the shards' outputs."""
+    E, h, I, G = num_experts, hidden_dim, intermediate_dim, num_shards
+    if G < 1 or I % G or not 0 <= shard < G:
+        raise ValueError(f"cannot take shard {shard} of {G} from intermediate_dim {I}")
+    dt = weight_buf.dtype
+    Is = I // G
+    full = weight_layout(E, h, I, dt)
+    part = weight_layout(E, h, Is, dt)  # raises for MXFP4 when I' % 32 != 0
+    bits = _CODE_BITS[dt]
+    if weight_buf.numel() * weight_buf.element_size() < E * full["expert_stride"]:
+        raise ValueError("weight_buf is smaller than the packed layer")
+
+    def nb(n):  # bytes of n codes
+        return n * bits // 8
+
+    src = weight_buf.reshape(-1).view(torch.uint8)[:E * full["expert_stride"]]
+    src = src.view(E, full["expert_stride"])
+    buf = zeros_weights(E * part["expert_stride"] // weight_buf.element_size(), dt,
+                        weight_buf.device)
+    dst = buf.view(torch.uint8).view(E, part["expert_stride"])
+    r0, r1 = shard * Is, (shard + 1) * Is
+
+    def rows(s_off, d_off, row_bytes):  # rows r0:r1 of a row-major block
+        dst[:, d_off:d_off + Is * row_bytes] = src[:, s_off + r0 * row_bytes:
+                                                   s_off + r1 * row_bytes]
+
+    def cols(s_off, d_off, n_rows, full_bytes, lo, hi):  # columns lo:hi (bytes) of every row
+        d = dst[:, d_off:d_off + n_rows * (hi - lo)].view(E, n_rows, hi - lo)
+        d.copy_(src[:, s_off:s_off + n_rows * full_bytes].view(E, n_rows, full_bytes)[:, :, lo:hi])
+
+    rows(full["gate_proj_offset"], part["gate_proj_offset"], nb(h))
+    rows(full["up_proj_offset"], part["up_proj_offset"], nb(h))
+    cols(full["down_proj_offset"], part["down_proj_offset"], h, nb(I), nb(r0), nb(r1))
+    if dt == torch.float8_e4m3fn:  # s_gate[I], s_up[I], s_down[h] (fp32)
+        sf, sp = full["scale_offset"], part["scale_offset"]
+        rows(sf, sp, 4)
+        rows(sf + 4 * I, sp + 4 * Is, 4)
+        dst[:, sp + 8 * Is:sp + 8 * Is + 4 * h] = src[:, sf + 8 * I:sf + 8 * I + 4 * h]
+    elif dt == torch.float4_e2m1fn_x2:  # E8M0 bytes: gate [I][h/32], up [I][h/32], down [h][I/32]
+        sf, sp = full["scale_offset"], part["scale_offset"]
+        hb = h // MX_BLOCK
+        rows(sf, sp, hb)
+        rows(sf + I * hb, sp + Is * hb, hb)
+        cols(sf + 2 * I * hb, sp + 2 * Is * hb, h, I // MX_BLOCK,
+             r0 // MX_BLOCK, r1 // MX_BLOCK)
+    return buf
+
+
 def fused_moe(
     x: torch.Tensor,
     gate_w: torch.Tensor,
