@@ -65,6 +65,15 @@
 #ifndef WR_F8_U2
 #define WR_F8_U2 2   // column chunks per down tile
 #endif
+// x staged in LDS by the gate/up blocks of the single-token fused kernel, for
+// h up to these bounds (0: never).  Measured: it gains for fp8 at h = 2048
+// and for MXFP4 up to h = 4096, and costs fp8 at h = 4096 and 6144.
+#ifndef WR_XL_FP8_MAXH
+#define WR_XL_FP8_MAXH 2048
+#endif
+#ifndef WR_XL_FP4_MAXH
+#define WR_XL_FP4_MAXH 4096
+#endif
 // MXFP4 weights in the single-token fused kernel (32 weights per 128-bit load)
 #ifndef WR_F4_U1
 #define WR_F4_U1 1   // gate/up column chunks per row per iteration (4 rows per wave)
@@ -546,6 +555,135 @@ __device__ __forceinline__ void gateup_item(const WT* __restrict__ wbuf, const X
   }
 }
 
+// x staged in LDS (fp8 and MXFP4 gate/up blocks), in x's own dtype.  The
+// copy is made of 16-byte slots; each VEC-element group of x (DS = VEC / E16
+// slots, E16 elements per slot) is followed by one pad slot, so that the VEC
+// values of lane l start at l (DS + 1) slots and the ds_read_b128s of 16
+// consecutive lanes hit 16 distinct 4-bank groups.  h <= kXlMaxH: the copy
+// is a static array of its size (at most 20 KB, so 4 blocks still fit a CU's
+// LDS), because dynamic LDS keeps the compiler from holding TopK in registers.
+constexpr int kXlMaxH = 4096;
+template <typename XT, int VEC>
+struct XlLayout {
+  static constexpr int kE16 = 16 / (int)sizeof(XT);  // x elements per slot
+  static constexpr int kDS = VEC / kE16;            // data slots per group
+  static constexpr int kGS = kDS + 1;               // slots per group
+  static_assert(VEC % kE16 == 0, "a group is whole slots");
+  __host__ __device__ static constexpr int slots(int h) { return h / VEC * kGS; }
+  __host__ __device__ static constexpr size_t bytes(int h) { return (size_t)slots(h) * 16; }
+};
+
+// Loads of round c0 of rows [r0, r0 + nrows) of one gate/up item.
+template <typename WT, int VEC, int RPW, int U>
+__device__ __forceinline__ void gateup_issue(typename WVec<WT, VEC>::type (&wg)[U][RPW],
+                                             typename WVec<WT, VEC>::type (&wu)[U][RPW],
+                                             const WT* blk, const WT* G, const WT* Up,
+                                             const Geom& g, int r0, int nrows, int c0) {
+  typedef typename WVec<WT, VEC>::type V;
+  constexpr int CH = kWave * VEC;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = c0 + u * CH;
+    const bool ok = c < g.h;
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+      const bool okj = ok && j < nrows;
+      wg[u][j] = okj ? load_wq<WT, VEC>(G + eoff<WT>((int64_t)j * g.h + c),
+                                        mx_at<WT>(mx_row(blk, g, 0, r0 + j), c))
+                     : vzero<V>();
+      wu[u][j] = okj ? load_wq<WT, VEC>(Up + eoff<WT>((int64_t)j * g.h + c),
+                                        mx_at<WT>(mx_row(blk, g, 1, r0 + j), c))
+                     : vzero<V>();
+    }
+  }
+}
+
+// gateup_item with x read from the block's LDS copy (XlLayout).  Every wave
+// of the block calls it, because the copy ends in a block barrier; a wave
+// without an item passes nrows = 0.  The copy is made with direct
+// global-to-LDS loads (no registers), issued before the first round of
+// weight loads; one wait covers both, so the weights are the only
+// long-lived registers and the copy costs no extra round trip.
+template <typename WT, typename XT, int VEC, int RPW, int U>
+__device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
+                                               const XT* __restrict__ xb, float* a,
+                                               const Geom& g, int eid, float wk, int r0,
+                                               int nrows, int lane) {
+  typedef typename WVec<WT, VEC>::type V;
+  typedef XlLayout<XT, VEC> L;
+  constexpr int CH = kWave * VEC;
+  __shared__ __align__(16) unsigned char xs_raw[L::bytes(kXlMaxH)];
+  const WT* blk = wbuf + (int64_t)eid * g.stride;
+  const WT* G = blk + eoff<WT>((int64_t)r0 * g.h);
+  const WT* Up = G + g.off_up;
+
+  // Slot s of the copy holds x[(s / GS) VEC + min(s % GS, DS - 1) E16 ..] (a
+  // pad slot repeats the group's last data slot).  Wave w fills the 64-slot
+  // runs w, w + 4, ... (one wave-uniform LDS base per load).
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+  const int nslots = L::slots(g.h);
+  for (int s0 = wave * kWave; s0 < nslots; s0 += kBlock) {
+    const int sl = s0 + lane;
+    if (sl < nslots) {
+      const int grp = sl / L::kGS;
+      const int r = min(sl - grp * L::kGS, L::kDS - 1);
+      __builtin_amdgcn_global_load_lds(
+          static_cast<const void*>(xb + grp * VEC + r * L::kE16),
+          (__attribute__((address_space(3))) void*)(xs_raw + (size_t)s0 * 16), 16,
+          0, 0);
+    }
+  }
+  V wg[U][RPW], wu[U][RPW];
+  gateup_issue<WT, VEC, RPW, U>(wg, wu, blk, G, Up, g, r0, nrows, lane * VEC);
+  __builtin_amdgcn_s_waitcnt(0);  // the copy's loads (and the weights) have landed
+  __syncthreads();
+
+  float ag[RPW], au[RPW];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) ag[j] = au[j] = 0.0f;
+  for (int c0 = lane * VEC; c0 < g.h; c0 += U * CH) {
+    if (c0 != lane * VEC) gateup_issue<WT, VEC, RPW, U>(wg, wu, blk, G, Up, g, r0, nrows, c0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * CH;
+      float xv[VEC];
+      if (c < g.h) {
+        const unsigned char* xp = xs_raw + (size_t)(c / VEC) * L::kGS * 16;
+#pragma unroll
+        for (int q = 0; q < L::kDS; ++q) {
+          if constexpr (std::is_same<XT, float>::value) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(xp + 16 * q);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[4 * q + i] = v[i];
+          } else {
+            const f16x8 v = *reinterpret_cast<const f16x8*>(xp + 16 * q);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[8 * q + i] = (float)v[i];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) xv[i] = 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < RPW; ++j)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          ag[j] = fmaf(wdec<WT>(wg[u][j], i), xv[i], ag[j]);
+          au[j] = fmaf(wdec<WT>(wu[u][j], i), xv[i], au[j]);
+        }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) {
+    const float gs = wave_sum(ag[j]);
+    const float us = wave_sum(au[j]);
+    if (lane == 0 && j < nrows)
+      __hip_atomic_store(a + j, act_value<WT>(blk, g, r0 + j, wk, gs, us), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // Down tile of a fused down block: U column chunks q = q0 + 4 u (chunk q is
 // columns [(q mod nch) * 64 VEC, +64 VEC) of selected expert q / nch), RPD rows
 // from r0.
@@ -559,10 +697,11 @@ __device__ __forceinline__ void down_tile_load(typename WVec<WT, VEC>::type (&wv
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int q = q0 + u * kWavesPerBlock;
-    const int kk = q / nch;
+    const bool okq = q < C;                  // wave-uniform
+    const int kk = okq ? q / nch : 0;        // a valid selection slot either way
     const int c = (q - kk * nch) * kWave * VEC + lane * VEC;
-    const bool ok = q < C && c < g.I;
-    const WT* blk = wbuf + (int64_t)topk_id(t, ok ? kk : 0) * g.stride;
+    const bool ok = okq && c < g.I;
+    const WT* blk = wbuf + (int64_t)topk_id(t, kk) * g.stride;
     const WT* D = blk + g.off_down + eoff<WT>((int64_t)r0 * g.I + c);
 #pragma unroll
     for (int j = 0; j < RPD; ++j)
@@ -617,7 +756,7 @@ __device__ __forceinline__ void down_tile_fma(float (&acc)[RPD], const V (&wv)[U
   }
 }
 
-template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2>
+template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2, bool XL>
 __global__ __launch_bounds__(kBlock) void k_fused_ffn(
     const WT* __restrict__ wbuf, const XT* __restrict__ x, const float* __restrict__ logits,
     float* act, XT* __restrict__ out, int32_t* __restrict__ ids_out, float* __restrict__ w_out,
@@ -627,7 +766,11 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   constexpr int LB = 32 / COLS;               // chunks per 128-byte act line
   static_assert(COLS * LB == 32 && COLS <= FusedWs::kMaxActCols, "unsupported rows per wave");
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  // With XL, readfirstlane keeps the (wave-uniform) wave index and the TopK
+  // lookups derived from it scalar; without it, that kernel keeps TopK in
+  // scratch memory.
+  const int wave = XL ? __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave)
+                      : (int)threadIdx.x / kWave;
   const int64_t act_row = FusedWs::act_row(g.I, COLS);
 
   TopK t;
@@ -647,7 +790,16 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
     const int items = (g.I + RPW - 1) / RPW;
     const int bpk = (items + kWavesPerBlock - 1) / kWavesPerBlock;  // chunks per expert
     const int G = chunk_of_block<LB>(blockIdx.x);
-    if (G < hs.chunks) {
+    if constexpr (XL) {
+      // Wave-uniform by construction; readfirstlane keeps them in SGPRs, so
+      // that the TopK lookups stay scalar selects.
+      const int kk = __builtin_amdgcn_readfirstlane(G < hs.chunks ? G / bpk : 0);
+      const int it = (G - kk * bpk) * kWavesPerBlock + wave;
+      const int nrows = (G < hs.chunks && it < items) ? min(RPW, g.I - it * RPW) : 0;
+      gateup_item_xl<WT, XT, VEC, RPW, U1>(wbuf, x, act + kk * act_row + it * RPW, g,
+                                           topk_id(t, kk), topk_w(t, kk),
+                                           nrows > 0 ? it * RPW : 0, nrows, lane);
+    } else if (G < hs.chunks) {
       const int kk = G / bpk;
       const int it = (G - kk * bpk) * kWavesPerBlock + wave;
       if (it < items)
@@ -845,7 +997,20 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   constexpr int RPD = kFp4 ? WR_F4_RPD : (kFp8 ? WR_F8_RPD : WR_FU_RPD);
   constexpr int U2 = kFp4 ? WR_F4_U2 : (kFp8 ? WR_F8_U2 : WR_FU_U);
   const int n2 = (p.h + RPD - 1) / RPD;
-  hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2>),
+  // fp8 and MXFP4 gate/up blocks read x from an LDS copy for small enough h.
+  constexpr int kXlMax = kFp8 ? WR_XL_FP8_MAXH : (kFp4 ? WR_XL_FP4_MAXH : 0);
+  static_assert(kXlMax <= kXlMaxH, "the LDS copy holds at most kXlMaxH elements");
+  constexpr bool kXl = kXlMax > 0 && VEC >= 16;
+  if constexpr (kXl) {
+    if (p.h <= kXlMax) {
+      hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true>),
+                         dim3(hs.n1 + n2), dim3(kBlock), 0, s,
+                         static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x), w.logits,
+                         w.act, static_cast<XT*>(p.out), p.topk_ids, p.topk_w, g, hs);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, false>),
                      dim3(hs.n1 + n2), dim3(kBlock), 0, s, static_cast<const WT*>(p.wbuf),
                      static_cast<const XT*>(p.x), w.logits, w.act, static_cast<XT*>(p.out),
                      p.topk_ids, p.topk_w, g, hs);
