@@ -66,10 +66,15 @@
 #define WR_F8_U2 2   // column chunks per down tile
 #endif
 // x staged in LDS by the gate/up blocks of the single-token fused kernel, for
-// h up to these bounds (0: never).  Measured: it gains for fp8 at h = 2048
-// and for MXFP4 up to h = 4096, and costs fp8 at h = 4096 and 6144.
+// h up to these bounds (0: never); fp8 also needs at most WR_XL_FP8_BPC gate/up
+// blocks per CU.  Measured: it gains for MXFP4 up to h = 4096 and for fp8
+// when the gate/up blocks fit in one round of residency (DeepSeek, Mixtral
+// shards), and costs fp8 with many rounds (Mixtral 3584 blocks) or h = 6144.
 #ifndef WR_XL_FP8_MAXH
-#define WR_XL_FP8_MAXH 2048
+#define WR_XL_FP8_MAXH 4096
+#endif
+#ifndef WR_XL_FP8_BPC
+#define WR_XL_FP8_BPC 4
 #endif
 #ifndef WR_XL_FP4_MAXH
 #define WR_XL_FP4_MAXH 4096
@@ -1002,7 +1007,7 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   static_assert(kXlMax <= kXlMaxH, "the LDS copy holds at most kXlMaxH elements");
   constexpr bool kXl = kXlMax > 0 && VEC >= 16;
   if constexpr (kXl) {
-    if (p.h <= kXlMax) {
+    if (p.h <= kXlMax && (!kFp8 || hs.n1 <= WR_XL_FP8_BPC * cu_count())) {
       hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true>),
                          dim3(hs.n1 + n2), dim3(kBlock), 0, s,
                          static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x), w.logits,
