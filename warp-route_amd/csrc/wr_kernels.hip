@@ -66,12 +66,16 @@
 #define WR_F8_U2 2   // column chunks per down tile
 #endif
 // x staged in LDS by the gate/up blocks of the single-token fused kernel, for
-// h up to these bounds (0: never); fp8 also needs at most WR_XL_FP8_BPC gate/up
-// blocks per CU.  Measured: it gains for MXFP4 up to h = 4096 and for fp8
-// when the gate/up blocks fit in one round of residency (DeepSeek, Mixtral
-// shards), and costs fp8 with many rounds (Mixtral 3584 blocks) or h = 6144.
+// h up to these bounds (0: never); fp8, fp16 and bf16 also need at most
+// WR_XL_FP8_BPC gate/up blocks per CU.  Measured: it gains for MXFP4 up to
+// h = 4096, and for the other types when the gate/up blocks fit in one round
+// of residency (DeepSeek, Mixtral shards); it costs with many rounds (Mixtral,
+// 3584 blocks) or at h = 6144.
 #ifndef WR_XL_FP8_MAXH
 #define WR_XL_FP8_MAXH 4096
+#endif
+#ifndef WR_XL_F16_MAXH
+#define WR_XL_F16_MAXH 4096
 #endif
 #ifndef WR_XL_FP8_BPC
 #define WR_XL_FP8_BPC 4
@@ -1002,12 +1006,15 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   constexpr int RPD = kFp4 ? WR_F4_RPD : (kFp8 ? WR_F8_RPD : WR_FU_RPD);
   constexpr int U2 = kFp4 ? WR_F4_U2 : (kFp8 ? WR_F8_U2 : WR_FU_U);
   const int n2 = (p.h + RPD - 1) / RPD;
-  // fp8 and MXFP4 gate/up blocks read x from an LDS copy for small enough h.
-  constexpr int kXlMax = kFp8 ? WR_XL_FP8_MAXH : (kFp4 ? WR_XL_FP4_MAXH : 0);
+  // Gate/up blocks read x from an LDS copy for small enough h (and, except
+  // for MXFP4, few enough gate/up blocks).
+  constexpr bool k16 = std::is_same<WT, f16>::value || std::is_same<WT, bf16w>::value;
+  constexpr int kXlMax =
+      kFp8 ? WR_XL_FP8_MAXH : (kFp4 ? WR_XL_FP4_MAXH : (k16 ? WR_XL_F16_MAXH : 0));
   static_assert(kXlMax <= kXlMaxH, "the LDS copy holds at most kXlMaxH elements");
-  constexpr bool kXl = kXlMax > 0 && VEC >= 16;
+  constexpr bool kXl = kXlMax > 0 && VEC >= 8;
   if constexpr (kXl) {
-    if (p.h <= kXlMax && (!kFp8 || hs.n1 <= WR_XL_FP8_BPC * cu_count())) {
+    if (p.h <= kXlMax && (kFp4 || hs.n1 <= WR_XL_FP8_BPC * cu_count())) {
       hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true>),
                          dim3(hs.n1 + n2), dim3(kBlock), 0, s,
                          static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x), w.logits,
