@@ -45,10 +45,17 @@ namespace wr {
 
 namespace {
 
+#ifndef WR_SMALL_TILE_MAX_B
+#define WR_SMALL_TILE_MAX_B 16  // batches up to this size use 16-token tiles
+#endif
+#ifndef WR_MID_TILE_MAX_B
+#define WR_MID_TILE_MAX_B 32    // and up to this size 32-token tiles
+#endif
+
 constexpr int kBlk = 256;       // 4 waves
 constexpr int kBK = 128;        // K step (columns per LDS tile)
 constexpr int kBM = 64;         // rows per block: 4 waves x 16
-constexpr int kMaxTok = 64;     // tokens per pass: 4 MFMA N tiles
+constexpr int kMaxTok = 64;     // tokens per pass, at most: 4 MFMA N tiles
 constexpr int kPieces = kBK / 8;        // 16-byte pieces per token row of a tile
 constexpr int kLdsRow = kPieces + 1;    // padded row: spreads lanes over the LDS banks
 
@@ -172,22 +179,31 @@ __global__ __launch_bounds__(1024) void k_route(const float* __restrict__ logits
 // Token tiles in LDS.  xs[0] holds the hi terms, xs[1] the lo terms; row n is
 // token n of the pass, piece c covers columns [8 c, 8 c + 8) of the K step.
 // ---------------------------------------------------------------------------
+// TOK tokens per pass (16, 32 or 64): a launch whose experts have at most 16
+// (32) tokens each takes the smaller tile, whose LDS and registers leave room
+// for more blocks per CU.
+template <int TOK>
 struct TokTile {
-  H8 hi[kMaxTok][kLdsRow];
-  H8 lo[kMaxTok][kLdsRow];
+  H8 hi[TOK][kLdsRow];
+  H8 lo[TOK][kLdsRow];
 };
 
 // One thread's share of a token tile, held in registers between the global
 // loads and the LDS stores: pieces i = threadIdx.x + kBlk * q, token row
 // n = i / kPieces, 8 columns at 8 (i % kPieces) of the K step.
-constexpr int kTilePieces = kMaxTok * kPieces / kBlk;  // 4
+template <int TOK>
+constexpr int tile_pieces() {
+  static_assert(TOK * kPieces % kBlk == 0, "whole pieces per thread");
+  return TOK * kPieces / kBlk;  // 1 or 4
+}
 
 // Element offset of each piece's row start (plus its column), or -1 for a
 // padding token; fixed for a whole pass.
-__device__ __forceinline__ void tile_rows(int64_t (&off)[kTilePieces], const int32_t* rows,
-                                          int direct0, int mt, int ld) {
+template <int TP>
+__device__ __forceinline__ void tile_rows(int64_t (&off)[TP], const int32_t* rows, int direct0,
+                                          int mt, int ld) {
 #pragma unroll
-  for (int q = 0; q < kTilePieces; ++q) {
+  for (int q = 0; q < TP; ++q) {
     const int i = threadIdx.x + kBlk * q;
     const int n = i / kPieces, c = i % kPieces;
     const int row = rows != nullptr ? (n < mt ? rows[n] : 0) : direct0 + n;
@@ -196,13 +212,13 @@ __device__ __forceinline__ void tile_rows(int64_t (&off)[kTilePieces], const int
 }
 
 // Gate/up: x as two precomputed fp16 terms.
-__device__ __forceinline__ void gu_tile_load(H8 (&hi)[kTilePieces], H8 (&lo)[kTilePieces],
+template <int TP>
+__device__ __forceinline__ void gu_tile_load(H8 (&hi)[TP], H8 (&lo)[TP],
                                              const f16* __restrict__ x_hi,
                                              const f16* __restrict__ x_lo,
-                                             const int64_t (&off)[kTilePieces], int kb,
-                                             bool with_lo) {
+                                             const int64_t (&off)[TP], int kb, bool with_lo) {
 #pragma unroll
-  for (int q = 0; q < kTilePieces; ++q) {
+  for (int q = 0; q < TP; ++q) {
     hi[q] = lo[q] = h8zero();
     if (off[q] >= 0) {
       hi[q] = *reinterpret_cast<const H8*>(x_hi + off[q] + kb);
@@ -212,12 +228,12 @@ __device__ __forceinline__ void gu_tile_load(H8 (&hi)[kTilePieces], H8 (&lo)[kTi
 }
 
 // Down: act rows, fp32, split into two fp16 (or, BF, bf16) terms.
-template <bool BF>
-__device__ __forceinline__ void dn_tile_load(H8 (&hi)[kTilePieces], H8 (&lo)[kTilePieces],
+template <bool BF, int TP>
+__device__ __forceinline__ void dn_tile_load(H8 (&hi)[TP], H8 (&lo)[TP],
                                              const float* __restrict__ act,
-                                             const int64_t (&off)[kTilePieces], int kb) {
+                                             const int64_t (&off)[TP], int kb) {
 #pragma unroll
-  for (int q = 0; q < kTilePieces; ++q) {
+  for (int q = 0; q < TP; ++q) {
     hi[q] = lo[q] = h8zero();
     if (off[q] >= 0) {
       const float* a = act + off[q] + kb;
@@ -240,10 +256,12 @@ __device__ __forceinline__ void dn_tile_load(H8 (&hi)[kTilePieces], H8 (&lo)[kTi
   }
 }
 
-__device__ __forceinline__ void tile_store(TokTile& xs, const H8 (&hi)[kTilePieces],
-                                           const H8 (&lo)[kTilePieces], bool with_lo) {
+template <int TOK, int TP>
+__device__ __forceinline__ void tile_store(TokTile<TOK>& xs, const H8 (&hi)[TP],
+                                           const H8 (&lo)[TP], bool with_lo) {
+  static_assert(TP == tile_pieces<TOK>(), "tile shares");
 #pragma unroll
-  for (int q = 0; q < kTilePieces; ++q) {
+  for (int q = 0; q < TP; ++q) {
     const int i = threadIdx.x + kBlk * q;
     const int n = i / kPieces, c = i % kPieces;
     xs.hi[n][c] = hi[q];
@@ -360,8 +378,8 @@ __device__ __forceinline__ void w_store(WTile<ROWS>& t, const WRegs<WT, ROWS>& r
 // the K loop has no per-tile branches.  A wave's weight tile holds its 16 gate
 // rows (tile rows 0-15) and the same 16 up rows (tile rows 16-31).
 // ---------------------------------------------------------------------------
-template <typename WT, bool LO, int NT>
-__device__ __forceinline__ void gu_pass(TokTile& xs, WTile<32>& wt,
+template <typename WT, bool LO, int NT, int TOK>
+__device__ __forceinline__ void gu_pass(TokTile<TOK>& xs, WTile<32>& wt,
                                         const WT* const (&wbase)[WRegs<WT, 32>::N],
                                         const uint8_t* const (&wsc)[WRegs<WT, 32>::N],
                                         const f16* __restrict__ x_hi,
@@ -371,14 +389,15 @@ __device__ __forceinline__ void gu_pass(TokTile& xs, WTile<32>& wt,
   f32x4 ag[NT], au[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) ag[n] = au[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  int64_t off[kTilePieces];
+  constexpr int TP = tile_pieces<TOK>();
+  int64_t off[TP];
   tile_rows(off, r.pair_tok + p0, 0, mt, g.h);
   const int ns = g.h / kBK;
 
   // Software pipeline, one K step deep: step s+1's weight and token loads are
   // issued before step s's MFMAs.
   WRegs<WT, 32> wr;
-  H8 th[kTilePieces], tl[kTilePieces];
+  H8 th[TP], tl[TP];
   w_load<WT, 32>(wr, wbase, wsc, 0);
   gu_tile_load(th, tl, x_hi, x_lo, off, 0, LO);
   for (int s = 0; s < ns; ++s) {
@@ -438,12 +457,12 @@ __device__ __forceinline__ void gu_pass(TokTile& xs, WTile<32>& wt,
   }
 }
 
-template <typename WT, bool LO>
+template <typename WT, bool LO, int TOK>
 __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
                                                   const f16* __restrict__ x_hi,
                                                   const f16* __restrict__ x_lo, BatchRoute r,
                                                   float* __restrict__ act, Geom g) {
-  __shared__ TokTile xs;
+  __shared__ TokTile<TOK> xs;
   __shared__ WTile<32> wts[kBlk / kWave];
   const int slot = blockIdx.y;
   if (slot >= *r.n_active) return;  // block-uniform
@@ -469,14 +488,23 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
   const float* sc = nullptr;
   if constexpr (std::is_same<WT, fp8w>::value) sc = wscales(blk, g.off_scale);
   WTile<32>& wt = wts[wave];
-  for (int m0 = 0; m0 < M; m0 += kMaxTok) {
-    const int mt = min(kMaxTok, M - m0);
+  for (int m0 = 0; m0 < M; m0 += TOK) {
+    const int mt = min(TOK, M - m0);
     const int p0 = pbeg + m0;
-    switch ((mt + 15) / 16) {
-      case 1: gu_pass<WT, LO, 1>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
-      case 2: gu_pass<WT, LO, 2>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
-      case 3: gu_pass<WT, LO, 3>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
-      default: gu_pass<WT, LO, 4>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
+    if constexpr (TOK == 16) {
+      gu_pass<WT, LO, 1, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane);
+    } else if constexpr (TOK == 32) {
+      if (mt <= 16)
+        gu_pass<WT, LO, 1, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane);
+      else
+        gu_pass<WT, LO, 2, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane);
+    } else {
+      switch ((mt + 15) / 16) {
+        case 1: gu_pass<WT, LO, 1, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
+        case 2: gu_pass<WT, LO, 2, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
+        case 3: gu_pass<WT, LO, 3, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
+        default: gu_pass<WT, LO, 4, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
+      }
     }
   }
 }
@@ -485,8 +513,8 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
 // Down.  grid (h / 64, kKSplit, expert slots).  K slice ks covers steps
 // [nsteps * ks / kKSplit, nsteps * (ks + 1) / kKSplit).
 // ---------------------------------------------------------------------------
-template <typename WT, int NT>
-__device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt,
+template <typename WT, int NT, int TOK>
+__device__ __forceinline__ void dn_pass(TokTile<TOK>& xs, WTile<16>& wt,
                                         const WT* const (&wbase)[WRegs<WT, 16>::N],
                                         const uint8_t* const (&wsc)[WRegs<WT, 16>::N],
                                         const float* __restrict__ act, int p0, int mt, int sb,
@@ -497,10 +525,11 @@ __device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt,
 #pragma unroll
   for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   if (sb < se) {
-    int64_t off[kTilePieces];
+    constexpr int TP = tile_pieces<TOK>();
+    int64_t off[TP];
     tile_rows(off, nullptr, p0, mt, g.I);
     WRegs<WT, 16> wr;
-    H8 th[kTilePieces], tl[kTilePieces];
+    H8 th[TP], tl[TP];
     w_load<WT, 16>(wr, wbase, wsc, sb * kBK);
     dn_tile_load<bf16_ops<WT>()>(th, tl, act, off, sb * kBK);
     for (int s = sb; s < se; ++s) {
@@ -543,11 +572,11 @@ __device__ __forceinline__ void dn_pass(TokTile& xs, WTile<16>& wt,
   }
 }
 
-template <typename WT>
+template <typename WT, int TOK>
 __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, BatchRoute r,
                                                   const float* __restrict__ act,
                                                   float* __restrict__ ypart, Geom g, int P) {
-  __shared__ TokTile xs;
+  __shared__ TokTile<TOK> xs;
   __shared__ WTile<16> wts[kBlk / kWave];
   const int slot = blockIdx.z;
   if (slot >= *r.n_active) return;
@@ -578,13 +607,22 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, B
   }
   float* y = ypart + (int64_t)ks * P * g.h;
   WTile<16>& wt = wts[wave];
-  for (int m0 = 0; m0 < M; m0 += kMaxTok) {
-    const int mt = min(kMaxTok, M - m0);
-    switch ((mt + 15) / 16) {
-      case 1: dn_pass<WT, 1>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-      case 2: dn_pass<WT, 2>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-      case 3: dn_pass<WT, 3>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-      default: dn_pass<WT, 4>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+  for (int m0 = 0; m0 < M; m0 += TOK) {
+    const int mt = min(TOK, M - m0);
+    if constexpr (TOK == 16) {
+      dn_pass<WT, 1, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+    } else if constexpr (TOK == 32) {
+      if (mt <= 16)
+        dn_pass<WT, 1, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+      else
+        dn_pass<WT, 2, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+    } else {
+      switch ((mt + 15) / 16) {
+        case 1: dn_pass<WT, 1, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 2: dn_pass<WT, 2, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 3: dn_pass<WT, 3, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        default: dn_pass<WT, 4, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+      }
     }
   }
 }
@@ -629,11 +667,27 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
   if (err != hipSuccess) return err;
   // The lo term of x: fp32 x, or any x against bf16 (8-bit mantissa) terms.
   constexpr bool LO = std::is_same<XT, float>::value || bf16_ops<WT>();
-  hipLaunchKernelGGL((k_gu_mfma<WT, LO>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s, wb, w.x_hi,
-                     w.x_lo, w.route, w.act, g);
-  if ((err = hipGetLastError()) != hipSuccess) return err;
-  hipLaunchKernelGGL((k_dn_mfma<WT>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s,
-                     wb, w.route, w.act, w.ypart, g, P);
+  // An expert has at most B tokens (a token selects it at most once), so
+  // small batches take token tiles of 16 or 32.
+  if (p.B <= WR_SMALL_TILE_MAX_B) {
+    hipLaunchKernelGGL((k_gu_mfma<WT, LO, 16>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s, wb,
+                       w.x_hi, w.x_lo, w.route, w.act, g);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    hipLaunchKernelGGL((k_dn_mfma<WT, 16>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk),
+                       0, s, wb, w.route, w.act, w.ypart, g, P);
+  } else if (p.B <= WR_MID_TILE_MAX_B) {
+    hipLaunchKernelGGL((k_gu_mfma<WT, LO, 32>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s, wb,
+                       w.x_hi, w.x_lo, w.route, w.act, g);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    hipLaunchKernelGGL((k_dn_mfma<WT, 32>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk),
+                       0, s, wb, w.route, w.act, w.ypart, g, P);
+  } else {
+    hipLaunchKernelGGL((k_gu_mfma<WT, LO, kMaxTok>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s,
+                       wb, w.x_hi, w.x_lo, w.route, w.act, g);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    hipLaunchKernelGGL((k_dn_mfma<WT, kMaxTok>), dim3(p.h / kBM, BatchWs::kKSplit, slots),
+                       dim3(kBlk), 0, s, wb, w.route, w.act, w.ypart, g, P);
+  }
   if ((err = hipGetLastError()) != hipSuccess) return err;
   hipLaunchKernelGGL((k_combine<XT>), dim3((p.h + kBlk - 1) / kBlk, p.B), dim3(kBlk), 0, s,
                      w.ypart, w.route, static_cast<XT*>(p.out), p.h, p.k, P);
