@@ -40,6 +40,9 @@ SMALL = [
     (5, 100, 36, 2, F16, True),
     (3, 33, 17, 3, F16, False),    # odd shapes, k == E
     (1, 64, 64, 1, F16, False),    # single expert
+    (8, 264, 520, 2, F16, True),   # x staged in LDS, partial last chunk of a row
+    (4, 8200, 64, 2, F16, False),  # h above the LDS copy's bound: x from registers
+    (8, 256, 8448, 2, F16, False), # 1056 gate/up blocks, over 4 per CU: x from registers
 ]
 
 
