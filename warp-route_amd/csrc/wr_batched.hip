@@ -314,7 +314,7 @@ template <typename WT, int ROWS>
 struct WRegs {
   static constexpr int N = ROWS / WGeo<WT>::kRowsPer;  // load instructions per K step
   u32x4 v[N];
-  float s[std::is_same<WT, fp4x2>::value ? N : 1];     // MXFP4 block scales
+  uint32_t e[std::is_same<WT, fp4x2>::value ? N : 1];  // MXFP4 E8M0 scale bytes
 };
 
 // Loads of one K step: base[i] is this lane's address for row group i at
@@ -327,7 +327,7 @@ __device__ __forceinline__ void w_load(WRegs<WT, ROWS>& r,
 #pragma unroll
   for (int i = 0; i < WRegs<WT, ROWS>::N; ++i) {
     r.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base[i] + eoff<WT>(kb)));
-    if constexpr (std::is_same<WT, fp4x2>::value) r.s[i] = e8m0_value(sc[i][kb / 32]);
+    if constexpr (std::is_same<WT, fp4x2>::value) r.e[i] = sc[i][kb / 32];
   }
 }
 
@@ -360,8 +360,9 @@ __device__ __forceinline__ void w_store(WTile<ROWS>& t, const WRegs<WT, ROWS>& r
     const int row = RP * i + lane / LR;
     if constexpr (std::is_same<WT, fp4x2>::value) {
       const int c = 4 * (lane % LR);
+      const float s = e8m0_value(r.e[i]);
 #pragma unroll
-      for (int p = 0; p < 4; ++p) t.w[row][c + p] = fp4x8_to_h8(r.v[i][p], r.s[i]);
+      for (int p = 0; p < 4; ++p) t.w[row][c + p] = fp4x8_to_h8(r.v[i][p], s);
     } else if constexpr (std::is_same<WT, fp8w>::value) {
       const int c = 2 * (lane % LR);
       t.w[row][c] = fp8x8_to_h8(r.v[i][0], r.v[i][1]);

@@ -49,16 +49,19 @@ __host__ __device__ constexpr int64_t eoff(int64_t elems) {
   return elems / epu<WT>();
 }
 
-// A loaded MXFP4 vector: its codes and the fp32 value of its block scale.
+// A loaded MXFP4 vector: its codes and the raw E8M0 byte of its block scale.
 // Vectors never straddle a 32-element block (32 elements per 16 bytes, or
-// 2 per byte on the unaligned path).
+// 2 per byte on the unaligned path).  The byte is turned into an fp32 scale
+// where the codes are decoded, not where it is loaded: a conversion next to
+// the load (which sits in a branch when the load is conditional) would make
+// the wave wait for the byte before it issues its next loads.
 struct fp4v32 {
   u32x4 q;
-  float s;
+  uint32_t e;
 };
 struct fp4v2 {
   uint8_t q;
-  float s;
+  uint32_t e;
 };
 
 // E8M0 scale byte -> 2^(e - 127) as fp32 (e = 0 is the subnormal 2^-127;
@@ -131,6 +134,14 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 struct TopK {
   int id[WR_MAX_TOPK];
   float w[WR_MAX_TOPK];
+  // The same selection spread over lanes (lane kk holds slot kk, lanes past
+  // the last slot hold id 0 and weight 0), for reads with a runtime slot
+  // index: a v_readlane into a scalar register.  A select chain over the
+  // arrays can be folded back into a runtime-indexed array, which then
+  // lives in scratch memory, and a scratch load's wait also waits for every
+  // weight load issued before it.
+  int lid;
+  float lw;
 };
 
 // `l` is this lane's logit (lane e holds expert e; lanes >= E are ignored).
@@ -145,6 +156,8 @@ __device__ __forceinline__ void wave_select_topk_reg(float l_in, int E, int k, i
   const float p = ex / s;
   bool avail = valid;
   float tot = 0.0f;
+  t.lid = 0;
+  t.lw = 0.0f;
 #pragma unroll
   for (int kk = 0; kk < WR_MAX_TOPK; ++kk) {
     t.id[kk] = 0;
@@ -157,6 +170,10 @@ __device__ __forceinline__ void wave_select_topk_reg(float l_in, int E, int k, i
       const float wv = mask ? best : -3.402823466e38f;
       t.id[kk] = __builtin_amdgcn_readfirstlane(id);
       t.w[kk] = wv;
+      if (lane == kk) {
+        t.lid = t.id[kk];
+        t.lw = wv;
+      }
       tot += wv;
       if (lane == id) avail = false;
     }
@@ -165,6 +182,7 @@ __device__ __forceinline__ void wave_select_topk_reg(float l_in, int E, int k, i
 #pragma unroll
     for (int kk = 0; kk < WR_MAX_TOPK; ++kk)
       if (kk < k) t.w[kk] = t.w[kk] / tot;
+    if (lane < k) t.lw = t.lw / tot;
   }
 }
 
@@ -243,17 +261,18 @@ __device__ __forceinline__ void invalidate_l1() {
   asm volatile("buffer_inv sc0\n\ts_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// Runtime-index read of a TopK field without a scratch-memory array.
+// Runtime-index read of a TopK slot (kk wave-uniform, 0 <= kk < WR_MAX_TOPK).
 __device__ __forceinline__ int topk_id(const TopK& t, int kk) {
-  int r = t.id[0];
-#pragma unroll
-  for (int i = 1; i < WR_MAX_TOPK; ++i) r = (kk == i) ? t.id[i] : r;
-  return r;
+  return __builtin_amdgcn_readlane(t.lid, kk);
 }
 __device__ __forceinline__ float topk_w(const TopK& t, int kk) {
-  float r = t.w[0];
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t.lw), kk));
+}
+// Same for a slot index that may differ across the lanes of a wave.
+__device__ __forceinline__ int topk_id_lanes(const TopK& t, int kk) {
+  int r = __builtin_amdgcn_readlane(t.lid, 0);
 #pragma unroll
-  for (int i = 1; i < WR_MAX_TOPK; ++i) r = (kk == i) ? t.w[i] : r;
+  for (int i = 1; i < WR_MAX_TOPK; ++i) r = (kk == i) ? __builtin_amdgcn_readlane(t.lid, i) : r;
   return r;
 }
 
@@ -311,7 +330,7 @@ __device__ __forceinline__ typename WVec<T, VEC>::type load_wq(const T* p, const
       v.q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
     else
       v.q = __builtin_nontemporal_load(reinterpret_cast<const uint8_t*>(p));
-    v.s = e8m0_value(*sc);
+    v.e = *sc;
     return v;
   } else {
     (void)sc;
@@ -337,16 +356,17 @@ __device__ __forceinline__ float wdec(const V& v, int i) {
   if constexpr (std::is_same<WT, fp4x2>::value) {
     // v_cvt_scalef32_pk_f32_fp4: the two codes of one byte, times the scale
     // (checked against the E2M1 table for every byte on gfx950).
+    const float sc = e8m0_value(v.e);
     if constexpr (std::is_same<V, fp4v2>::value) {
-      return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((uint32_t)v.q, v.s, 0)[i & 1];
+      return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((uint32_t)v.q, sc, 0)[i & 1];
     } else {
       const uint32_t w = v.q[i >> 3];
       f32x2 pr;
       switch ((i >> 1) & 3) {
-        case 0: pr = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, v.s, 0); break;
-        case 1: pr = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, v.s, 1); break;
-        case 2: pr = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, v.s, 2); break;
-        default: pr = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, v.s, 3); break;
+        case 0: pr = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 0); break;
+        case 1: pr = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 1); break;
+        case 2: pr = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 2); break;
+        default: pr = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, 3); break;
       }
       return pr[i & 1];
     }
@@ -381,9 +401,9 @@ __device__ __forceinline__ const float* wscales(const WT* blk, int64_t off_scale
 template <typename V>
 __device__ __forceinline__ V vzero() {
   if constexpr (std::is_same<V, fp4v32>::value) {
-    return fp4v32{u32x4{0u, 0u, 0u, 0u}, 1.0f};
+    return fp4v32{u32x4{0u, 0u, 0u, 0u}, 127u};  // scale 1
   } else if constexpr (std::is_same<V, fp4v2>::value) {
-    return fp4v2{0, 1.0f};
+    return fp4v2{0, 127u};
   } else if constexpr (std::is_same<V, f16>::value || std::is_same<V, float>::value ||
                        std::is_integral<V>::value) {
     return V(0);

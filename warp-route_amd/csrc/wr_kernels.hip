@@ -87,6 +87,9 @@
 #ifndef WR_F4_U1
 #define WR_F4_U1 1   // gate/up column chunks per row per iteration (4 rows per wave)
 #endif
+#ifndef WR_F4_RPW
+#define WR_F4_RPW 4  // gate/up rows per wave (4 or 8)
+#endif
 #ifndef WR_F4_RPD
 #define WR_F4_RPD 8  // output rows per down block
 #endif
@@ -841,7 +844,10 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   if constexpr (kFp8) {
     // Published to the block by the __syncthreads after the wait below.
     const int i = threadIdx.x, kk = i / RPD, j = i % RPD;
-    if (kk < g.k) sdn[i] = j < nrows ? down_scale(wbuf, g, t, kk, r0 + j) : 0.0f;
+    if (kk < g.k)
+      sdn[i] = j < nrows ? wscales(wbuf + (int64_t)topk_id_lanes(t, kk) * g.stride,
+                                   g.off_scale)[2 * g.I + r0 + j]
+                         : 0.0f;
   }
 
   if (wave == 0) {
@@ -973,7 +979,7 @@ hipError_t logits_t(const Problem& p, float* logits, unsigned* zero, int nzero, 
 int fused_rpw(const Problem& p) {
   const int64_t row_bytes = (int64_t)p.h * weight_es(p.wdt);
   if (p.wdt == WR_FP8_E4M3) return p.vec > 1 ? WR_F8_RPW : 2;
-  if (p.wdt == WR_MXFP4) return p.vec == 32 ? 4 : 2;
+  if (p.wdt == WR_MXFP4) return p.vec == 32 ? WR_F4_RPW : 2;
   return (p.vec > 1 && row_bytes <= 4096) ? 4 : 2;
 }
 
@@ -1040,6 +1046,9 @@ constexpr int fused_u1() {
 
 template <typename WT, typename XT, int VEC>
 hipError_t fused_t(const Problem& p, const FusedWs& w, hipStream_t s) {
+  if constexpr (std::is_same<WT, fp4x2>::value && WR_F4_RPW == 8 && VEC == 32) {
+    if (fused_rpw(p) == 8) return fused_rpw_t<WT, XT, VEC, 8, fused_u1<WT, 8>()>(p, w, s);
+  }
   if (fused_rpw(p) == 4) return fused_rpw_t<WT, XT, VEC, 4, fused_u1<WT, 4>()>(p, w, s);
   return fused_rpw_t<WT, XT, VEC, 2, fused_u1<WT, 2>()>(p, w, s);
 }
