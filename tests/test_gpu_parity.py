@@ -102,6 +102,8 @@ LOWP = [
     (64, 256, 512, 6, MX4, False),
     (16, 512, 1024, 4, MX4, True),
     (8, 4096, 1024, 2, MX4, True),    # 2 KB code rows
+    (8, 6144, 512, 2, MX4, False),    # 3 KB code rows: x staged in LDS up to h = 6144
+    (4, 6176, 256, 2, MX4, True),     # h just above the MXFP4 LDS copy: x from registers
     (5, 96, 64, 2, MX4, False),       # three and two blocks per row, k == 2 of 5
 ]
 
@@ -417,9 +419,9 @@ def _fused_args(x, gw, buf, E, h, I, k, out, work, renorm=0):
 @pytest.mark.parametrize("shape", [(16, 512, 256, 4, F16), (8, 4096, 14336, 2, F16),
                                    (64, 2048, 1408, 6, F16), (8, 192, 100, 3, F16),
                                    (8, 4096, 14336, 2, FP8), (16, 6144, 10752, 4, FP8),
-                                   (8, 4096, 14336, 2, MX4)],
+                                   (8, 4096, 14336, 2, MX4), (16, 6144, 10752, 4, MX4)],
                          ids=["small", "mixtral", "deepseek", "ragged", "mixtral-fp8",
-                              "dbrx-fp8", "mixtral-mxfp4"])
+                              "dbrx-fp8", "mixtral-mxfp4", "dbrx-mxfp4"])
 def test_fused_handoff_never_times_out(cuda, shape):
     """Single-token fused kernel: every gate/up block incremented its arrival
     counter (64 counters, 256 bytes apart) and no down block's bounded wait

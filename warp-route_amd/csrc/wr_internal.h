@@ -46,7 +46,7 @@ struct FusedWs {
   static constexpr size_t kCtrlBytes = (size_t)kCtrlWords * kCounterStride * 4;
   // Single-token act rows: I rounded up to whole chunks of `cols` columns, the
   // columns one gate/up block computes (4 waves x rows per wave: 8 or 16).
-  static constexpr int kMaxActCols = 32;
+  static constexpr int kMaxActCols = 16;
 
   unsigned* ctrl;  // kCtrlBytes
   float* logits;   // [B][WR_MAX_EXPERTS]: token b's E logits, padded to 64

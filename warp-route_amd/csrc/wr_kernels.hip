@@ -68,7 +68,7 @@
 // x staged in LDS by the gate/up blocks of the single-token fused kernel, for
 // h up to these bounds (0: never); fp8, fp16 and bf16 also need at most
 // WR_XL_FP8_BPC gate/up blocks per CU.  Measured: it gains for MXFP4 up to
-// h = 4096, and for the other types when the gate/up blocks fit in one round
+// h = 6144, and for the other types when the gate/up blocks fit in one round
 // of residency (DeepSeek, Mixtral shards); it costs with many rounds (Mixtral,
 // 3584 blocks) or at h = 6144.
 #ifndef WR_XL_FP8_MAXH
@@ -81,14 +81,11 @@
 #define WR_XL_FP8_BPC 4
 #endif
 #ifndef WR_XL_FP4_MAXH
-#define WR_XL_FP4_MAXH 4096
+#define WR_XL_FP4_MAXH 6144
 #endif
 // MXFP4 weights in the single-token fused kernel (32 weights per 128-bit load)
 #ifndef WR_F4_U1
 #define WR_F4_U1 1   // gate/up column chunks per row per iteration (4 rows per wave)
-#endif
-#ifndef WR_F4_RPW
-#define WR_F4_RPW 4  // gate/up rows per wave (4 or 8)
 #endif
 #ifndef WR_F4_RPD
 #define WR_F4_RPD 8  // output rows per down block
@@ -248,12 +245,33 @@ __device__ __forceinline__ const uint8_t* mx_at(const uint8_t* row, int64_t c) {
 // up dot products gs and us and the gate weight wk:
 //   wk * silu(gs) * us                                  (unscaled types)
 //   wk * silu(gs * s_gate[r]) * (us * s_up[r])          (fp8 row scales)
-template <typename WT>
-__device__ __forceinline__ float act_value(const WT* blk, const Geom& g, int r, float wk,
-                                           float gs, float us) {
+// The fp8 scales of rows [r0, r0 + RPW) are loaded by every lane, with the
+// item's weights and outside any branch, so that the epilogue waits for
+// them once (rows past nrows repeat a valid row; their values are unused).
+template <typename WT, int RPW>
+struct RowScales {
+  float gate[RPW], up[RPW];
+};
+template <typename WT, int RPW>
+__device__ __forceinline__ void load_row_scales(RowScales<WT, RPW>& rs, const WT* blk,
+                                                const Geom& g, int r0, int nrows) {
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) rs.gate[j] = rs.up[j] = 1.0f;
   if constexpr (std::is_same<WT, fp8w>::value) {
     const float* sc = wscales(blk, g.off_scale);
-    return wk * (silu(gs * sc[r]) * (us * sc[g.I + r]));
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+      const int r = r0 + max(min(j, nrows - 1), 0);
+      rs.gate[j] = sc[r];
+      rs.up[j] = sc[g.I + r];
+    }
+  }
+}
+template <typename WT, int RPW>
+__device__ __forceinline__ float act_value(const RowScales<WT, RPW>& rs, int j, float wk,
+                                           float gs, float us) {
+  if constexpr (std::is_same<WT, fp8w>::value) {
+    return wk * (silu(gs * rs.gate[j]) * (us * rs.up[j]));
   } else {
     return wk * (silu(gs) * us);
   }
@@ -310,6 +328,8 @@ __global__ __launch_bounds__(kBlock) void k_gateup(const WT* __restrict__ wbuf,
     const WT* G = blk + eoff<WT>((int64_t)r0 * g.h);
     const WT* Up = G + g.off_up;
     const int nrows = min(RPW, g.I - r0);
+    RowScales<WT, RPW> rs;
+    load_row_scales<WT, RPW>(rs, blk, g, r0, nrows);
 
     float ag[RPW], au[RPW];
 #pragma unroll
@@ -356,8 +376,7 @@ __global__ __launch_bounds__(kBlock) void k_gateup(const WT* __restrict__ wbuf,
     for (int j = 0; j < RPW; ++j) {
       const float gs = wave_sum(ag[j]);
       const float us = wave_sum(au[j]);
-      if (lane == 0 && j < nrows) a[j] = act_value<WT>(wbuf + (int64_t)e * g.stride, g, r0 + j,
-                                                       wk, gs, us);
+      if (lane == 0 && j < nrows) a[j] = act_value<WT, RPW>(rs, j, wk, gs, us);
     }
   }
 }
@@ -519,6 +538,8 @@ __device__ __forceinline__ void gateup_item(const WT* __restrict__ wbuf, const X
   const WT* G = blk + eoff<WT>((int64_t)r0 * g.h);
   const WT* Up = G + g.off_up;
   const int nrows = min(RPW, g.I - r0);
+  RowScales<WT, RPW> rs;
+  load_row_scales<WT, RPW>(rs, blk, g, r0, nrows);
   float ag[RPW], au[RPW];
 #pragma unroll
   for (int j = 0; j < RPW; ++j) ag[j] = au[j] = 0.0f;
@@ -562,7 +583,7 @@ __device__ __forceinline__ void gateup_item(const WT* __restrict__ wbuf, const X
     const float gs = wave_sum(ag[j]);
     const float us = wave_sum(au[j]);
     if (lane == 0 && j < nrows)
-      __hip_atomic_store(a + j, act_value<WT>(blk, g, r0 + j, wk, gs, us), __ATOMIC_RELAXED,
+      __hip_atomic_store(a + j, act_value<WT, RPW>(rs, j, wk, gs, us), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -571,10 +592,18 @@ __device__ __forceinline__ void gateup_item(const WT* __restrict__ wbuf, const X
 // copy is made of 16-byte slots; each VEC-element group of x (DS = VEC / E16
 // slots, E16 elements per slot) is followed by one pad slot, so that the VEC
 // values of lane l start at l (DS + 1) slots and the ds_read_b128s of 16
-// consecutive lanes hit 16 distinct 4-bank groups.  h <= kXlMaxH: the copy
-// is a static array of its size (at most 20 KB, so 4 blocks still fit a CU's
-// LDS), because dynamic LDS keeps the compiler from holding TopK in registers.
-constexpr int kXlMaxH = 4096;
+// consecutive lanes hit 16 distinct 4-bank groups.  h <= xl_max_h<WT>(): the
+// copy is a static array of that size (at most 28 KB, so 4 blocks still fit a
+// CU's LDS), because dynamic LDS keeps the compiler from holding the kernel's
+// small arrays in registers.
+template <typename WT>
+constexpr int xl_max_h() {
+  if constexpr (std::is_same<WT, fp8w>::value) return WR_XL_FP8_MAXH;
+  if constexpr (std::is_same<WT, fp4x2>::value) return WR_XL_FP4_MAXH;
+  if constexpr (std::is_same<WT, f16>::value || std::is_same<WT, bf16w>::value)
+    return WR_XL_F16_MAXH;
+  return 0;
+}
 template <typename XT, int VEC>
 struct XlLayout {
   static constexpr int kE16 = 16 / (int)sizeof(XT);  // x elements per slot
@@ -624,7 +653,7 @@ __device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
   typedef typename WVec<WT, VEC>::type V;
   typedef XlLayout<XT, VEC> L;
   constexpr int CH = kWave * VEC;
-  __shared__ __align__(16) unsigned char xs_raw[L::bytes(kXlMaxH)];
+  __shared__ __align__(16) unsigned char xs_raw[L::bytes(xl_max_h<WT>())];
   const WT* blk = wbuf + (int64_t)eid * g.stride;
   const WT* G = blk + eoff<WT>((int64_t)r0 * g.h);
   const WT* Up = G + g.off_up;
@@ -647,6 +676,8 @@ __device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
   }
   V wg[U][RPW], wu[U][RPW];
   gateup_issue<WT, VEC, RPW, U>(wg, wu, blk, G, Up, g, r0, nrows, lane * VEC);
+  RowScales<WT, RPW> rs;
+  load_row_scales<WT, RPW>(rs, blk, g, r0, nrows);
   __builtin_amdgcn_s_waitcnt(0);  // the copy's loads (and the weights) have landed
   __syncthreads();
 
@@ -691,7 +722,7 @@ __device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
     const float gs = wave_sum(ag[j]);
     const float us = wave_sum(au[j]);
     if (lane == 0 && j < nrows)
-      __hip_atomic_store(a + j, act_value<WT>(blk, g, r0 + j, wk, gs, us), __ATOMIC_RELAXED,
+      __hip_atomic_store(a + j, act_value<WT, RPW>(rs, j, wk, gs, us), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -979,7 +1010,7 @@ hipError_t logits_t(const Problem& p, float* logits, unsigned* zero, int nzero, 
 int fused_rpw(const Problem& p) {
   const int64_t row_bytes = (int64_t)p.h * weight_es(p.wdt);
   if (p.wdt == WR_FP8_E4M3) return p.vec > 1 ? WR_F8_RPW : 2;
-  if (p.wdt == WR_MXFP4) return p.vec == 32 ? WR_F4_RPW : 2;
+  if (p.wdt == WR_MXFP4) return p.vec == 32 ? 4 : 2;
   return (p.vec > 1 && row_bytes <= 4096) ? 4 : 2;
 }
 
@@ -1014,10 +1045,7 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   const int n2 = (p.h + RPD - 1) / RPD;
   // Gate/up blocks read x from an LDS copy for small enough h (and, except
   // for MXFP4, few enough gate/up blocks).
-  constexpr bool k16 = std::is_same<WT, f16>::value || std::is_same<WT, bf16w>::value;
-  constexpr int kXlMax =
-      kFp8 ? WR_XL_FP8_MAXH : (kFp4 ? WR_XL_FP4_MAXH : (k16 ? WR_XL_F16_MAXH : 0));
-  static_assert(kXlMax <= kXlMaxH, "the LDS copy holds at most kXlMaxH elements");
+  constexpr int kXlMax = xl_max_h<WT>();
   constexpr bool kXl = kXlMax > 0 && VEC >= 8;
   if constexpr (kXl) {
     if (p.h <= kXlMax && (kFp4 || hs.n1 <= WR_XL_FP8_BPC * cu_count())) {
@@ -1046,9 +1074,6 @@ constexpr int fused_u1() {
 
 template <typename WT, typename XT, int VEC>
 hipError_t fused_t(const Problem& p, const FusedWs& w, hipStream_t s) {
-  if constexpr (std::is_same<WT, fp4x2>::value && WR_F4_RPW == 8 && VEC == 32) {
-    if (fused_rpw(p) == 8) return fused_rpw_t<WT, XT, VEC, 8, fused_u1<WT, 8>()>(p, w, s);
-  }
   if (fused_rpw(p) == 4) return fused_rpw_t<WT, XT, VEC, 4, fused_u1<WT, 4>()>(p, w, s);
   return fused_rpw_t<WT, XT, VEC, 2, fused_u1<WT, 2>()>(p, w, s);
 }
