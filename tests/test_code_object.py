@@ -1,0 +1,108 @@
+"""Resource checks on the gfx950 code object built here (no GPU needed).
+
+The kernels' speed rests on properties the source does not show:
+- no kernel may keep an array in scratch memory (a scratch load's wait also
+  waits for every weight load issued before it, since vmcnt counts in order)
+  or spill;
+- the register-path kernels may not hold a per-thread array in LDS;
+- the fp16 / bf16 / MXFP4 single-token kernels must fit 128 VGPRs (4 waves
+  per SIMD).
+The compiler has broken the first two silently, by folding a select chain
+over the TopK arrays back into a runtime-indexed array (in scratch memory in
+the x-in-LDS kernels, in LDS in the others).  These tests read the kernel
+descriptors' metadata (the AMDGPU note in the code object of
+libwarp_route_hip.so) with the ROCm LLVM tools.
+"""
+import os
+import re
+import subprocess
+
+import pytest
+
+from warp_route import capi
+
+LLVM = "/opt/rocm/llvm/bin"
+TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
+
+
+def _tool(name):
+    path = os.path.join(LLVM, name)
+    if not os.access(path, os.X_OK):
+        pytest.skip(f"{path} not available")
+    return path
+
+
+@pytest.fixture(scope="module")
+def kernels(tmp_path_factory):
+    """{kernel symbol: {metadata key: int}} of every kernel in the library."""
+    if not os.path.exists(capi.LIB_PATH):
+        pytest.fail(f"{capi.LIB_PATH} is not built (run __graft_entry__.build())")
+    d = tmp_path_factory.mktemp("codeobj")
+    fat = d / "fat.bin"
+    subprocess.run([_tool("llvm-objcopy"), f"--dump-section=.hip_fatbin={fat}", capi.LIB_PATH,
+                    str(d / "host.so")], check=True, capture_output=True)
+    # One offload bundle per translation unit with device code, back to back.
+    blob = fat.read_bytes()
+    starts = [m.start() for m in re.finditer(rb"__CLANG_OFFLOAD_BUNDLE__", blob)]
+    assert starts and starts[0] == 0, "no offload bundle in .hip_fatbin"
+    out = {}
+    for i, s in enumerate(starts):
+        part, co = d / f"bundle{i}.bin", d / f"gfx950_{i}.elf"
+        part.write_bytes(blob[s:starts[i + 1] if i + 1 < len(starts) else len(blob)])
+        subprocess.run([_tool("clang-offload-bundler"), "--unbundle", "--type=o",
+                        f"--input={part}", f"--targets={TARGET}", f"--output={co}"],
+                       check=True, capture_output=True)
+        notes = subprocess.run([_tool("llvm-readelf"), "--notes", str(co)], check=True,
+                               capture_output=True, text=True).stdout
+        # Each kernel is one item of the amdhsa.kernels list, its keys in
+        # alphabetical order (.group_segment_fixed_size comes before .name).
+        m = re.search(r"^(\s*)amdhsa\.kernels:\s*$", notes, re.M)
+        assert m, "no amdhsa.kernels in the code object notes"
+        item = re.compile(rf"^{m.group(1)}  - \.")
+        rec = None
+        for line in notes[m.end():].splitlines():
+            if item.match(line):
+                rec = {}
+            kv = re.match(rf"^{m.group(1)}  (?:- |  )\.(\w+):\s+(\S+)\s*$", line)
+            if rec is None or not kv:
+                continue
+            key, val = kv.groups()
+            if key == "name":
+                out[val] = rec
+            elif re.fullmatch(r"-?\d+", val):
+                rec.setdefault(key, int(val))
+    assert any("k_fused_ffn" in k for k in out) and any("k_gu_mfma" in k for k in out), \
+        f"expected kernels missing from the code object ({len(out)} found)"
+    return out
+
+
+def test_no_kernel_uses_scratch_memory_or_spills(kernels):
+    bad = {k: (v.get("private_segment_fixed_size"), v.get("vgpr_spill_count"))
+           for k, v in kernels.items()
+           if v.get("private_segment_fixed_size", 0) != 0 or v.get("vgpr_spill_count", 0) != 0}
+    assert not bad, f"kernels with scratch memory or VGPR spills: {bad}"
+
+
+def test_single_token_kernels_keep_four_waves_per_simd(kernels):
+    # k_fused_ffn<WT, XT, VEC, ...> with 16-byte vectors: f16 / bf16 (VEC 8)
+    # and MXFP4 (VEC 32).  fp8 keeps 3 waves by design (16 fp32 x values
+    # per chunk and lane on the register path).
+    fused = {k: v["vgpr_count"] for k, v in kernels.items()
+             if "k_fused_ffn" in k and re.search(r"(DF16_|bf16w)E\w*?Li8E|fp4x2E\w*?Li32E", k)}
+    assert len(fused) >= 8, sorted(fused)
+    over = {k: n for k, n in fused.items() if n > 128}
+    assert not over, f"single-token kernels above 128 VGPRs: {over}"
+
+
+def test_register_path_kernels_hold_no_per_thread_arrays_in_lds(kernels):
+    # Without x staged in LDS (k_fused_ffn<..., false>, k_gateup, k_down) a
+    # kernel's LDS is its few block-shared words (partial sums, fp8 down
+    # scales, the logits of E > 16).  A per-thread array promoted to LDS
+    # adds 256 copies of itself (the TopK selection, 48 bytes, once took
+    # 12 KB there, and every read of it waited between weight loads).
+    reg = {k: v.get("group_segment_fixed_size", 0) for k, v in kernels.items()
+           if ("k_fused_ffn" in k and re.search(r"Lb0EEEv", k)) or "k_gateup" in k
+           or "k_down" in k}
+    assert len(reg) >= 16, sorted(reg)
+    big = {k: n for k, n in reg.items() if n > 1024}
+    assert not big, f"register-path kernels with more than 1 KB of LDS: {big}"
