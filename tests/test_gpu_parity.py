@@ -427,7 +427,7 @@ def test_fused_handoff_never_times_out(cuda, shape):
     counter (64 counters, 256 bytes apart) and no down block's bounded wait
     expired (timeout word after the counters).  Gate/up blocks = act chunks
     k * ceil(ceil(I / rpw) / 4), rounded up to a multiple of 8 * 32 / (4 rpw),
-    with rpw = 4 rows per wave for fp16 rows of at most 4 KB (h <= 2048, 16-byte
+    with rpw = 4 rows per wave for fp16 rows of at most 2 KB (h <= 1024, 16-byte
     vectors) and for all 16-byte-vector fp8 rows, else 2.  The workspace starts as junk: the router kernel must
     zero the control block on every call.  The 64 rotation masks (after the
     timeout word and one unused word) each hold one bit per XCD rotation
@@ -447,7 +447,7 @@ def test_fused_handoff_never_times_out(cuda, shape):
     elif wd == MX4:
         rpw = 4  # 16-byte aligned buffers
     else:
-        rpw = 4 if (h % 8 == 0 and I % 8 == 0 and h * 2 <= 4096) else 2
+        rpw = 4 if (h % 8 == 0 and I % 8 == 0 and h * 2 <= 2048) else 2
     group = 8 * (32 // (4 * rpw))
     n1 = (k * (((I + rpw - 1) // rpw + 3) // 4) + group - 1) // group * group
     for _ in range(3):
