@@ -91,11 +91,65 @@ __device__ __forceinline__ H8 h8zero() {
 // ---------------------------------------------------------------------------
 constexpr int kRouteLds = 4096;
 
+// Groups the P = B k selections (sel_id / sel_w, index q = t k + kk) by
+// expert: off[E + 1], active (experts with pairs, ascending), *na, and for
+// pair p (expert-major, tokens ascending within an expert) pair_tok[p] and
+// pair_w[p], with tok_pair[q] = p.  Ballot prefix sums, no atomics, so the
+// order is deterministic.  cnt and off_s are LDS scratch of E and E + 1
+// ints; the outputs may be LDS or global memory (off may be off_s).  Every
+// thread of the block calls it.
+__device__ __forceinline__ void group_pairs(int P, int E, int k, const int* sel_id,
+                                            const float* sel_w, int* cnt, int* off_s, int* off,
+                                            int* active, int* na, int32_t* pair_tok,
+                                            float* pair_w, int32_t* tok_pair) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  for (int e = wave; e < E; e += nw) {
+    int c = 0;
+    for (int q0 = 0; q0 < P; q0 += kWave) {
+      const int q = q0 + lane;
+      c += __popcll(__ballot(q < P && sel_id[q] == e));
+    }
+    if (lane == 0) cnt[e] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int o = 0, n = 0;
+    for (int e = 0; e < E; ++e) {
+      off_s[e] = o;
+      off[e] = o;
+      if (cnt[e] > 0) active[n++] = e;
+      o += cnt[e];
+    }
+    off_s[E] = o;
+    off[E] = o;
+    *na = n;
+  }
+  __syncthreads();
+  // Stable placement: expert e's pairs in token order.
+  for (int e = wave; e < E; e += nw) {
+    int j = off_s[e];
+    for (int q0 = 0; q0 < P; q0 += kWave) {
+      const int q = q0 + lane;
+      const bool m = q < P && sel_id[q] == e;
+      const unsigned long long mask = __ballot(m);
+      if (m) {
+        const int pos = j + __popcll(mask & ((1ull << lane) - 1ull));
+        pair_tok[pos] = q / k;
+        pair_w[pos] = sel_w[q];
+        tok_pair[q] = pos;
+      }
+      j += __popcll(mask);
+    }
+  }
+}
+
 __global__ __launch_bounds__(1024) void k_route(const float* __restrict__ logits, int B, int E,
                                                 int k, int renorm, int32_t* __restrict__ ids_out,
                                                 float* __restrict__ w_out, BatchRoute r) {
   __shared__ int s_cnt[WR_MAX_EXPERTS];
-  __shared__ int s_off[WR_MAX_EXPERTS];
+  __shared__ int s_off[WR_MAX_EXPERTS + 1];
   __shared__ int s_id[kRouteLds];
   __shared__ float s_w[kRouteLds];
   const int lane = threadIdx.x & (kWave - 1);
@@ -133,46 +187,76 @@ __global__ __launch_bounds__(1024) void k_route(const float* __restrict__ logits
     }
   }
   __syncthreads();
+  group_pairs(P, E, k, sel_id, sel_w, s_cnt, s_off, r.off, r.active, r.n_active, r.pair_tok,
+              r.pair_w, r.tok_pair);
+}
 
-  // Pairs per expert.
-  for (int e = wave; e < E; e += nw) {
-    int cnt = 0;
-    for (int q0 = 0; q0 < P; q0 += kWave) {
-      const int q = q0 + lane;
-      cnt += __popcll(__ballot(q < P && sel_id[q] == e));
-    }
-    if (lane == 0) s_cnt[e] = cnt;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int off = 0, na = 0;
-    for (int e = 0; e < E; ++e) {
-      s_off[e] = off;
-      r.off[e] = off;
-      if (s_cnt[e] > 0) r.active[na++] = e;
-      off += s_cnt[e];
-    }
-    r.off[E] = off;
-    *r.n_active = na;
-  }
-  __syncthreads();
+// In-block routing for small batches (B <= WR_SMALL_TILE_MAX_B): every
+// gate/up block selects the B tokens' experts and groups the pairs itself,
+// in LDS, instead of waiting for a separate k_route launch.  The selection
+// is the same wave_select_topk_reg, so ids and weights are bit-identical.
+constexpr int kSmallPairs = WR_SMALL_TILE_MAX_B * WR_MAX_TOPK;
+struct SmallRoute {
+  int cnt[WR_MAX_EXPERTS];
+  int off[WR_MAX_EXPERTS + 1];
+  int active[WR_MAX_EXPERTS];
+  int na;
+  int sel_id[kSmallPairs];
+  float sel_w[kSmallPairs];
+  int32_t pair_tok[kSmallPairs];
+  float pair_w[kSmallPairs];
+  int32_t tok_pair[kSmallPairs];
+};
 
-  // Stable placement: expert e's pairs in token order.
-  for (int e = wave; e < E; e += nw) {
-    int j = s_off[e];
-    for (int q0 = 0; q0 < P; q0 += kWave) {
-      const int q = q0 + lane;
-      const bool m = q < P && sel_id[q] == e;
-      const unsigned long long mask = __ballot(m);
-      if (m) {
-        const int pos = j + __popcll(mask & ((1ull << lane) - 1ull));
-        r.pair_tok[pos] = q / k;
-        r.pair_w[pos] = sel_w[q];
-        r.tok_pair[q] = pos;
+__device__ __forceinline__ void route_small(SmallRoute& sr, const float* __restrict__ logits,
+                                            int B, int E, int k, int renorm) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  constexpr int nw = kBlk / kWave;
+  constexpr int kPer = (WR_SMALL_TILE_MAX_B + nw - 1) / nw;  // tokens per wave, at most
+  float l[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {  // all loads in flight before the first selection
+    const int t = wave + i * nw;
+    l[i] = t < B ? logits[(int64_t)t * WR_MAX_EXPERTS + lane] : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int t = wave + i * nw;
+    if (t < B) {  // wave-uniform
+      TopK tk;
+      wave_select_topk_reg(l[i], E, k, renorm, tk);
+      if (lane < k) {
+        sr.sel_id[t * k + lane] = tk.lid;
+        sr.sel_w[t * k + lane] = tk.lw;
       }
-      j += __popcll(mask);
     }
   }
+  __syncthreads();
+  group_pairs(B * k, E, k, sr.sel_id, sr.sel_w, sr.cnt, sr.off, sr.off, sr.active, &sr.na,
+              sr.pair_tok, sr.pair_w, sr.tok_pair);
+  __syncthreads();
+}
+
+// Block (0, 0)'s copy of the routing, for the down and combine kernels (and
+// the caller's ids and weights).
+__device__ __forceinline__ void route_small_publish(const SmallRoute& sr, int B, int E, int k,
+                                                    const BatchRoute& r,
+                                                    int32_t* __restrict__ ids_out,
+                                                    float* __restrict__ w_out) {
+  const int P = B * k;
+  for (int i = threadIdx.x; i < P; i += kBlk) {
+    r.pair_tok[i] = sr.pair_tok[i];
+    r.pair_w[i] = sr.pair_w[i];
+    r.tok_pair[i] = sr.tok_pair[i];
+    if (ids_out != nullptr) ids_out[i] = sr.sel_id[i];
+    if (w_out != nullptr) w_out[i] = sr.sel_w[i];
+  }
+  for (int e = threadIdx.x; e <= E; e += kBlk) {
+    r.off[e] = sr.off[e];
+    if (e < E) r.active[e] = sr.active[e];
+  }
+  if (threadIdx.x == 0) *r.n_active = sr.na;
 }
 
 // ---------------------------------------------------------------------------
@@ -458,17 +542,48 @@ __device__ __forceinline__ void gu_pass(TokTile<TOK>& xs, WTile<32>& wt,
   }
 }
 
-template <typename WT, bool LO, int TOK>
+// SmallRoute in LDS, for the ROUTE variant only.
+template <bool ROUTE>
+struct GuRouteLds {
+  SmallRoute sr;
+};
+template <>
+struct GuRouteLds<false> {};
+
+// ROUTE: the block routes the batch itself (route_small) instead of reading
+// k_route's output; block (0, 0) publishes the routing for the later kernels.
+template <typename WT, bool LO, int TOK, bool ROUTE>
 __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
                                                   const f16* __restrict__ x_hi,
                                                   const f16* __restrict__ x_lo, BatchRoute r,
-                                                  float* __restrict__ act, Geom g) {
+                                                  float* __restrict__ act, Geom g,
+                                                  const float* __restrict__ logits,
+                                                  int32_t* __restrict__ ids_out,
+                                                  float* __restrict__ w_out) {
   __shared__ TokTile<TOK> xs;
   __shared__ WTile<32> wts[kBlk / kWave];
+  __shared__ GuRouteLds<ROUTE> rl;
   const int slot = blockIdx.y;
-  if (slot >= *r.n_active) return;  // block-uniform
-  const int e = r.active[slot];
-  const int pbeg = r.off[e], M = r.off[e + 1] - pbeg;
+  int e, pbeg, M;
+  if constexpr (ROUTE) {
+    route_small(rl.sr, logits, g.B, g.E, g.k, g.renorm);
+    if (blockIdx.x == 0 && blockIdx.y == 0)
+      route_small_publish(rl.sr, g.B, g.E, g.k, r, ids_out, w_out);
+    if (slot >= rl.sr.na) return;  // block-uniform
+    e = rl.sr.active[slot];
+    pbeg = rl.sr.off[e];
+    M = rl.sr.off[e + 1] - pbeg;
+    r.pair_tok = rl.sr.pair_tok;  // the passes read the LDS copy
+    r.pair_w = rl.sr.pair_w;
+  } else {
+    (void)logits;
+    (void)ids_out;
+    (void)w_out;
+    if (slot >= *r.n_active) return;  // block-uniform
+    e = r.active[slot];
+    pbeg = r.off[e];
+    M = r.off[e + 1] - pbeg;
+  }
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int row0 = blockIdx.x * kBM + wave * 16;
@@ -662,29 +777,32 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
   const int slots = std::min(p.E, P);
   const WT* wb = static_cast<const WT*>(p.wbuf);
 
-  hipLaunchKernelGGL(k_route, dim3(1), dim3(1024), 0, s, w.logits, p.B, p.E, p.k, p.renorm,
-                     p.topk_ids, p.topk_w, w.route);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
+  hipError_t err = hipSuccess;
+  // Small batches route inside the gate/up kernel (one launch fewer).
+  if (p.B > WR_SMALL_TILE_MAX_B) {
+    hipLaunchKernelGGL(k_route, dim3(1), dim3(1024), 0, s, w.logits, p.B, p.E, p.k, p.renorm,
+                       p.topk_ids, p.topk_w, w.route);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
   // The lo term of x: fp32 x, or any x against bf16 (8-bit mantissa) terms.
   constexpr bool LO = std::is_same<XT, float>::value || bf16_ops<WT>();
   // An expert has at most B tokens (a token selects it at most once), so
   // small batches take token tiles of 16 or 32.
   if (p.B <= WR_SMALL_TILE_MAX_B) {
-    hipLaunchKernelGGL((k_gu_mfma<WT, LO, 16>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s, wb,
-                       w.x_hi, w.x_lo, w.route, w.act, g);
+    hipLaunchKernelGGL((k_gu_mfma<WT, LO, 16, true>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s,
+                       wb, w.x_hi, w.x_lo, w.route, w.act, g, w.logits, p.topk_ids, p.topk_w);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     hipLaunchKernelGGL((k_dn_mfma<WT, 16>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk),
                        0, s, wb, w.route, w.act, w.ypart, g, P);
   } else if (p.B <= WR_MID_TILE_MAX_B) {
-    hipLaunchKernelGGL((k_gu_mfma<WT, LO, 32>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s, wb,
-                       w.x_hi, w.x_lo, w.route, w.act, g);
+    hipLaunchKernelGGL((k_gu_mfma<WT, LO, 32, false>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s,
+                       wb, w.x_hi, w.x_lo, w.route, w.act, g, nullptr, nullptr, nullptr);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     hipLaunchKernelGGL((k_dn_mfma<WT, 32>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk),
                        0, s, wb, w.route, w.act, w.ypart, g, P);
   } else {
-    hipLaunchKernelGGL((k_gu_mfma<WT, LO, kMaxTok>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s,
-                       wb, w.x_hi, w.x_lo, w.route, w.act, g);
+    hipLaunchKernelGGL((k_gu_mfma<WT, LO, kMaxTok, false>), dim3(p.I / kBM, slots), dim3(kBlk),
+                       0, s, wb, w.x_hi, w.x_lo, w.route, w.act, g, nullptr, nullptr, nullptr);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     hipLaunchKernelGGL((k_dn_mfma<WT, kMaxTok>), dim3(p.h / kBM, BatchWs::kKSplit, slots),
                        dim3(kBlk), 0, s, wb, w.route, w.act, w.ypart, g, P);
