@@ -11,7 +11,9 @@
 //      wave_select_topk as every other path, so ids and weights are
 //      bit-identical to the single-token op) and groups the (token, expert)
 //      pairs by expert, tokens ascending, with ballot prefix sums
-//      (deterministic, no atomics).
+//      (deterministic, no atomics).  For B <= WR_SMALL_TILE_MAX_B there is
+//      no k_route launch: every gate/up block of step 3 does the same
+//      routing in LDS (route_small), and block (0, 0) publishes it.
 //   3. k_gu_mfma: block (row tile, expert slot): 4 waves x 16 gate rows and
 //      the same 16 up rows each, all of the expert's tokens (up to 64 per
 //      pass); the token tile is staged in LDS and shared by the 4 waves.
