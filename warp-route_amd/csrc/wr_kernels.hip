@@ -809,9 +809,8 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   constexpr int LB = 32 / COLS;               // chunks per 128-byte act line
   static_assert(COLS * LB == 32 && COLS <= FusedWs::kMaxActCols, "unsupported rows per wave");
   const int lane = threadIdx.x & (kWave - 1);
-  // With XL, readfirstlane keeps the (wave-uniform) wave index and the TopK
-  // lookups derived from it scalar; without it, that kernel keeps TopK in
-  // scratch memory.
+  // With XL, readfirstlane keeps the (wave-uniform) wave index, and the item
+  // indices derived from it, in SGPRs.
   const int wave = XL ? __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave)
                       : (int)threadIdx.x / kWave;
   const int64_t act_row = FusedWs::act_row(g.I, COLS);
@@ -834,8 +833,8 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
     const int bpk = (items + kWavesPerBlock - 1) / kWavesPerBlock;  // chunks per expert
     const int G = chunk_of_block<LB>(blockIdx.x);
     if constexpr (XL) {
-      // Wave-uniform by construction; readfirstlane keeps them in SGPRs, so
-      // that the TopK lookups stay scalar selects.
+      // Wave-uniform by construction; readfirstlane keeps them in SGPRs (the
+      // TopK reads below take a scalar slot index).
       const int kk = __builtin_amdgcn_readfirstlane(G < hs.chunks ? G / bpk : 0);
       const int it = (G - kk * bpk) * kWavesPerBlock + wave;
       const int nrows = (G < hs.chunks && it < items) ? min(RPW, g.I - it * RPW) : 0;
