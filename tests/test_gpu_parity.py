@@ -212,6 +212,42 @@ def test_exact_tie_known_answers(cuda, op):
     assert ids3[:2] == [2, 6]
 
 
+@pytest.mark.parametrize("E", [8, 24], ids=["E8-rows", "E24-wave"])
+@pytest.mark.parametrize("B", [3, 20], ids=["B3-in-kernel-route", "B20-route-kernel"])
+def test_batched_exact_tie_known_answers(cuda, B, E):
+    """The same ties through the grouped batched path (h and I multiples of
+    128).  B = 3 routes inside the gate/up kernel, B = 20 in k_route; E = 8
+    selects four tokens per wave (one per 16-lane row), E = 24 one token per
+    wave.  Every token must get the answers the single-token op gives."""
+    h, I, k = 128, 128, 3
+    _, gw, buf = make_layer(E, h, I, F16, router_std=0.1, seed=1, device=cuda)
+    print(f"[gpu] batched ties E={E} B={B}", flush=True)
+
+    def run(x, g):
+        ids = torch.empty(B, k, dtype=torch.int32, device=cuda)
+        ws = torch.empty(B, k, dtype=torch.float32, device=cuda)
+        out = F.batched_fused_moe(x, g, buf, E, h, I, k, False, ids, ws)
+        torch.cuda.synchronize()
+        return ids, ws, out
+
+    # 1. x == 0: all logits exactly 0 -> ids 0..k-1, weights 1/E, output 0.
+    ids, ws, out = run(torch.zeros(B, h, device=cuda), gw)
+    assert ids.tolist() == [[0, 1, 2]] * B
+    assert torch.all(ws == torch.tensor(1.0 / E, dtype=torch.float32))
+    assert torch.all(out == 0)
+    # 2. all router rows identical -> ids 0..k-1 for any x.
+    x = torch.randn(B, h, device=cuda)
+    same = gw[0:1].expand(E, h).contiguous()
+    assert run(x, same)[0].tolist() == [[0, 1, 2]] * B
+    # 3. duplicate rows 2 and 6 forced to the top for every token: 2 first.
+    g3 = gw.clone()
+    g3[2] = x[0] / x[0].norm() * 4.0
+    g3[6] = g3[2]
+    x3 = x[0:1].expand(B, h).contiguous()
+    ids3 = run(x3, g3)[0]
+    assert ids3[:, :2].tolist() == [[2, 6]] * B
+
+
 @pytest.mark.parametrize("B", [1, 4, 16, 64])
 @pytest.mark.parametrize("cfg", [(8, 256, 512, 1, F32, False), (8, 256, 512, 2, F32, False),
                                  (16, 512, 1024, 2, F16, True), (64, 256, 512, 6, F16, False)],

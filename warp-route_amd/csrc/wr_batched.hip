@@ -161,28 +161,45 @@ __global__ __launch_bounds__(1024) void k_route(const float* __restrict__ logits
   int* sel_id = P <= kRouteLds ? s_id : r.sel_id;
   float* sel_w = P <= kRouteLds ? s_w : r.sel_w;
 
-  // Selection: lane e holds logit e; a wave's next 4 tokens are loaded at once.
-  for (int t0 = wave; t0 < B; t0 += 4 * nw) {
-    float l[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = t0 + i * nw;
-      l[i] = t < B ? logits[(int64_t)t * WR_MAX_EXPERTS + lane] : 0.0f;
+  // Selection.  E <= 16: four tokens per wave at once, one per 16-lane row
+  // (row_select_topk).  Else lane e holds logit e, and a wave's next 4 tokens
+  // are loaded at once.
+  if (E <= 16) {
+    const int row = lane >> 4, li = lane & 15;
+    for (int t0 = 4 * wave; t0 < B; t0 += 4 * nw) {  // wave-uniform bound
+      const int t = t0 + row;
+      const float l = t < B ? logits[(int64_t)t * WR_MAX_EXPERTS + li] : 0.0f;
+      int sid;
+      float sw;
+      row_select_topk(l, E, k, renorm, sid, sw);
+      if (t < B && li < k) {
+        const int q = t * k + li;
+        sel_id[q] = sid;
+        sel_w[q] = sw;
+        if (ids_out != nullptr) ids_out[q] = sid;
+        if (w_out != nullptr) w_out[q] = sw;
+      }
     }
+  } else {
+    for (int t0 = wave; t0 < B; t0 += 4 * nw) {
+      float l[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = t0 + i * nw;
-      if (t < B) {  // wave-uniform
-        TopK tk;
-        wave_select_topk_reg(l[i], E, k, renorm, tk);
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + i * nw;
+        l[i] = t < B ? logits[(int64_t)t * WR_MAX_EXPERTS + lane] : 0.0f;
+      }
 #pragma unroll
-        for (int kk = 0; kk < WR_MAX_TOPK; ++kk) {
-          if (kk < k && lane == kk) {
-            const int q = t * k + kk;
-            sel_id[q] = tk.id[kk];
-            sel_w[q] = tk.w[kk];
-            if (ids_out != nullptr) ids_out[q] = tk.id[kk];
-            if (w_out != nullptr) w_out[q] = tk.w[kk];
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + i * nw;
+        if (t < B) {  // wave-uniform
+          TopK tk;
+          wave_select_topk_reg(l[i], E, k, renorm, tk);
+          if (lane < k) {
+            const int q = t * k + lane;
+            sel_id[q] = tk.lid;
+            sel_w[q] = tk.lw;
+            if (ids_out != nullptr) ids_out[q] = tk.lid;
+            if (w_out != nullptr) w_out[q] = tk.lw;
           }
         }
       }
@@ -215,22 +232,36 @@ __device__ __forceinline__ void route_small(SmallRoute& sr, const float* __restr
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   constexpr int nw = kBlk / kWave;
-  constexpr int kPer = (WR_SMALL_TILE_MAX_B + nw - 1) / nw;  // tokens per wave, at most
-  float l[kPer];
+  if (E <= 16) {  // four tokens per wave at once, one per 16-lane row
+    static_assert(WR_SMALL_TILE_MAX_B <= 4 * nw, "one pass");
+    const int row = lane >> 4, li = lane & 15;
+    const int t = 4 * wave + row;
+    const float l = t < B ? logits[(int64_t)t * WR_MAX_EXPERTS + li] : 0.0f;
+    int sid;
+    float sw;
+    row_select_topk(l, E, k, renorm, sid, sw);
+    if (t < B && li < k) {
+      sr.sel_id[t * k + li] = sid;
+      sr.sel_w[t * k + li] = sw;
+    }
+  } else {
+    constexpr int kPer = (WR_SMALL_TILE_MAX_B + nw - 1) / nw;  // tokens per wave, at most
+    float l[kPer];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {  // all loads in flight before the first selection
-    const int t = wave + i * nw;
-    l[i] = t < B ? logits[(int64_t)t * WR_MAX_EXPERTS + lane] : 0.0f;
-  }
+    for (int i = 0; i < kPer; ++i) {  // all loads in flight before the first selection
+      const int t = wave + i * nw;
+      l[i] = t < B ? logits[(int64_t)t * WR_MAX_EXPERTS + lane] : 0.0f;
+    }
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int t = wave + i * nw;
-    if (t < B) {  // wave-uniform
-      TopK tk;
-      wave_select_topk_reg(l[i], E, k, renorm, tk);
-      if (lane < k) {
-        sr.sel_id[t * k + lane] = tk.lid;
-        sr.sel_w[t * k + lane] = tk.lw;
+    for (int i = 0; i < kPer; ++i) {
+      const int t = wave + i * nw;
+      if (t < B) {  // wave-uniform
+        TopK tk;
+        wave_select_topk_reg(l[i], E, k, renorm, tk);
+        if (lane < k) {
+          sr.sel_id[t * k + lane] = tk.lid;
+          sr.sel_w[t * k + lane] = tk.lw;
+        }
       }
     }
   }

@@ -106,6 +106,24 @@ __device__ __forceinline__ float wave_sum(float v) {
   return lane_bcast(v, 63);
 }
 
+// The same four in-row steps alone: every lane gets the sum (max) of its
+// 16-lane row.
+__device__ __forceinline__ float row_sum(float v) {
+  v += dpp_mov<0xb1>(0.0f, v);
+  v += dpp_mov<0x4e>(0.0f, v);
+  v += dpp_mov<0x141>(0.0f, v);
+  v += dpp_mov<0x140>(0.0f, v);
+  return v;
+}
+__device__ __forceinline__ float row_max(float v) {
+  const float ninf = -__builtin_inff();
+  v = fmaxf(v, dpp_mov<0xb1>(ninf, v));
+  v = fmaxf(v, dpp_mov<0x4e>(ninf, v));
+  v = fmaxf(v, dpp_mov<0x141>(ninf, v));
+  v = fmaxf(v, dpp_mov<0x140>(ninf, v));
+  return v;
+}
+
 // Max over the wave (IEEE maxNum: a NaN lane never wins), uniform result.
 __device__ __forceinline__ float wave_max(float v) {
   const float ninf = -__builtin_inff();
@@ -184,6 +202,46 @@ __device__ __forceinline__ void wave_select_topk_reg(float l_in, int E, int k, i
       if (kk < k) t.w[kk] = t.w[kk] / tot;
     if (lane < k) t.lw = t.lw / tot;
   }
+}
+
+// Four selections at once, one per 16-lane row, for E <= 16: lane 16 r + e
+// holds token r's logit e.  With E <= 16, every full-wave reduction of
+// wave_select_topk_reg gives exactly its in-row result (the other rows hold
+// zeros or -inf, and x + 0 = x, max(x, -inf) = x), so ids and weights are
+// bit-identical to it.  Lane 16 r + kk (kk < k) gets slot kk of row r's
+// selection in sid / sw (renormalised if asked); other lanes get 0.
+__device__ __forceinline__ void row_select_topk(float l_in, int E, int k, int renorm, int& sid,
+                                                float& sw) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int li = lane & 15, row = lane >> 4;
+  const bool valid = li < E;
+  const float l = valid ? l_in : -__builtin_inff();
+  const float m = row_max(l);
+  const float ex = valid ? expf(l - m) : 0.0f;
+  const float s = row_sum(ex);
+  const float p = ex / s;
+  bool avail = valid;
+  float tot = 0.0f;
+  sid = 0;
+  sw = 0.0f;
+#pragma unroll
+  for (int kk = 0; kk < WR_MAX_TOPK; ++kk) {
+    if (kk < k) {
+      const bool cand = avail && (p > -3.402823466e38f);
+      const float best = row_max(cand ? p : -__builtin_inff());
+      const unsigned rmask =
+          (unsigned)(__ballot(cand && p == best) >> (16 * row)) & 0xffffu;  // this row's lanes
+      const int id = rmask ? (__ffs(rmask) - 1) : 0;
+      const float wv = rmask ? best : -3.402823466e38f;
+      if (li == kk) {
+        sid = id;
+        sw = wv;
+      }
+      tot += wv;
+      if (li == id) avail = false;
+    }
+  }
+  if (renorm && li < k) sw = sw / tot;
 }
 
 // Lane e (< 16 NB) gets logit e from NB scalar loads of 16 floats, all issued
