@@ -83,6 +83,14 @@
 #ifndef WR_XL_FP4_MAXH
 #define WR_XL_FP4_MAXH 6144
 #endif
+// Down blocks of the single-token fused kernel (register-path variant, 16-byte
+// weight vectors) also stage this many 1 KB row-chunks per wave of their
+// next down chunks in LDS before the hand-off wait, with direct global-to-LDS
+// loads (no registers): 8 = 32 KB per block, 2 chunks of 4 rows (fp16, bf16)
+// or 1 chunk of 8 rows (fp8).
+#ifndef WR_DN_LDS_ROWCHUNKS
+#define WR_DN_LDS_ROWCHUNKS 8
+#endif
 // MXFP4 weights in the single-token fused kernel (32 weights per 128-bit load)
 #ifndef WR_F4_U1
 #define WR_F4_U1 1   // gate/up column chunks per row per iteration (4 rows per wave)
@@ -871,6 +879,36 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
 
   V pre[U2][RPD];
   down_tile_load<WT, VEC, RPD, U2>(pre, wbuf, g, t, r0, nrows, wave, nch, lane);
+  // The next PRE chunks of this wave (after the U2 in registers) go to LDS:
+  // the tail after the hand-off then has one dependent load round fewer, and
+  // those bytes stream during the end of the gate/up phase.  Slot (v, j)
+  // holds row j of chunk wave + 4 (U2 + v), lane l's 16 bytes at 16 l.
+  // Register-path kernels only: the x-in-LDS variant's copy takes the LDS.
+  constexpr int PRE = (!XL && sizeof(V) == 16) ? WR_DN_LDS_ROWCHUNKS / RPD : 0;
+  constexpr int kPreBytes = kWavesPerBlock * PRE * RPD * kWave * 16;
+  __shared__ __align__(16) unsigned char dpre[kPreBytes > 0 ? kPreBytes : 16];
+  const int wu = __builtin_amdgcn_readfirstlane(wave);
+  if constexpr (PRE > 0) {
+#pragma unroll
+    for (int v = 0; v < PRE; ++v) {
+      const int q = wu + kWavesPerBlock * (U2 + v);
+      if (q < C) {  // wave-uniform
+        const int kk = q / nch;
+        const int c = (q - kk * nch) * kWave * VEC + lane * VEC;
+        const WT* D = wbuf + (int64_t)topk_id(t, kk) * g.stride + g.off_down +
+                      eoff<WT>((int64_t)r0 * g.I + c);
+#pragma unroll
+        for (int j = 0; j < RPD; ++j) {
+          if (j < nrows && c < g.I)
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void*>(D + eoff<WT>((int64_t)j * g.I)),
+                (__attribute__((address_space(3))) void*)(dpre + (size_t)((wu * PRE + v) * RPD + j) *
+                                                                     kWave * 16),
+                16, 0, 0);
+        }
+      }
+    }
+  }
   if constexpr (kFp8) {
     // Published to the block by the __syncthreads after the wait below.
     const int i = threadIdx.x, kk = i / RPD, j = i % RPD;
@@ -915,7 +953,27 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
 #pragma unroll
   for (int j = 0; j < RPD; ++j) acc[j] = 0.0f;
   down_tile_fma<WT, V, VEC, RPD, U2>(acc, pre, act, g, act_row, wave, nch, lane, sdn);
-  for (int q0 = wave + kWavesPerBlock * U2; q0 < C; q0 += kWavesPerBlock * U2) {
+  if constexpr (PRE > 0) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's global-to-LDS loads have landed
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int v = 0; v < PRE; ++v) {
+      const int q = wu + kWavesPerBlock * (U2 + v);
+      if (q < C) {
+        const int kk = q / nch;
+        const int c = (q - kk * nch) * kWave * VEC + lane * VEC;
+        V lw[1][RPD];
+#pragma unroll
+        for (int j = 0; j < RPD; ++j)
+          lw[0][j] = (j < nrows && c < g.I)
+                         ? *reinterpret_cast<const V*>(
+                               dpre + (size_t)((wu * PRE + v) * RPD + j) * kWave * 16 + lane * 16)
+                         : vzero<V>();
+        down_tile_fma<WT, V, VEC, RPD, 1>(acc, lw, act, g, act_row, q, nch, lane, sdn);
+      }
+    }
+  }
+  for (int q0 = wave + kWavesPerBlock * (U2 + PRE); q0 < C; q0 += kWavesPerBlock * U2) {
     V wv[U2][RPD];
     down_tile_load<WT, VEC, RPD, U2>(wv, wbuf, g, t, r0, nrows, q0, nch, lane);
     down_tile_fma<WT, V, VEC, RPD, U2>(acc, wv, act, g, act_row, q0, nch, lane, sdn);
