@@ -776,20 +776,38 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, B
   }
 }
 
-// out[t][row]: grid (ceil(h / 256), B).
-template <typename OT>
+// out[t][row]: grid (ceil(h / 256), B); K = k, so that every loop is exact.
+// Every pair index, then every partial, is loaded before the first add (two
+// round trips instead of 2 K); the adds keep their order (experts in
+// selection order, K slices ascending).
+template <typename OT, int K>
 __global__ __launch_bounds__(kBlk) void k_combine(const float* __restrict__ ypart, BatchRoute r,
-                                                  OT* __restrict__ out, int h, int k, int P) {
+                                                  OT* __restrict__ out, int h, int P) {
   const int t = blockIdx.y;
   const int row = blockIdx.x * kBlk + threadIdx.x;
   if (row >= h) return;
-  float s = 0.0f;
-  for (int kk = 0; kk < k; ++kk) {
-    const int p = r.tok_pair[t * k + kk];
+  int p[K];
 #pragma unroll
-    for (int ks = 0; ks < BatchWs::kKSplit; ++ks) s += ypart[((int64_t)ks * P + p) * h + row];
-  }
+  for (int kk = 0; kk < K; ++kk) p[kk] = r.tok_pair[t * K + kk];
+  float v[K][BatchWs::kKSplit];
+#pragma unroll
+  for (int kk = 0; kk < K; ++kk)
+#pragma unroll
+    for (int ks = 0; ks < BatchWs::kKSplit; ++ks)
+      v[kk][ks] = ypart[((int64_t)ks * P + p[kk]) * h + row];
+  float s = 0.0f;
+#pragma unroll
+  for (int kk = 0; kk < K; ++kk)
+#pragma unroll
+    for (int ks = 0; ks < BatchWs::kKSplit; ++ks) s += v[kk][ks];
   out[(int64_t)t * h + row] = to_out<OT>(s);
+}
+
+template <typename OT, int K>
+hipError_t launch_combine(const BatchWs& w, const Problem& p, hipStream_t s) {
+  hipLaunchKernelGGL((k_combine<OT, K>), dim3((p.h + kBlk - 1) / kBlk, p.B), dim3(kBlk), 0, s,
+                     w.ypart, w.route, static_cast<OT*>(p.out), p.h, p.B * K);
+  return hipGetLastError();
 }
 
 template <typename WT, typename XT>
@@ -841,9 +859,15 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
                        dim3(kBlk), 0, s, wb, w.route, w.act, w.ypart, g, P);
   }
   if ((err = hipGetLastError()) != hipSuccess) return err;
-  hipLaunchKernelGGL((k_combine<XT>), dim3((p.h + kBlk - 1) / kBlk, p.B), dim3(kBlk), 0, s,
-                     w.ypart, w.route, static_cast<XT*>(p.out), p.h, p.k, P);
-  return hipGetLastError();
+  static_assert(WR_MAX_TOPK == 6, "one combine instantiation per k");
+  switch (p.k) {
+    case 1: return launch_combine<XT, 1>(w, p, s);
+    case 2: return launch_combine<XT, 2>(w, p, s);
+    case 3: return launch_combine<XT, 3>(w, p, s);
+    case 4: return launch_combine<XT, 4>(w, p, s);
+    case 5: return launch_combine<XT, 5>(w, p, s);
+    default: return launch_combine<XT, 6>(w, p, s);
+  }
 }
 
 }  // namespace
