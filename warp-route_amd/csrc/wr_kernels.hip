@@ -66,11 +66,14 @@
 #define WR_F8_U2 2   // column chunks per down tile
 #endif
 // x staged in LDS by the gate/up blocks of the single-token fused kernel, for
-// h up to these bounds (0: never); fp8, fp16 and bf16 also need at most
-// WR_XL_FP8_BPC gate/up blocks per CU.  Measured: it gains for MXFP4 up to
-// h = 6144, and for the other types when the gate/up blocks fit in one round
-// of residency (DeepSeek, Mixtral shards); it costs with many rounds (Mixtral,
-// 3584 blocks) or at h = 6144.
+// h up to these bounds (0: never); fp8 also needs at most WR_XL_FP8_BPC gate/up
+// blocks per CU, fp16 and bf16 at most WR_XL_F16_BPC.  Measured: it gains for
+// MXFP4 up to h = 6144, and for the other types when the gate/up blocks are
+// few; it costs with many rounds of residency (Mixtral, 3584 blocks) or at
+// h = 6144.  fp16 and bf16 take the lower bound because the register path
+// has the down blocks' LDS-staged prefetch, which the x copy leaves no room
+// for (Mixtral tp4 shard, 3.5 blocks per CU: 45.2 us against 48.3 with x in
+// LDS; tp8 shard, 1.75 per CU: 30.7 against 29.6).
 #ifndef WR_XL_FP8_MAXH
 #define WR_XL_FP8_MAXH 4096
 #endif
@@ -79,6 +82,9 @@
 #endif
 #ifndef WR_XL_FP8_BPC
 #define WR_XL_FP8_BPC 4
+#endif
+#ifndef WR_XL_F16_BPC
+#define WR_XL_F16_BPC 2
 #endif
 #ifndef WR_XL_FP4_MAXH
 #define WR_XL_FP4_MAXH 6144
@@ -1107,7 +1113,8 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   constexpr int kXlMax = xl_max_h<WT>();
   constexpr bool kXl = kXlMax > 0 && VEC >= 8;
   if constexpr (kXl) {
-    if (p.h <= kXlMax && (kFp4 || hs.n1 <= WR_XL_FP8_BPC * cu_count())) {
+    constexpr int kBpc = kFp8 ? WR_XL_FP8_BPC : WR_XL_F16_BPC;  // MXFP4: no bound
+    if (p.h <= kXlMax && (kFp4 || hs.n1 <= kBpc * cu_count())) {
       hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true>),
                          dim3(hs.n1 + n2), dim3(kBlock), 0, s,
                          static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x), w.logits,
