@@ -19,6 +19,14 @@ bounded sample of the same layer.
   python bench.py [--steps K] [--warmup W] [--layers L] [--config mixtral]
   python bench.py --weights fp8    # the same layers in bf16 or fp8 E4M3 (not the headline)
   python bench.py --copy-probe     # plain device copy, for counter calibration
+  python bench.py --op naive       # the naive multi-kernel path, with fused beside it
+  python bench.py --read-probe     # read-only streaming ceiling over the same bytes
+
+The headline line also carries roofline.read_ceiling: the best rate of a
+plain read-only streaming kernel (libwr_probe.so) over exactly the selected
+experts' bytes of the same rotated layers, measured in the same run, so the
+kernel's rate can be read against what the chip streams, not only against
+the 8 TB/s peak.
 
 Two further workloads of BASELINE.json configs[4] print their own JSON line
 (not the headline): --batch B[,B...] times batched_fused_moe on clustered
@@ -274,6 +282,139 @@ def stack_bench(args) -> int:
     return 0
 
 
+def probe_lib():
+    """ctypes handle of libwr_probe.so (include/wr_probe.h)."""
+    import ctypes
+    path = os.path.join(ROOT, "warp-route_amd", "warp_route", "libwr_probe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built (python warp-route_amd/build.py)")
+    lib = ctypes.CDLL(path)
+    lib.wr_probe_read.argtypes = [ctypes.POINTER(ctypes.c_void_p),
+                                  ctypes.POINTER(ctypes.c_int64), ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.wr_probe_read.restype = ctypes.c_int
+    return lib
+
+
+# (blocks per CU, loads in flight per lane) tried by read_ceiling
+PROBE_SHAPES = [(2, 4), (4, 4), (8, 4), (4, 8), (8, 2), (16, 2)]
+
+
+def read_ceiling(range_sets, steps: int, warmup: int = 5) -> dict:
+    """Best rate of the read-only streaming probe over range_sets (one list
+    of (ptr, bytes) per rotated layer, read in one launch per call, rotating),
+    over PROBE_SHAPES: the achievable HBM read bandwidth for these bytes."""
+    import ctypes
+    import torch
+    lib = probe_lib()
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    calls = []
+    for rs in range_sets:
+        ptrs = (ctypes.c_void_p * len(rs))(*[p for p, _ in rs])
+        nb = (ctypes.c_int64 * len(rs))(*[n for _, n in rs])
+        calls.append((ptrs, nb, len(rs), sum(n for _, n in rs)))
+    results = []
+    for bpc, unroll in PROBE_SHAPES:
+        def step(i):
+            ptrs, nb, n, _ = calls[i % len(calls)]
+            if lib.wr_probe_read(ptrs, nb, n, bpc, unroll, ctypes.c_void_p(sink.data_ptr()),
+                                 ctypes.c_void_p(stream)) != 0:
+                raise RuntimeError("wr_probe_read failed")
+        us = _timed(step, steps, warmup)
+        nbytes = sum(c[3] for c in calls) / len(calls)
+        results.append({"blocks_per_cu": bpc, "loads_in_flight": unroll,
+                        "us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1)})
+    best = max(results, key=lambda r: r["GBps"])
+    return {"GBps": best["GBps"], "us": best["us"], "shape": [best["blocks_per_cu"],
+                                                              best["loads_in_flight"]],
+            "bytes_per_call": int(sum(c[3] for c in calls) / len(calls)), "sweep": results}
+
+
+def selected_ranges(layers, cfg):
+    """Per layer, the (device pointer, bytes) of each selected expert's
+    weights (its three matrices and, for fp8 / MXFP4, their scales: the
+    algorithmic bytes), rounded down to 16 bytes."""
+    from warp_route import functional as F
+    from warp_route.synthetic import expert_weight_bytes
+    E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+    stride = F.weight_layout(E, h, I, cfg.weight_dtype)["expert_stride"]
+    nb = expert_weight_bytes(h, I, cfg.weight_dtype) // 16 * 16
+    out = []
+    for x, gw, buf in layers:
+        ids, _ = F.gate_topk(x, gw, E, h, k, cfg.renormalize)
+        out.append([(buf.data_ptr() + int(e) * stride, nb) for e in ids.tolist()])
+    return out
+
+
+def read_probe_bench(args) -> int:
+    """The read-only streaming ceiling: the probe over the selected experts'
+    bytes of the rotated layers (what one MoE call must read), and over one
+    contiguous 1 GiB buffer."""
+    import torch
+    from warp_route.synthetic import CONFIGS, make_config_layer
+    cfg = CONFIGS[args.config].with_weights(weight_dtype(args.weights))
+    dev = torch.device("cuda:0")
+    layers = [make_config_layer(cfg, seed=s, device=dev, gen_device=dev)
+              for s in range(args.layers)]
+    sel = read_ceiling(selected_ranges(layers, cfg), args.steps)
+    flat = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    big = read_ceiling([[(flat.data_ptr(), flat.numel())]], max(20, args.steps // 10))
+    print(json.dumps({
+        "metric": "read-only HBM streaming ceiling (GB/s)", "value": sel["GBps"],
+        "unit": "GB/s", "higher_is_better": True, "n_gpus": 1, "steps": args.steps,
+        "config": {"workload": f"{cfg.name} selected experts ({args.weights}), "
+                               f"{args.layers} layers rotated",
+                   "bytes_per_call": sel["bytes_per_call"]},
+        "selected_experts": sel, "contiguous_1GiB": big,
+        "peak_GBps": HBM_PEAK_GBPS, "frac_of_peak": round(sel["GBps"] / HBM_PEAK_GBPS, 4),
+    }), flush=True)
+    return 0
+
+
+def naive_bench(args) -> int:
+    """The naive multi-kernel path (warp_route.functional.naive_moe: router,
+    host softmax / top-K after one stream synchronisation, then per selected
+    expert gate, up, SwiGLU, down and weighted-accumulate launches) on the
+    headline layers, with the fused op timed on the same layers beside it:
+    the comparison of benchmarks/bench_latency.cu:83-122 in the reference."""
+    import torch
+    from warp_route import functional as F
+    from warp_route.synthetic import CONFIGS, make_config_layer
+    cfg = CONFIGS[args.config].with_weights(weight_dtype(args.weights))
+    E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+    dev = torch.device("cuda:0")
+    layers = [make_config_layer(cfg, seed=s, device=dev, gen_device=dev)
+              for s in range(args.layers)]
+    L = len(layers)
+    steps = max(10, args.steps // 4)  # each naive call synchronises the stream once
+
+    def naive(i):
+        x, gw, buf = layers[i % L]
+        return F.naive_moe(x, gw, buf, E, h, I, k, cfg.renormalize)
+
+    def fused(i):
+        x, gw, buf = layers[i % L]
+        return F.fused_moe(x, gw, buf, E, h, I, k, cfg.renormalize)
+
+    us_naive = _timed(naive, steps, args.warmup)
+    us_fused = _timed(fused, args.steps, args.warmup)
+    nbytes = cfg.selected_bytes
+    print(json.dumps({
+        "metric": f"µs per MoE layer at batch=1 ({cfg.name} shape), naive multi-kernel path",
+        "value": round(us_naive, 2), "unit": "us/layer", "higher_is_better": False,
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "dtype": WLABEL[args.weights] + " weights, f32 accumulate",
+        "data": "synthetic (seeded random-init layers drawn on the GPU)",
+        "config": {"workload": f"{cfg.name} MoE layer, decode batch 1, naive op",
+                   "launches_per_call": 3 + 5 * k, "layers_rotated": L},
+        "naive_GBps": round(nbytes / us_naive / 1e3, 1),
+        "fused_us": round(us_fused, 2), "fused_GBps": round(nbytes / us_fused / 1e3, 1),
+        "fused_speedup": round(us_naive / us_fused, 3),
+    }), flush=True)
+    return 0
+
+
 def copy_probe(nbytes: int, iters: int) -> dict:
     """Device-to-device copy of nbytes (torch's copy kernel): the achievable
     streaming ceiling, and the calibration run for FETCH_SIZE / WRITE_SIZE."""
@@ -306,6 +447,12 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true")
+    ap.add_argument("--read-probe", action="store_true",
+                    help="time the read-only streaming ceiling over the selected experts")
+    ap.add_argument("--op", default="fused", choices=["fused", "naive"],
+                    help="naive: time the naive multi-kernel op (with fused beside it)")
+    ap.add_argument("--no-ceiling", action="store_true",
+                    help="skip the streaming-ceiling measurement in the headline line")
     ap.add_argument("--batch", default=None,
                     help="comma-separated batch sizes: time batched decode instead")
     ap.add_argument("--stack", type=int, default=0,
@@ -332,6 +479,10 @@ def main() -> int:
     if args.copy_probe:
         print(json.dumps(copy_probe(1 << 30, 50)), flush=True)
         return 0
+    if args.read_probe:
+        return read_probe_bench(args)
+    if args.op == "naive":
+        return naive_bench(args)
     if args.batch:
         return batched_bench(args)
     if args.stack:
@@ -434,6 +585,13 @@ def main() -> int:
         "per_call_us": {"p10": round(p10, 2), "p50": round(p50, 2), "p90": round(p90, 2)},
         "selected_bytes_per_call": sel_bytes,
     }
+    if not args.no_ceiling:
+        ceil = read_ceiling(selected_ranges(layers, cfg), args.steps)
+        result["roofline"]["read_ceiling"] = {
+            "GBps": ceil["GBps"], "us": ceil["us"], "shape": ceil["shape"],
+            "kernel_frac_of_ceiling": round(achieved / ceil["GBps"], 4),
+            "what": "best read-only streaming kernel (libwr_probe.so) over exactly the "
+                    "selected experts' bytes of the same rotated layers"}
     if not args.no_cpu_baseline:
         x, gw, buf = layers[0]
         log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s sample)")

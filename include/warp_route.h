@@ -68,6 +68,8 @@ typedef enum wr_status {
   WR_EINVAL_BATCH = 8,        /* batch_size < 0, or != 1 for a single-token op */
   WR_EINVAL_KIND = 9,         /* unknown wr_kind                               */
   WR_EINVAL_BLOCK = 10,       /* MXFP4 weights need h and I multiples of 32    */
+  WR_ETIMEOUT = 11,           /* a single-token hand-off wait expired: the rows
+                                 of the blocks that gave up are NaN            */
   WR_EHIP = 100               /* a HIP runtime call failed                     */
 } wr_status;
 
@@ -151,6 +153,18 @@ typedef struct wr_layout_info {
   int32_t weight_dtype;   /* wr_dtype                                       */
 } wr_layout_info;
 
+/* Options of the single-token fused kernel's hand-off between its gate/up
+ * and down blocks (see wr_fused_moe_opts).  Zero-initialise for the
+ * defaults. */
+typedef struct wr_fused_opts {
+  uint32_t spin_limit;  /* polls before a down block's wait expires; 0 = the
+                           default (2^20 polls, about 0.2 s)                  */
+  uint32_t wait_extra;  /* added to every arrival target.  0 in normal use; a
+                           nonzero value makes every wait expire after
+                           spin_limit polls, so that tests can exercise the
+                           expiry path while every kernel still exits normally */
+} wr_fused_opts;
+
 /* Human-readable name of a status code (never NULL). */
 WR_API const char *wr_status_str(int status);
 
@@ -192,6 +206,24 @@ WR_API int wr_gate_topk(const wr_moe_args *args, void *stream);
 /* Single-token fused MoE (batch_size must be 1).  Replaces fused_moe_forward
  * (src/fused_moe.cu:233-263, declared at src/fused_moe.cuh:29-32). */
 WR_API int wr_fused_moe(const wr_moe_args *args, void *stream);
+
+/* wr_fused_moe with explicit hand-off options (opts may be NULL: defaults).
+ * On expiry of a down block's bounded wait, that block writes NaN to its
+ * output rows and sets the workspace's timeout word, which
+ * wr_fused_moe_status reports.  The reference has no such wait: its fused
+ * kernel is one warp (src/fused_moe.cu:76-227) and its error paths call
+ * exit(1) (src/fused_moe.cu:9-15). */
+WR_API int wr_fused_moe_opts(const wr_moe_args *args, const wr_fused_opts *opts, void *stream);
+
+/* Status of the last single-token fused call that used `workspace` (size
+ * workspace_bytes, at least wr_workspace_bytes(WR_KIND_FUSED, ...)): WR_OK, or
+ * WR_ETIMEOUT if a hand-off wait expired (the output then holds NaN rows).
+ * Reads the timeout word with a copy on `stream` and synchronises `stream`;
+ * call it after the op and before the next single-token call on the same
+ * workspace, whose router launch clears the word.  Has no counterpart in the
+ * reference, whose fused kernel exits the process on error
+ * (src/fused_moe.cu:9-15). */
+WR_API int wr_fused_moe_status(const void *workspace, size_t workspace_bytes, void *stream);
 
 /* The two launches of wr_fused_moe, for callers that issue them separately
  * (to overlap the router with other work on the stream's timeline, or to time

@@ -55,6 +55,36 @@ def oracle_token(x: torch.Tensor, gate_w: torch.Tensor, buf: torch.Tensor, E: in
     return {"out": out, "ids": ids, "weights": ws, "robust": robust}
 
 
+def oracle_rows(x: torch.Tensor, gate_w: torch.Tensor, buf: torch.Tensor, E: int, h: int,
+                I: int, k: int, renorm: bool):
+    """oracle_token for every row of x [B, h], fetching each selected expert
+    from the device once for all the rows that select it (the FFN of those
+    rows as one fp64 matrix product: expert_ffn on an [h, n] block).  Returns
+    one dict per row, as oracle_token."""
+    xn = f64(x).reshape(-1, h)
+    gw = f64(gate_w)
+    rows, users = [], {}
+    for b in range(xn.shape[0]):
+        logits64 = O.router_logits(gw, xn[b])
+        _, ids, ws = O.softmax_topk(logits64.astype(np.float32), k, renorm)
+        p64 = np.exp(logits64 - logits64.max())
+        p64 /= p64.sum()
+        w64 = p64[ids]
+        if renorm:
+            w64 = w64 / w64.sum()
+        rows.append({"out": np.zeros(h), "ids": ids, "weights": ws, "w64": w64,
+                     "robust": O.selection_is_robust(gw, xn[b], k)})
+        for kk in range(k):
+            users.setdefault(int(ids[kk]), []).append((b, kk))
+    for e, lst in sorted(users.items()):
+        g, u, d = expert_mats(buf, e, E, h, I)
+        y = O.expert_ffn(xn[[b for b, _ in lst]].T, g, u, d)  # [h, n]
+        for j, (b, kk) in enumerate(lst):
+            rows[b]["out"] += rows[b]["w64"][kk] * y[:, j]
+        del g, u, d
+    return rows
+
+
 def assert_parity(got_out, got_ids, got_w, ref, rel_tol=1e-4, w_rtol=1e-5, label=""):
     """The parity bar: ids bit-exact (the case must pass the margin guard),
     weights within w_rtol, output within rtol = atol = 1e-2 and within

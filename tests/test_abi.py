@@ -24,7 +24,8 @@ def test_header_declares_the_expected_entry_points():
     assert sorted(declared_symbols()) == sorted([
         "wr_status_str", "wr_layout", "wr_total_weight_bytes", "wr_layout_dtype",
         "wr_weight_bytes", "wr_workspace_bytes", "wr_gate_topk", "wr_fused_moe",
-        "wr_fused_moe_route", "wr_fused_moe_ffn", "wr_batched_fused_moe", "wr_naive_moe"])
+        "wr_fused_moe_route", "wr_fused_moe_ffn", "wr_batched_fused_moe", "wr_naive_moe",
+        "wr_fused_moe_opts", "wr_fused_moe_status"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -42,6 +43,7 @@ def test_header_constants_match_binding():
                  "WR_EINVAL_EXPERTS", "WR_EINVAL_DTYPE", "WR_EINVAL_WEIGHT_SIZE",
                  "WR_EINVAL_WORKSPACE", "WR_EINVAL_BATCH", "WR_EINVAL_KIND", "WR_EHIP",
                  "WR_F32", "WR_F16", "WR_BF16", "WR_FP8_E4M3", "WR_MXFP4", "WR_EINVAL_BLOCK",
+                 "WR_ETIMEOUT",
                  "WR_KIND_FUSED",
                  "WR_KIND_BATCHED", "WR_KIND_NAIVE"):
         m = re.search(rf"\b{name} = (\d+)", text)
@@ -138,17 +140,19 @@ def test_workspace_bytes():
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 64, 100, 3, 1) == (
         ctrl + 256 + 1536)  # 3 * 112 * 4 = 1344 -> 1536
     # batched, B > 1: the larger of the per-token layout above and the
-    # grouped MFMA layout: logits, x as two fp16 terms, five [P] pair arrays,
-    # expert offsets / active list / count, act [P][I] and four K-slice
-    # partials [4][P][h] (P = B * k), each region rounded up to 256 bytes.
+    # grouped MFMA layout: logits, x as two fp16 terms and its per-token
+    # exponents, one act-maximum word per pair on its own 256-byte line, five
+    # [P] pair arrays, expert offsets / active list / count, act [P][I] and
+    # four K-slice partials [4][P][h] (P = B * k), each region rounded up to
+    # 256 bytes.
     def up(n):
         return (n + 255) // 256 * 256
     B, E, h, I, k = 4, 8, 4096, 14336, 2
     P = B * k
     per_token = ctrl + B * 256 + P * I * 4
-    grouped = (up(B * 256) + 2 * up(B * h * 2) + 5 * up(P * 4) + up((E + 1) * 4) + up(E * 4)
-               + up(4) + up(P * I * 4) + up(4 * P * h * 4))
-    assert grouped == 1051648
+    grouped = (up(B * 256) + 2 * up(B * h * 2) + up(B * 4) + P * 256 + 5 * up(P * 4)
+               + up((E + 1) * 4) + up(E * 4) + up(4) + up(P * I * 4) + up(4 * P * h * 4))
+    assert grouped == 1051648 + 256 + 8 * 256
     assert lib.wr_workspace_bytes(capi.WR_KIND_BATCHED, E, h, I, k, B) == max(per_token, grouped)
     assert lib.wr_workspace_bytes(capi.WR_KIND_NAIVE, 8, 100, 10, 1, 1) == 256 + 3 * 256 + 2 * 512
     assert lib.wr_workspace_bytes(7, 8, 64, 64, 2, 1) == 0
@@ -158,7 +162,7 @@ def test_workspace_bytes():
 
 
 def test_status_strings():
-    for s in range(0, 12):
+    for s in range(0, 13):
         assert capi.status_str(s)
     assert capi.status_str(capi.WR_EHIP) == "HIP runtime error"
 
@@ -213,6 +217,27 @@ def test_validation_codes(entry, field, value, want):
     a = valid_args()
     setattr(a, field, value)
     assert capi.call(entry, a) == want
+
+
+def test_fused_opts_entry_point_validates_like_wr_fused_moe():
+    """wr_fused_moe_opts runs the same argument checks before any HIP call,
+    with or without options."""
+    opts = capi.WrFusedOpts(spin_limit=4, wait_extra=1)
+    for field, value, want in CASES:
+        a = valid_args()
+        setattr(a, field, value)
+        assert capi.lib().wr_fused_moe_opts(ctypes.byref(a), ctypes.byref(opts), None) == want
+        assert capi.lib().wr_fused_moe_opts(ctypes.byref(a), None, None) == want
+    a = valid_args(B=2)
+    assert capi.lib().wr_fused_moe_opts(ctypes.byref(a), None, None) == capi.WR_EINVAL_BATCH
+
+
+def test_fused_status_checks_its_workspace_before_hip():
+    lib = capi.lib()
+    assert lib.wr_fused_moe_status(None, 1 << 20, None) == capi.WR_EINVAL_NULL
+    # smaller than the control block (130 lines of 256 bytes)
+    assert lib.wr_fused_moe_status(FAKE, 130 * 256 - 1, None) == capi.WR_EINVAL_WORKSPACE
+    assert "NaN" in capi.status_str(capi.WR_ETIMEOUT)
 
 
 def test_mxfp4_needs_blocks_of_32():

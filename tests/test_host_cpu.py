@@ -134,6 +134,33 @@ def test_moelayer_pack_cache():
     np.testing.assert_array_equal(ue, layer.up_proj[1].data.half().numpy())
 
 
+def test_moelayer_data_writes_need_invalidate():
+    """p.data.copy_ does not bump the version counter, so the cached pack is
+    stale until invalidate_packed(); with cache_packed=False every forward
+    repacks (the reference's behaviour, warp_route/__init__.py:81)."""
+    layer = warp_route.MoELayer(3, 8, 4, top_k=2, weight_dtype=torch.float16)
+    a = layer._pack_weights()
+    new_down = torch.full((8, 4), 0.25)
+    layer.down_proj[2].data.copy_(new_down)
+    assert layer._pack_weights() is a  # not detected: documented
+    _, _, de = O.expert_views(a.numpy(), 2, 3, 8, 4)
+    assert not np.array_equal(de, new_down.half().numpy())
+    layer.invalidate_packed()
+    b = layer._pack_weights()
+    assert b is not a
+    _, _, de = O.expert_views(b.numpy(), 2, 3, 8, 4)
+    np.testing.assert_array_equal(de, new_down.half().numpy())
+
+    fresh = warp_route.MoELayer(3, 8, 4, top_k=2, weight_dtype=torch.float16,
+                                cache_packed=False)
+    c = fresh._pack_weights()
+    fresh.gate_proj[0].data.copy_(torch.ones(4, 8))
+    d = fresh._pack_weights()
+    assert d is not c
+    ge, _, _ = O.expert_views(d.numpy(), 0, 3, 8, 4)
+    np.testing.assert_array_equal(ge, np.ones((4, 8), np.float16))
+
+
 def test_moe_stack_validates_layers():
     from warp_route.stack import MoEStack
     with pytest.raises(ValueError):
@@ -313,3 +340,76 @@ def test_shard_expert_weights_argument_checks():
                          torch.float4_e2m1fn_x2, "cpu")
     with pytest.raises(ValueError):
         F.shard_expert_weights(b4, E, h, I, 2, 0)       # I' = 48 is not a multiple of 32
+
+
+def _split_fp16(v: np.ndarray, no_down: bool):
+    """The grouped path's fp16 split of a row v (fp32): e from max|v| as
+    split_exp does it (frexp exponent ex, e = 15 - ex, e >= 0 with
+    no_down), hi = fp16(v 2^e), lo = fp16(v 2^e - hi)."""
+    amax = float(np.max(np.abs(v)))
+    e = 0
+    if 0.0 < amax < np.inf:
+        e = 15 - int(np.frexp(np.float32(amax))[1])
+        if no_down and e < 0:
+            e = 0
+    vs = np.ldexp(v.astype(np.float32), e).astype(np.float32)
+    with np.errstate(over="ignore"):
+        hi = vs.astype(np.float16)
+        lo = (vs - hi.astype(np.float32)).astype(np.float16)
+    return vs, hi, lo, e
+
+
+@pytest.mark.parametrize("scale", [1.0, 1e5, 1e-6, 3e-30, 7e30])
+def test_fp16_split_bound_with_power_of_two_scaling(scale):
+    """|v 2^e - (hi + lo)| <= 2^-22 |v 2^e| + 2^-25 for every element, with
+    hi finite and max|v 2^e| in [2^14, 2^15), at any magnitude (the bound the
+    batched MFMA path relies on, split_exp in wr_device.h).  The same split
+    without the scaling breaks it: inf above fp16's range, and below it the
+    bound relative to |v| fails for most elements."""
+    rng = np.random.default_rng(0)
+    v = (rng.standard_normal(1 << 16) * scale).astype(np.float32)
+    vs, hi, lo, e = _split_fp16(v, no_down=False)
+    assert np.isfinite(hi).all() and np.isfinite(lo).all()
+    amax = np.max(np.abs(vs))
+    assert 2.0 ** 14 <= amax < 2.0 ** 15
+    err = np.abs(vs.astype(np.float64) - hi.astype(np.float64) - lo.astype(np.float64))
+    assert (err <= 2.0 ** -22 * np.abs(vs.astype(np.float64)) + 2.0 ** -25).all()
+    # unscaled, for contrast
+    with np.errstate(over="ignore", invalid="ignore"):
+        h0 = v.astype(np.float16)
+        l0 = (v - h0.astype(np.float32)).astype(np.float16)
+        e0 = np.abs(v.astype(np.float64) - h0.astype(np.float64) - l0.astype(np.float64))
+    if scale >= 1e5:
+        assert not np.isfinite(h0).all()
+    elif scale <= 1e-6:
+        assert np.mean(~(e0 <= 2.0 ** -22 * np.abs(v.astype(np.float64)))) > 0.5
+
+
+def test_fp16_split_of_fp16_input_is_exact():
+    """fp16 inputs are never scaled down (e >= 0): v 2^e is exact in fp16, so
+    the low term is zero, also right up to 65504."""
+    rng = np.random.default_rng(1)
+    for top in (65504.0, 3.0, 1e-3):
+        v = (rng.uniform(-1, 1, 4096) * top).astype(np.float16).astype(np.float32)
+        v[0] = np.float32(np.float16(top))
+        vs, hi, lo, e = _split_fp16(v, no_down=True)
+        assert e >= 0 and np.isfinite(hi).all()
+        np.testing.assert_array_equal(lo.astype(np.float32), 0.0)
+        np.testing.assert_array_equal(hi.astype(np.float32), vs)
+
+
+def test_oracle_rows_matches_per_token_oracle():
+    """The batched test helper (each selected expert fetched once, FFN of its
+    rows as one matrix product) equals oracle_token row by row."""
+    from tests._helpers import oracle_rows, oracle_token
+    from warp_route.synthetic import make_layer
+    E, h, I, k = 8, 64, 96, 2
+    x, gw, buf = make_layer(E, h, I, torch.float16, router_std=h ** -0.5, expert_std=0.05,
+                            seed=4, batch=6)
+    rows = oracle_rows(x, gw, buf, E, h, I, k, True)
+    for b in range(6):
+        ref = oracle_token(x[b], gw, buf, E, h, I, k, True)
+        np.testing.assert_array_equal(rows[b]["ids"], ref["ids"])
+        np.testing.assert_array_equal(rows[b]["weights"], ref["weights"])
+        np.testing.assert_allclose(rows[b]["out"], ref["out"], rtol=1e-12, atol=1e-14)
+        assert rows[b]["robust"] == ref["robust"]

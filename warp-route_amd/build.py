@@ -5,6 +5,9 @@
   _C.<ext-suffix>.so    the pybind11/torch module warp_route._C, compiled
                         from csrc/bindings.cpp with the host compiler and
                         linked against libwarp_route_hip.so (rpath $ORIGIN)
+  libwr_probe.so        the read-only HBM streaming probe bench.py uses for
+                        the achievable-bandwidth ceiling (include/wr_probe.h);
+                        a measurement utility, not part of the MoE library
 
 Both land in warp_route/ so that the package directory is self-contained and
 travels with the source tree.  Run ``python warp-route_amd/build.py``.
@@ -37,6 +40,8 @@ HIP_FLAGS = [
     "-Wall", "-Wno-unused-function",
 ]
 HIP_SOURCES = ["wr_api.hip", "wr_kernels.hip", "wr_batched.hip", "wr_naive.hip"]
+PROBE_SOURCE = "wr_probe.hip"
+PROBE_NAME = "libwr_probe.so"
 
 
 def _run(cmd, **kw):
@@ -64,6 +69,19 @@ def build_lib(verbose: bool = False) -> Path:
     lib = PKG / LIB_NAME
     tmp = BUILD / LIB_NAME
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
+    os.replace(tmp, lib)
+    return lib
+
+
+def build_probe(verbose: bool = False) -> Path:
+    """Compile csrc/wr_probe.hip into libwr_probe.so."""
+    BUILD.mkdir(exist_ok=True)
+    tmp = BUILD / PROBE_NAME
+    out = _run([HIPCC, *HIP_FLAGS, "-shared", f"-I{INCLUDE}", str(CSRC / PROBE_SOURCE),
+                "-o", str(tmp)])
+    if verbose and out.strip():
+        print(out)
+    lib = PKG / PROBE_NAME
     os.replace(tmp, lib)
     return lib
 
@@ -99,10 +117,13 @@ def build_ext(verbose: bool = False) -> Path:
 
 
 def build(verbose: bool = False) -> None:
-    lib = build_lib(verbose)
+    with cf.ThreadPoolExecutor(max_workers=2) as ex:
+        probe = ex.submit(build_probe, verbose)
+        lib = build_lib(verbose)
+        probe = probe.result()
     ext = build_ext(verbose)
     if verbose:
-        print(f"built {lib}\nbuilt {ext}")
+        print(f"built {lib}\nbuilt {ext}\nbuilt {probe}")
 
 
 if __name__ == "__main__":

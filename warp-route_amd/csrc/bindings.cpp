@@ -26,11 +26,23 @@
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/extension.h>
 
+#include <atomic>
+#include <cstdlib>
 #include <optional>
 
 #include "warp_route.h"
 
 namespace {
+
+// When set, fused_moe_forward reads the hand-off status of its call
+// (wr_fused_moe_status, which synchronises the stream) and raises if a wait
+// expired.  Off by default: the check costs a stream synchronisation and
+// cannot run under graph capture.  WARP_ROUTE_CHECK_HANDOFF=1 in the
+// environment turns it on at import.
+std::atomic<bool> g_check_handoff{[] {
+  const char* v = std::getenv("WARP_ROUTE_CHECK_HANDOFF");
+  return v != nullptr && v[0] != '\0' && v[0] != '0';
+}()};
 
 #define WR_CHECK_DEVICE(t) TORCH_CHECK((t).is_cuda(), #t " must be a CUDA (HIP) tensor")
 #define WR_CHECK_CONTIGUOUS(t) TORCH_CHECK((t).is_contiguous(), #t " must be contiguous")
@@ -154,9 +166,12 @@ torch::Tensor single_token_op(int kind, torch::Tensor hidden, torch::Tensor gate
   a.workspace = ws.data_ptr();
   a.workspace_bytes = (size_t)ws.numel();
   void* stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(dev.index()).stream();
-  if (kind == WR_KIND_FUSED)
+  if (kind == WR_KIND_FUSED) {
     check_status(wr_fused_moe(&a, stream), "fused_moe_forward");
-  else
+    if (g_check_handoff.load(std::memory_order_relaxed))
+      check_status(wr_fused_moe_status(a.workspace, a.workspace_bytes, stream),
+                   "fused_moe_forward");
+  } else
     check_status(wr_naive_moe(&a, stream), "naive_moe_forward");
   return out;
 }
@@ -264,6 +279,9 @@ std::tuple<torch::Tensor, torch::Tensor> gate_topk(torch::Tensor hidden, torch::
   return {ids, ws};
 }
 
+void set_handoff_check(bool enabled) { g_check_handoff.store(enabled); }
+bool handoff_check() { return g_check_handoff.load(); }
+
 py::dict layout(int num_experts, int hidden_dim, int intermediate_dim, int elem_bytes) {
   wr_offsets o;
   check_status(wr_layout(num_experts, hidden_dim, intermediate_dim, elem_bytes, &o), "layout");
@@ -281,20 +299,28 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   const auto opt = py::arg("topk_ids") = py::none();
   const auto optw = py::arg("topk_weights") = py::none();
   m.def("naive_moe_forward", &naive_moe_forward,
-        "Naive multi-kernel MoE forward (host top-K; fp32 or fp16 weights)", py::arg("hidden"),
+        "Naive multi-kernel MoE forward (host top-K; fp32, fp16, bf16, fp8 e4m3 or mxfp4 "
+        "weights)",
+        py::arg("hidden"),
         py::arg("gate_w"), py::arg("weight_buf"), py::arg("num_experts"), py::arg("hidden_dim"),
         py::arg("intermediate_dim"), py::arg("top_k"), py::arg("renormalize") = false, opt, optw);
   m.def("fused_moe_forward", &fused_moe_forward,
-        "Fused decode MoE forward for one token (fp32, fp16, bf16 or fp8 e4m3 weights)", py::arg("hidden"),
+        "Fused decode MoE forward for one token (fp32, fp16, bf16, fp8 e4m3 or mxfp4 weights)",
+        py::arg("hidden"),
         py::arg("gate_w"), py::arg("weight_buf"), py::arg("num_experts"), py::arg("hidden_dim"),
         py::arg("intermediate_dim"), py::arg("top_k"), py::arg("renormalize") = false, opt, optw);
   m.def("batched_fused_moe_forward", &batched_fused_moe_forward,
-        "Batched fused MoE forward for B tokens (fp32, fp16, bf16 or fp8 e4m3 weights)", py::arg("hidden_batch"),
+        "Batched fused MoE forward for B tokens (fp32, fp16, bf16, fp8 e4m3 or mxfp4 weights)",
+        py::arg("hidden_batch"),
         py::arg("gate_w"), py::arg("weight_buf"), py::arg("num_experts"), py::arg("hidden_dim"),
         py::arg("intermediate_dim"), py::arg("top_k"), py::arg("renormalize") = false, opt, optw);
   m.def("gate_topk", &gate_topk, "Router logits, softmax and top-K", py::arg("hidden"),
         py::arg("gate_w"), py::arg("num_experts"), py::arg("hidden_dim"), py::arg("top_k"),
         py::arg("renormalize") = false);
+  m.def("set_handoff_check", &set_handoff_check,
+        "Make fused_moe_forward synchronise and raise if its hand-off wait expired",
+        py::arg("enabled"));
+  m.def("handoff_check", &handoff_check, "Whether fused_moe_forward checks its hand-off");
   m.def("layout", &layout, "Packed expert layout offsets in bytes", py::arg("num_experts"),
         py::arg("hidden_dim"), py::arg("intermediate_dim"), py::arg("elem_bytes"));
   m.def("total_weight_bytes", &wr_total_weight_bytes, "Packed layout size in bytes (-1 if invalid)",

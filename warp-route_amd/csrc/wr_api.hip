@@ -8,7 +8,6 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-
 #include <cstdint>
 
 #include "warp_route.h"
@@ -159,6 +158,8 @@ int validate(const wr_moe_args* a, int kind, Problem* p) {
   p->ws = static_cast<char*>(a->workspace);
   p->ws_bytes = a->workspace_bytes;
   p->vec = kind < 0 ? 1 : choose_vec(a);
+  p->spin_limit = wr::kDefaultSpinLimit;
+  p->wait_extra = 0;
   return WR_OK;
 }
 
@@ -184,6 +185,8 @@ WR_API const char* wr_status_str(int status) {
     case WR_EINVAL_KIND: return "unknown workspace kind";
     case WR_EINVAL_BLOCK:
       return "MXFP4 weights need hidden_dim and intermediate_dim to be multiples of 32";
+    case WR_ETIMEOUT:
+      return "a fused-kernel hand-off wait expired (the affected output rows are NaN)";
     case WR_EHIP: return "HIP runtime error";
     default: return "unknown status";
   }
@@ -247,6 +250,29 @@ WR_API int wr_fused_moe(const wr_moe_args* args, void* stream) {
   const int st = validate(args, WR_KIND_FUSED, &p);
   if (st != WR_OK) return st;
   return hip_status(wr::launch_fused(p, static_cast<hipStream_t>(stream)));
+}
+
+WR_API int wr_fused_moe_opts(const wr_moe_args* args, const wr_fused_opts* opts, void* stream) {
+  Problem p{};
+  const int st = validate(args, WR_KIND_FUSED, &p);
+  if (st != WR_OK) return st;
+  if (opts != nullptr) {
+    if (opts->spin_limit != 0) p.spin_limit = opts->spin_limit;
+    p.wait_extra = opts->wait_extra;
+  }
+  return hip_status(wr::launch_fused(p, static_cast<hipStream_t>(stream)));
+}
+
+WR_API int wr_fused_moe_status(const void* workspace, size_t workspace_bytes, void* stream) {
+  if (workspace == nullptr) return WR_EINVAL_NULL;
+  if (workspace_bytes < wr::FusedWs::kCtrlBytes) return WR_EINVAL_WORKSPACE;
+  const unsigned* word = static_cast<const unsigned*>(workspace) + wr::FusedWs::kTimeoutWord;
+  unsigned v = 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (hipMemcpyAsync(&v, word, sizeof(v), hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return WR_EHIP;
+  return v != 0 ? WR_ETIMEOUT : WR_OK;
 }
 
 WR_API int wr_fused_moe_route(const wr_moe_args* args, void* stream) {

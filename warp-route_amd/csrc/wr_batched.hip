@@ -6,7 +6,9 @@
 // selected expert's weights for every token (src/fused_moe_batched.cu:66-184).
 // Here a call with B tokens is five launches:
 //   1. k_router_logits (wr_kernels.hip): logits[B][64]; it also splits x into
-//      two fp16 terms, x = hi + lo (|x - (hi + lo)| <= 2^-22 |x|).
+//      two 16-bit terms.  fp16 terms are of x 2^e_b, with a power of two e_b
+//      per token that puts max|x 2^e_b| in [2^14, 2^15): hi stays finite and
+//      |x 2^e_b - (hi + lo)| <= 2^-22 |x 2^e_b| + 2^-25 (split_exp).
 //   2. k_route: one block selects every token's top-K (the same
 //      wave_select_topk as every other path, so ids and weights are
 //      bit-identical to the single-token op) and groups the (token, expert)
@@ -19,23 +21,30 @@
 //      pass); the token tile is staged in LDS and shared by the 4 waves.
 //      v_mfma_f32_16x16x32_f16 with A = weight rows (fp16, or fp8 E4M3 codes
 //      converted exactly to fp16 while staging) and B = the hi and lo terms
-//      of x; products are exact and accumulate in fp32.  bf16 weights use
+//      of x; products are exact and accumulate in fp32, and the epilogue
+//      multiplies by 2^-e_b.  bf16 and MXFP4 weights (E2M1 codes times their
+//      E8M0 block scale are exact in bf16 at every scale) use
 //      v_mfma_f32_16x16x32_bf16 with x in two bf16 terms instead
-//      (|x - (hi + lo)| <= 2^-18 |x|, with fp32's exponent range).  Epilogue:
-//      act[pair][row] = w * silu(g) * u (src/fused_moe.cu:192-201), with fp8
-//      row scales applied to g and u (and to the down sums in step 4).
+//      (|x - (hi + lo)| <= 2^-18 |x|, with fp32's exponent range, so no
+//      scaling).  Epilogue: act[pair][row] = w * silu(g) * u
+//      (src/fused_moe.cu:192-201), with fp8 row scales applied to g and u (and
+//      to the down sums in step 4).  With fp16 operands it also folds
+//      max |act[pair][:]| into one word per pair (atomic max).
 //   4. k_dn_mfma: block (row tile, K slice, expert slot): the same scheme on
-//      the down rows against act (split into hi/lo fp16 while staging), four
-//      K slices so that the grid has enough blocks; partial sums per slice.
+//      the down rows against act, split into two terms while staging (fp16
+//      terms of act 2^e_p, e_p from the pair's maximum, undone in the
+//      epilogue), four K slices so that the grid has enough blocks; partial
+//      sums per slice.
 //   5. k_combine: out[t] = sum over t's experts (selection order) and K
 //      slices (ascending) of the partials, in that fixed order.
 // Every sum has a fixed order, so results are deterministic.  The MFMA work
 // is padded to 16 tokens per tile; at 2 MFMAs per product term it stays far
 // below the time the weight stream takes (the path is HBM-bound).
 //
-// Requirements (else the per-token kernels in wr_kernels.hip run): fp16, bf16
-// or fp8 weights with 16-byte aligned rows, h and I multiples of 128, and,
-// for fp16 and fp8, the fp16 range for x and act (|v| < 65504).
+// Requirements (else the per-token kernels in wr_kernels.hip run): fp16,
+// bf16, fp8 or MXFP4 weights with 16-byte aligned rows, and h and I
+// multiples of 128.  The power-of-two scaling leaves no range condition on x
+// or act beyond fp32's own.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -64,11 +73,11 @@ constexpr int kLdsRow = kPieces + 1;    // padded row: spreads lanes over the LD
 typedef f16x8 H8;  // eight 16-bit operands: fp16, or bf16 bit patterns
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// MFMA operand type of a weight type: bf16 for bf16 weights, fp16 otherwise
-// (fp8 codes are staged as fp16).
+// MFMA operand type of a weight type: bf16 for bf16 and MXFP4 weights, fp16
+// otherwise (fp8 codes are staged as fp16).
 template <typename WT>
 constexpr bool bf16_ops() {
-  return std::is_same<WT, bf16w>::value;
+  return std::is_same<WT, bf16w>::value || std::is_same<WT, fp4x2>::value;
 }
 
 template <bool BF>
@@ -344,11 +353,13 @@ __device__ __forceinline__ void gu_tile_load(H8 (&hi)[TP], H8 (&lo)[TP],
   }
 }
 
-// Down: act rows, fp32, split into two fp16 (or, BF, bf16) terms.
+// Down: act rows, fp32, split into two bf16 terms (BF), or two fp16 terms of
+// act 2^sx[q] (sx: the piece's pair exponent, split_exp).
 template <bool BF, int TP>
 __device__ __forceinline__ void dn_tile_load(H8 (&hi)[TP], H8 (&lo)[TP],
                                              const float* __restrict__ act,
-                                             const int64_t (&off)[TP], int kb) {
+                                             const int64_t (&off)[TP], const int (&sx)[TP],
+                                             int kb) {
 #pragma unroll
   for (int q = 0; q < TP; ++q) {
     hi[q] = lo[q] = h8zero();
@@ -358,7 +369,7 @@ __device__ __forceinline__ void dn_tile_load(H8 (&hi)[TP], H8 (&lo)[TP],
       const f32x4 v1 = *reinterpret_cast<const f32x4*>(a + 4);
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
-        const float v = t < 4 ? v0[t] : v1[t - 4];
+        const float v = BF ? (t < 4 ? v0[t] : v1[t - 4]) : ldexpf(t < 4 ? v0[t] : v1[t - 4], sx[q]);
         if constexpr (BF) {
           const __bf16 vh = (__bf16)v;
           hi[q][t] = __builtin_bit_cast(f16, vh);
@@ -457,16 +468,19 @@ __device__ __forceinline__ H8 fp8x8_to_h8(uint32_t a, uint32_t b) {
   return H8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
-// MXFP4: eight codes (one 32-bit word) -> eight fp16 values times the block
-// scale (v_cvt_scalef32_pk_f16_fp4, checked against the E2M1 table; exact
-// while the scaled values are fp16 normals, i.e. scales of 2^-15 and up).
-__device__ __forceinline__ H8 fp4x8_to_h8(uint32_t w, float s) {
-  typedef f16 h2 __attribute__((ext_vector_type(2)));
-  const h2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 0);
-  const h2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 1);
-  const h2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 2);
-  const h2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 3);
-  return H8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+// MXFP4: eight codes (one 32-bit word, element 2i in the low nibble of byte
+// i) -> eight bf16 values times the block scale
+// (v_cvt_scalef32_pk_bf16_fp4).  An E2M1 value has at most two significant
+// bits and the scale is a power of two, so the product is exact in bf16 at
+// every scale bf16's exponent range holds (fp16 would overflow above 2^13 or
+// round below 2^-24).
+__device__ __forceinline__ H8 fp4x8_to_bf8(uint32_t w, float s) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const b2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 0);
+  const b2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 1);
+  const b2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 2);
+  const b2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 3);
+  return __builtin_bit_cast(H8, bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]});
 }
 
 template <typename WT, int ROWS>
@@ -479,7 +493,7 @@ __device__ __forceinline__ void w_store(WTile<ROWS>& t, const WRegs<WT, ROWS>& r
       const int c = 4 * (lane % LR);
       const float s = e8m0_value(r.e[i]);
 #pragma unroll
-      for (int p = 0; p < 4; ++p) t.w[row][c + p] = fp4x8_to_h8(r.v[i][p], s);
+      for (int p = 0; p < 4; ++p) t.w[row][c + p] = fp4x8_to_bf8(r.v[i][p], s);
     } else if constexpr (std::is_same<WT, fp8w>::value) {
       const int c = 2 * (lane % LR);
       t.w[row][c] = fp8x8_to_h8(r.v[i][0], r.v[i][1]);
@@ -496,6 +510,16 @@ __device__ __forceinline__ void w_store(WTile<ROWS>& t, const WRegs<WT, ROWS>& r
 // the K loop has no per-tile branches.  A wave's weight tile holds its 16 gate
 // rows (tile rows 0-15) and the same 16 up rows (tile rows 16-31).
 // ---------------------------------------------------------------------------
+// Range scaling of the fp16-operand passes (unused with bf16 operands): x_exp
+// = the tokens' x exponents, amax = the per-pair act maxima in global memory
+// (kAmaxStride words apart), s_amax = this block's TOK-word LDS copy for the
+// current pass, zero between passes.
+struct GuScale {
+  const int32_t* x_exp;
+  unsigned* amax;
+  unsigned* s_amax;
+};
+
 template <typename WT, bool LO, int NT, int TOK>
 __device__ __forceinline__ void gu_pass(TokTile<TOK>& xs, WTile<32>& wt,
                                         const WT* const (&wbase)[WRegs<WT, 32>::N],
@@ -503,7 +527,8 @@ __device__ __forceinline__ void gu_pass(TokTile<TOK>& xs, WTile<32>& wt,
                                         const f16* __restrict__ x_hi,
                                         const f16* __restrict__ x_lo, const BatchRoute& r,
                                         int p0, int mt, float* __restrict__ act, int row0,
-                                        const float* __restrict__ sc, const Geom& g, int lane) {
+                                        const float* __restrict__ sc, const GuScale& xsc,
+                                        const Geom& g, int lane) {
   f32x4 ag[NT], au[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) ag[n] = au[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -511,6 +536,15 @@ __device__ __forceinline__ void gu_pass(TokTile<TOK>& xs, WTile<32>& wt,
   int64_t off[TP];
   tile_rows(off, r.pair_tok + p0, 0, mt, g.h);
   const int ns = g.h / kBK;
+  // fp16 operands: the epilogue tokens' x exponents, loaded here so that the
+  // loads are in flight with the first K step's.
+  constexpr bool SC = !bf16_ops<WT>();
+  int xe[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int tn = n * 16 + (lane & 15);
+    xe[n] = (SC && tn < mt) ? xsc.x_exp[r.pair_tok[p0 + tn]] : 0;
+  }
 
   // Software pipeline, one K step deep: step s+1's weight and token loads are
   // issued before step s's MFMAs.
@@ -550,6 +584,8 @@ __device__ __forceinline__ void gu_pass(TokTile<TOK>& xs, WTile<32>& wt,
 
   // D layout: lane holds token n*16 + (lane % 16), rows 4 (lane / 16) .. +4.
   // fp8: sc = the expert's row scales, gate rows at sc, up rows at sc + I.
+  // fp16 operands: the sums are of x 2^e_t; ldexpf by -e_t undoes that
+  // exactly (a power of two).
   const int rq = row0 + (lane >> 4) * 4;
   f32x4 sg, su;
   if constexpr (std::is_same<WT, fp8w>::value) {
@@ -559,18 +595,42 @@ __device__ __forceinline__ void gu_pass(TokTile<TOK>& xs, WTile<32>& wt,
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     const int tn = n * 16 + (lane & 15);
+    float m = 0.0f;
     if (tn < mt) {
       const int p = p0 + tn;
       const float w = r.pair_w[p];
       f32x4 v;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
+        const float gs = SC ? ldexpf(ag[n][i], -xe[n]) : ag[n][i];
+        const float us = SC ? ldexpf(au[n][i], -xe[n]) : au[n][i];
         if constexpr (std::is_same<WT, fp8w>::value)
-          v[i] = w * (silu(ag[n][i] * sg[i]) * (au[n][i] * su[i]));
+          v[i] = w * (silu(gs * sg[i]) * (us * su[i]));
         else
-          v[i] = w * (silu(ag[n][i]) * au[n][i]);
+          v[i] = w * (silu(gs) * us);
+        m = fmaxf(m, fabsf(v[i]));
       }
       *reinterpret_cast<f32x4*>(act + (int64_t)p * g.I + rq) = v;
+    }
+    if constexpr (SC) {
+      // max over the 16 rows of this wave's tile (lanes l, l^16, l^32, l^48
+      // hold the same token), then over the block's waves in LDS.
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      if (lane < 16 && tn < mt) atomicMax(xsc.s_amax + tn, __float_as_uint(m));
+    }
+  }
+  if constexpr (SC) {
+    // One global atomic per token of the pass.  Non-negative floats order
+    // like their bit patterns.  The thread that reads an LDS word clears it
+    // for the next pass, whose first write comes after the next pass's K-loop
+    // barriers.
+    __syncthreads();
+    if ((int)threadIdx.x < mt) {
+      const unsigned v = xsc.s_amax[threadIdx.x];
+      xsc.s_amax[threadIdx.x] = 0u;
+      __hip_atomic_fetch_max(xsc.amax + (int64_t)(p0 + threadIdx.x) * BatchWs::kAmaxStride, v,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -588,7 +648,9 @@ struct GuRouteLds<false> {};
 template <typename WT, bool LO, int TOK, bool ROUTE>
 __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
                                                   const f16* __restrict__ x_hi,
-                                                  const f16* __restrict__ x_lo, BatchRoute r,
+                                                  const f16* __restrict__ x_lo,
+                                                  const int32_t* __restrict__ x_exp,
+                                                  unsigned* __restrict__ amax, BatchRoute r,
                                                   float* __restrict__ act, Geom g,
                                                   const float* __restrict__ logits,
                                                   int32_t* __restrict__ ids_out,
@@ -596,6 +658,9 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
   __shared__ TokTile<TOK> xs;
   __shared__ WTile<32> wts[kBlk / kWave];
   __shared__ GuRouteLds<ROUTE> rl;
+  __shared__ unsigned s_amax[bf16_ops<WT>() ? 1 : TOK];
+  if (!bf16_ops<WT>() && (int)threadIdx.x < TOK) s_amax[threadIdx.x] = 0u;
+  const GuScale xsc{x_exp, amax, s_amax};
   const int slot = blockIdx.y;
   int e, pbeg, M;
   if constexpr (ROUTE) {
@@ -641,18 +706,18 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
     const int mt = min(TOK, M - m0);
     const int p0 = pbeg + m0;
     if constexpr (TOK == 16) {
-      gu_pass<WT, LO, 1, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane);
+      gu_pass<WT, LO, 1, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
     } else if constexpr (TOK == 32) {
       if (mt <= 16)
-        gu_pass<WT, LO, 1, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane);
+        gu_pass<WT, LO, 1, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
       else
-        gu_pass<WT, LO, 2, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane);
+        gu_pass<WT, LO, 2, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
     } else {
       switch ((mt + 15) / 16) {
-        case 1: gu_pass<WT, LO, 1, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
-        case 2: gu_pass<WT, LO, 2, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
-        case 3: gu_pass<WT, LO, 3, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
-        default: gu_pass<WT, LO, 4, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, g, lane); break;
+        case 1: gu_pass<WT, LO, 1, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
+        case 2: gu_pass<WT, LO, 2, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
+        case 3: gu_pass<WT, LO, 3, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
+        default: gu_pass<WT, LO, 4, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
       }
     }
   }
@@ -662,25 +727,52 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
 // Down.  grid (h / 64, kKSplit, expert slots).  K slice ks covers steps
 // [nsteps * ks / kKSplit, nsteps * (ks + 1) / kKSplit).
 // ---------------------------------------------------------------------------
+// The exponent e_p of pair p's act split (split_exp of its maximum); 0 with
+// bf16 operands.
+template <typename WT>
+__device__ __forceinline__ int pair_exp(const unsigned* __restrict__ amax, int p) {
+  if constexpr (bf16_ops<WT>()) {
+    (void)amax;
+    (void)p;
+    return 0;
+  } else {
+    return split_exp(__uint_as_float(amax[(int64_t)p * BatchWs::kAmaxStride]), false);
+  }
+}
+
 template <typename WT, int NT, int TOK>
 __device__ __forceinline__ void dn_pass(TokTile<TOK>& xs, WTile<16>& wt,
                                         const WT* const (&wbase)[WRegs<WT, 16>::N],
                                         const uint8_t* const (&wsc)[WRegs<WT, 16>::N],
-                                        const float* __restrict__ act, int p0, int mt, int sb,
-                                        int se, float* __restrict__ y, int row0,
+                                        const float* __restrict__ act,
+                                        const unsigned* __restrict__ amax, int p0, int mt,
+                                        int sb, int se, float* __restrict__ y, int row0,
                                         const float* __restrict__ sdown, const Geom& g,
                                         int lane) {
   f32x4 acc[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // The epilogue tokens' act exponents, loaded before the K loop.
+  int ae[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int tn = n * 16 + (lane & 15);
+    ae[n] = tn < mt ? pair_exp<WT>(amax, p0 + tn) : 0;
+  }
   if (sb < se) {
     constexpr int TP = tile_pieces<TOK>();
     int64_t off[TP];
     tile_rows(off, nullptr, p0, mt, g.I);
+    int sx[TP];  // each staged piece's pair exponent
+#pragma unroll
+    for (int q = 0; q < TP; ++q) {
+      const int n = ((int)threadIdx.x + kBlk * q) / kPieces;
+      sx[q] = n < mt ? pair_exp<WT>(amax, p0 + n) : 0;
+    }
     WRegs<WT, 16> wr;
     H8 th[TP], tl[TP];
     w_load<WT, 16>(wr, wbase, wsc, sb * kBK);
-    dn_tile_load<bf16_ops<WT>()>(th, tl, act, off, sb * kBK);
+    dn_tile_load<bf16_ops<WT>()>(th, tl, act, off, sx, sb * kBK);
     for (int s = sb; s < se; ++s) {
       __syncthreads();
       tile_store(xs, th, tl, true);
@@ -688,7 +780,7 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK>& xs, WTile<16>& wt,
       __syncthreads();
       if (s + 1 < se) {
         w_load<WT, 16>(wr, wbase, wsc, (s + 1) * kBK);
-        dn_tile_load<bf16_ops<WT>()>(th, tl, act, off, (s + 1) * kBK);
+        dn_tile_load<bf16_ops<WT>()>(th, tl, act, off, sx, (s + 1) * kBK);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -703,7 +795,8 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK>& xs, WTile<16>& wt,
       }
     }
   }
-  // fp8: rows row0 + 4 (lane / 16) .. + 4 times their scales.
+  // The sums are of act 2^e_p (fp16 operands): ldexpf by -e_p undoes that
+  // exactly.  fp8: rows row0 + 4 (lane / 16) .. + 4 times their scales.
   const int rq = row0 + (lane >> 4) * 4;
   f32x4 sd;
   if constexpr (std::is_same<WT, fp8w>::value) sd = *reinterpret_cast<const f32x4*>(sdown + rq);
@@ -712,6 +805,10 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK>& xs, WTile<16>& wt,
     const int tn = n * 16 + (lane & 15);
     if (tn < mt) {
       f32x4 v = acc[n];
+      if constexpr (!bf16_ops<WT>()) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = ldexpf(v[i], -ae[n]);
+      }
       if constexpr (std::is_same<WT, fp8w>::value) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] *= sd[i];
@@ -724,6 +821,7 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK>& xs, WTile<16>& wt,
 template <typename WT, int TOK>
 __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, BatchRoute r,
                                                   const float* __restrict__ act,
+                                                  const unsigned* __restrict__ amax,
                                                   float* __restrict__ ypart, Geom g, int P) {
   __shared__ TokTile<TOK> xs;
   __shared__ WTile<16> wts[kBlk / kWave];
@@ -759,18 +857,18 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, B
   for (int m0 = 0; m0 < M; m0 += TOK) {
     const int mt = min(TOK, M - m0);
     if constexpr (TOK == 16) {
-      dn_pass<WT, 1, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+      dn_pass<WT, 1, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
     } else if constexpr (TOK == 32) {
       if (mt <= 16)
-        dn_pass<WT, 1, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+        dn_pass<WT, 1, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
       else
-        dn_pass<WT, 2, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+        dn_pass<WT, 2, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
     } else {
       switch ((mt + 15) / 16) {
-        case 1: dn_pass<WT, 1, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-        case 2: dn_pass<WT, 2, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-        case 3: dn_pass<WT, 3, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-        default: dn_pass<WT, 4, TOK>(xs, wt, wbase, wsc, act, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 1: dn_pass<WT, 1, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 2: dn_pass<WT, 2, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 3: dn_pass<WT, 3, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        default: dn_pass<WT, 4, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
       }
     }
   }
@@ -841,22 +939,25 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
   // small batches take token tiles of 16 or 32.
   if (p.B <= WR_SMALL_TILE_MAX_B) {
     hipLaunchKernelGGL((k_gu_mfma<WT, LO, 16, true>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s,
-                       wb, w.x_hi, w.x_lo, w.route, w.act, g, w.logits, p.topk_ids, p.topk_w);
+                       wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, w.logits,
+                       p.topk_ids, p.topk_w);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     hipLaunchKernelGGL((k_dn_mfma<WT, 16>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk),
-                       0, s, wb, w.route, w.act, w.ypart, g, P);
+                       0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
   } else if (p.B <= WR_MID_TILE_MAX_B) {
     hipLaunchKernelGGL((k_gu_mfma<WT, LO, 32, false>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s,
-                       wb, w.x_hi, w.x_lo, w.route, w.act, g, nullptr, nullptr, nullptr);
+                       wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, nullptr, nullptr,
+                       nullptr);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     hipLaunchKernelGGL((k_dn_mfma<WT, 32>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk),
-                       0, s, wb, w.route, w.act, w.ypart, g, P);
+                       0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
   } else {
     hipLaunchKernelGGL((k_gu_mfma<WT, LO, kMaxTok, false>), dim3(p.I / kBM, slots), dim3(kBlk),
-                       0, s, wb, w.x_hi, w.x_lo, w.route, w.act, g, nullptr, nullptr, nullptr);
+                       0, s, wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, nullptr,
+                       nullptr, nullptr);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     hipLaunchKernelGGL((k_dn_mfma<WT, kMaxTok>), dim3(p.h / kBM, BatchWs::kKSplit, slots),
-                       dim3(kBlk), 0, s, wb, w.route, w.act, w.ypart, g, P);
+                       dim3(kBlk), 0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
   }
   if ((err = hipGetLastError()) != hipSuccess) return err;
   static_assert(WR_MAX_TOPK == 6, "one combine instantiation per k");
@@ -880,7 +981,10 @@ bool grouped_ok(const Problem& p) {
 
 hipError_t launch_grouped(const Problem& p, hipStream_t s) {
   const BatchWs w = BatchWs::carve(p.ws, p.E, p.h, p.I, p.k, p.B);
-  hipError_t err = launch_logits_split(p, w.logits, w.x_hi, w.x_lo, p.wdt == WR_BF16 ? 1 : 0, s);
+  // bf16 operands (bf16 and MXFP4 weights): bf16 terms, no scaling.
+  const bool bf = p.wdt == WR_BF16 || p.wdt == WR_MXFP4;
+  hipError_t err = launch_logits_split(p, w.logits, w.x_hi, w.x_lo, w.x_exp,
+                                       bf ? nullptr : w.amax, bf ? 1 : 0, s);
   if (err != hipSuccess) return err;
   if (p.wdt == WR_FP8_E4M3)
     return p.adt == WR_F16 ? grouped_t<fp8w, f16>(p, w, s) : grouped_t<fp8w, float>(p, w, s);

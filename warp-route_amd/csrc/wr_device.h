@@ -136,6 +136,23 @@ __device__ __forceinline__ float wave_max(float v) {
   return lane_bcast(v, 63);
 }
 
+// Power-of-two exponent e that brings amax = max|v| into [2^14, 2^15) before
+// the values v are split into two fp16 terms, hi = fp16(v 2^e) and
+// lo = fp16(v 2^e - hi).  Then hi is finite (|v 2^e| < 2^15 < 65504), and
+// |v 2^e - (hi + lo)| <= 2^-22 |v 2^e| + 2^-25: lo is an fp16 normal unless
+// |v| < 2^-17 amax, and below that its absolute error (half the fp16
+// subnormal spacing) is 2^-39 of the scaled maximum.  Returns 0 for amax 0,
+// inf or NaN (nothing to scale, or no finite result anyway).  With
+// no_down, e >= 0: fp16 inputs are never scaled down, so v 2^e stays exact
+// in fp16 and lo = 0.
+__device__ __forceinline__ int split_exp(float amax, bool no_down) {
+  if (!(amax > 0.0f) || !(amax <= 3.402823466e38f)) return 0;
+  int ex;
+  (void)frexpf(amax, &ex);  // amax = m 2^ex, m in [0.5, 1)
+  const int e = 15 - ex;
+  return (no_down && e < 0) ? 0 : e;
+}
+
 // SiLU(g) = g / (1 + exp(-g)) (src/fused_moe.cu:30-32), with the accurate
 // OCML expf and IEEE division.
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }

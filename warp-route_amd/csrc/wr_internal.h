@@ -26,7 +26,14 @@ struct Problem {
   int64_t stride_b, off_up_b, off_down_b;  // layout, bytes
   int64_t off_scale_b;  // fp8 scales [3][I] fp32 within an expert block, bytes; -1 if none
   int vec;  // elements per lane per weight access: 16 / element bytes, or 1
+  // Single-token hand-off wait: polls before a down block gives up, and a
+  // count added to every arrival target (nonzero only to force the expiry
+  // path from the host in tests: the wait then cannot complete).
+  unsigned spin_limit, wait_extra;
 };
+
+// Polls of the single-token hand-off wait before it expires (about 0.2 s).
+constexpr unsigned kDefaultSpinLimit = 1u << 20;
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 constexpr size_t kWsAlign = 256;
@@ -92,9 +99,20 @@ struct BatchRoute {
 
 struct BatchWs {
   static constexpr int kKSplit = 4;  // K slices of the down GEMM
+  // Per-pair act maxima sit one per 256-byte line, so that the gate/up
+  // blocks' atomic max updates of different pairs do not serialise.
+  static constexpr int kAmaxStride = 64;  // words
   float* logits;  // [B][WR_MAX_EXPERTS]
-  _Float16* x_hi;  // [B][h]: x = hi + lo (fp16 terms, or bf16 bit patterns for bf16 weights)
+  // x 2^x_exp[b] = hi + lo: fp16 terms (x_exp chosen so that max|x 2^x_exp|
+  // lies in [2^14, 2^15)), or bf16 bit patterns for bf16-operand weights
+  // (bf16 and MXFP4; x_exp = 0).
+  _Float16* x_hi;  // [B][h]
   _Float16* x_lo;  // [B][h]
+  int32_t* x_exp;  // [B]
+  // amax[p * kAmaxStride]: max |act[p][:]| as fp32 bits (fp16-operand
+  // weights only), built with atomic max by the gate/up kernel; the down
+  // kernel scales pair p's act by a power of two from it before splitting.
+  unsigned* amax;
   BatchRoute route;
   float* act;    // [P][I], grouped pair order, scaled by the gate weight
   float* ypart;  // [kKSplit][P][h]: down partial sums
@@ -120,6 +138,8 @@ struct BatchWs {
     w.logits = reinterpret_cast<float*>(take((size_t)B * WR_MAX_EXPERTS * 4));
     w.x_hi = reinterpret_cast<_Float16*>(take((size_t)B * h * 2));
     w.x_lo = reinterpret_cast<_Float16*>(take((size_t)B * h * 2));
+    w.x_exp = reinterpret_cast<int32_t*>(take((size_t)B * 4));
+    w.amax = reinterpret_cast<unsigned*>(take(P * kAmaxStride * 4));
     w.route.sel_id = reinterpret_cast<int32_t*>(take(P * 4));
     w.route.sel_w = reinterpret_cast<float*>(take(P * 4));
     w.route.pair_tok = reinterpret_cast<int32_t*>(take(P * 4));
@@ -162,10 +182,12 @@ struct NaiveWs {
 // Launchers (wr_kernels.hip, wr_naive.hip).  Each returns the first HIP
 // error it meets.
 hipError_t launch_logits(const Problem& p, float* logits, hipStream_t s);
-// Logits, plus x split into two 16-bit terms x = hi + lo: fp16 (lo = 0 for
-// fp16 x), or bf16 when split_bf16.
+// Logits, plus x split into two 16-bit terms for the grouped batched path:
+// bf16 terms x = hi + lo when split_bf16, else fp16 terms
+// x 2^x_exp[b] = hi + lo (lo = 0 for fp16 x); also zeroes amax (k words per
+// token, BatchWs::kAmaxStride apart) when it is not NULL.
 hipError_t launch_logits_split(const Problem& p, float* logits, _Float16* x_hi, _Float16* x_lo,
-                               int split_bf16, hipStream_t s);
+                               int32_t* x_exp, unsigned* amax, int split_bf16, hipStream_t s);
 // Grouped batched path: usable when grouped_ok(p).
 bool grouped_ok(const Problem& p);
 hipError_t launch_grouped(const Problem& p, hipStream_t s);

@@ -119,15 +119,19 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 // Wave q (0..3) of a 4-wave group: fp32 partial dot over quarter q of the row
 // (quarters are whole 64*VEC-element chunks).  Every producer of logits uses
 // this and the same combine order, so all of them produce identical bits.
+// With want_max it also sets xmax = max |x| over the quarter (every lane),
+// from the same loads; the sums are unaffected.
 template <typename XT, int VEC>
 __device__ __forceinline__ float router_partial(const float* __restrict__ row,
-                                                const XT* __restrict__ x, int h, int q) {
+                                                const XT* __restrict__ x, int h, int q,
+                                                bool want_max, float& xmax) {
   const int lane = threadIdx.x & (kWave - 1);
   constexpr int CH = kWave * VEC;
   const int span = (h + 4 * CH - 1) / (4 * CH) * CH;
   const int beg = q * span;
   const int end = min(h, beg + span);
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float m = 0.0f;
   for (int c0 = beg + lane * VEC; c0 < end; c0 += 8 * CH) {
     float w[8][VEC], xv[8][VEC];
 #pragma unroll
@@ -145,7 +149,14 @@ __device__ __forceinline__ float router_partial(const float* __restrict__ row,
     for (int u = 0; u < 8; ++u)
 #pragma unroll
       for (int i = 0; i < VEC; ++i) acc[u & 3] = fmaf(w[u][i], xv[u][i], acc[u & 3]);
+    if (want_max) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) m = fmaxf(m, fabsf(xv[u][i]));
+    }
   }
+  xmax = want_max ? wave_max(m) : 0.0f;
   return wave_sum((acc[0] + acc[1]) + (acc[2] + acc[3]));
 }
 
@@ -153,52 +164,76 @@ __device__ __forceinline__ float router_combine(const float* p) {
   return (p[0] + p[1]) + (p[2] + p[3]);
 }
 
+// x split into two 16-bit terms for the grouped batched path.  hi == NULL:
+// no split.  bf16: bf16 terms x = hi + lo (bf16 keeps fp32's exponent range,
+// so no scaling).  Otherwise fp16 terms of x 2^e, e = split_exp(max|x|), and
+// exp[b] = e; amax (when not NULL) gets its k words of token b zeroed, every
+// kAmaxStride words.
+struct XSplit {
+  f16* hi;
+  f16* lo;
+  int32_t* exp;
+  unsigned* amax;
+  int k;
+  int bf16;
+};
+
 // grid (E, B), block 256.  Token b's logits go to logits[b * 64 + e] (padded
 // so that consumers can read all 64 with scalar loads).  Block (0, 0) also
 // zeroes the words zero[i * zstride], i < nzero <= kBlock (the fused kernel's
 // arrival counters, timeout flag and rotation masks), which the next kernel on
-// the stream reads.
-// With x_hi != nullptr, block (e, b) also writes its 1/E share of token b's x
-// as two 16-bit terms x = hi + lo: fp16 terms, or bf16 terms when split_bf16
-// (bit patterns in the same buffers),
-// as two fp16 terms, hi = fp16(x) and lo = fp16(x - hi) (lo = 0 for fp16 x),
-// for the batched MFMA path.
+// the stream reads.  With xs.hi != NULL, block (e, b) also writes its 1/E
+// share of token b's split x (XSplit); every block of the token derives the
+// same exponent from the whole row.
 template <typename XT, int VEC>
 __global__ __launch_bounds__(kBlock) void k_router_logits(const float* __restrict__ gate_w,
                                                           const XT* __restrict__ x,
                                                           float* __restrict__ logits, int E,
                                                           int h, unsigned* __restrict__ zero,
-                                                          int nzero, int zstride,
-                                                          f16* __restrict__ x_hi,
-                                                          f16* __restrict__ x_lo,
-                                                          int split_bf16) {
+                                                          int nzero, int zstride, XSplit xs) {
   __shared__ float part[4];
+  __shared__ float pmax[4];
   const int q = threadIdx.x / kWave;
   const int e = blockIdx.x, b = blockIdx.y;
-  if (x_hi != nullptr) {
-    const int cs = (h + E - 1) / E;
-    const int end = min(h, (e + 1) * cs);
-    for (int i = e * cs + (int)threadIdx.x; i < end; i += kBlock) {
-      const float v = (float)x[(int64_t)b * h + i];
-      const f16 vh = (f16)v;
-      if (split_bf16) {
-        const __bf16 bh = (__bf16)v;
-        const __bf16 bl = (__bf16)(v - (float)bh);
-        x_hi[(int64_t)b * h + i] = __builtin_bit_cast(f16, bh);
-        x_lo[(int64_t)b * h + i] = __builtin_bit_cast(f16, bl);
-      } else {
-        x_hi[(int64_t)b * h + i] = vh;
-        x_lo[(int64_t)b * h + i] =
-            std::is_same<XT, float>::value ? (f16)(v - (float)vh) : (f16)0.0f;
-      }
-    }
+  const bool scaled = xs.hi != nullptr && !xs.bf16;
+  float m = 0.0f;
+  const float p = router_partial<XT, VEC>(gate_w + (int64_t)e * h, x + (int64_t)b * h, h, q,
+                                          scaled, m);
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    part[q] = p;
+    pmax[q] = m;
   }
   if (zero != nullptr && e == 0 && b == 0 && (int)threadIdx.x < nzero)
     zero[(int64_t)threadIdx.x * zstride] = 0u;
-  const float p = router_partial<XT, VEC>(gate_w + (int64_t)e * h, x + (int64_t)b * h, h, q);
-  if ((threadIdx.x & (kWave - 1)) == 0) part[q] = p;
   __syncthreads();
   if (threadIdx.x == 0) logits[(int64_t)b * WR_MAX_EXPERTS + e] = router_combine(part);
+  if (xs.hi != nullptr) {
+    const XT* xb = x + (int64_t)b * h;
+    const int ex = scaled ? split_exp(fmaxf(fmaxf(pmax[0], pmax[1]), fmaxf(pmax[2], pmax[3])),
+                                      std::is_same<XT, f16>::value)
+                          : 0;
+    const int cs = (h + E - 1) / E;
+    const int end = min(h, (e + 1) * cs);
+    for (int i = e * cs + (int)threadIdx.x; i < end; i += kBlock) {
+      const float v = (float)xb[i];
+      if (xs.bf16) {
+        const __bf16 bh = (__bf16)v;
+        const __bf16 bl = (__bf16)(v - (float)bh);
+        xs.hi[(int64_t)b * h + i] = __builtin_bit_cast(f16, bh);
+        xs.lo[(int64_t)b * h + i] = __builtin_bit_cast(f16, bl);
+      } else {
+        const float vs = ldexpf(v, ex);
+        const f16 vh = (f16)vs;
+        xs.hi[(int64_t)b * h + i] = vh;
+        xs.lo[(int64_t)b * h + i] = (f16)(vs - (float)vh);
+      }
+    }
+    if (e == 0) {
+      if (threadIdx.x == 0 && xs.exp != nullptr) xs.exp[b] = ex;
+      if (xs.amax != nullptr && (int)threadIdx.x < xs.k)
+        xs.amax[((int64_t)b * xs.k + threadIdx.x) * BatchWs::kAmaxStride] = 0u;
+    }
+  }
 }
 
 // Standalone gate: grid B, block 1024 (four 4-wave groups).  Group g handles
@@ -215,7 +250,9 @@ __global__ __launch_bounds__(1024) void k_gate_topk(const float* __restrict__ ga
   const int g = wave / 4, q = wave % 4;
   const int b = blockIdx.x;
   for (int e = g; e < E; e += 4) {
-    const float p = router_partial<XT, VEC>(gate_w + (int64_t)e * h, x + (int64_t)b * h, h, q);
+    float unused;
+    const float p =
+        router_partial<XT, VEC>(gate_w + (int64_t)e * h, x + (int64_t)b * h, h, q, false, unused);
     if (lane == 0) part[e][q] = p;
   }
   __syncthreads();
@@ -500,8 +537,10 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 // Why this cannot deadlock: workgroups of a grid are dispatched in index
 // order (on each XCD), so every gate/up block is dispatched before any down
 // block that could occupy its slot, and gate/up blocks never wait.  Every wait
-// is nevertheless bounded (about 0.2 s); on expiry the block records a
-// timeout flag and finishes, so the kernel cannot hang.
+// is nevertheless bounded (about 0.2 s), so the kernel cannot hang.  On
+// expiry the block sets the timeout word and writes NaN to its output rows
+// (its act reads may have been incomplete), so a broken hand-off can never
+// pass for a plausible result; wr_fused_moe_status reports the word.
 //
 // Why down blocks read fresh act without invalidating L2 (each XCD has its
 // own L2, not coherent with the others): blocks are dispatched to the XCDs
@@ -526,11 +565,12 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 // ---------------------------------------------------------------------------
 struct Handoff {
   unsigned* cnt;        // FusedWs::kCounters counters, FusedWs::kCounterStride words apart
-  unsigned* timeout;    // set to 1 if a wait expired (results then invalid)
+  unsigned* timeout;    // set to 1 if a wait expired (that block's rows are then NaN)
   unsigned* rot;        // FusedWs::kCounters rotation masks, FusedWs::kCounterStride words apart
   int n1;               // gate/up blocks (the first n1 block ids), a multiple of 8 LB
   int chunks;           // k * bpk
   unsigned spin_limit;  // polls before a wait gives up
+  unsigned wait_extra;  // added to every arrival target: 0, or (tests) a wait that cannot complete
 };
 
 // The chunk gate/up block b computes: a permutation of each aligned group of
@@ -878,6 +918,7 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   constexpr bool kFp8 = std::is_same<WT, fp8w>::value;
   __shared__ float part[kWavesPerBlock][RPD];
   __shared__ float sdn[kFp8 ? WR_MAX_TOPK * RPD : 1];  // fp8 row scales [kk][j]
+  __shared__ int expired;  // this block's wait gave up
   const int r0 = ((int)blockIdx.x - hs.n1) * RPD;
   const int nrows = min(RPD, g.h - r0);
   const int nch = (g.I + kWave * VEC - 1) / (kWave * VEC);
@@ -928,18 +969,22 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
     // Lane c waits for the blocks counted by counter c: ids b < n1, b % 64 == c.
     const int c = lane;
     const unsigned target =
-        c < hs.n1 ? (unsigned)((hs.n1 - c + FusedWs::kCounters - 1) / FusedWs::kCounters) : 0u;
+        (c < hs.n1 ? (unsigned)((hs.n1 - c + FusedWs::kCounters - 1) / FusedWs::kCounters)
+                   : 0u) + hs.wait_extra;
     const unsigned* ctr = hs.cnt + c * FusedWs::kCounterStride;
     unsigned spins = 0;
+    int gave_up = 0;
     while (__ballot(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
                     target) != 0) {
       if (++spins > hs.spin_limit) {
+        gave_up = 1;
         if (lane == 0)
           __hip_atomic_store(hs.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
       __builtin_amdgcn_s_sleep(8);
     }
+    if (lane == 0) expired = gave_up;
     // One rotation for every gate/up block <=> exactly one bit in the OR of
     // the masks.
     const unsigned m = __hip_atomic_load(hs.rot + c * FusedWs::kCounterStride, __ATOMIC_RELAXED,
@@ -991,7 +1036,9 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   }
   __syncthreads();
   if (wave == 0 && lane < nrows)
-    out[r0 + lane] = to_out<XT>((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
+    out[r0 + lane] = to_out<XT>(expired ? __builtin_nanf("")
+                                        : (part[0][lane] + part[1][lane]) +
+                                              (part[2][lane] + part[3][lane]));
 }
 
 // ---------------------------------------------------------------------------
@@ -1052,16 +1099,15 @@ bool router_vec4(const Problem& p) {
 
 template <typename XT>
 hipError_t logits_t(const Problem& p, float* logits, unsigned* zero, int nzero, int zstride,
-                    hipStream_t s, f16* x_hi = nullptr, f16* x_lo = nullptr,
-                    int split_bf16 = 0) {
+                    hipStream_t s, XSplit xs = XSplit{nullptr, nullptr, nullptr, nullptr, 0, 0}) {
   const dim3 grid(p.E, p.B);
   const XT* x = static_cast<const XT*>(p.x);
   if (router_vec4(p))
     hipLaunchKernelGGL((k_router_logits<XT, 4>), grid, dim3(kBlock), 0, s, p.gate_w, x, logits,
-                       p.E, p.h, zero, nzero, zstride, x_hi, x_lo, split_bf16);
+                       p.E, p.h, zero, nzero, zstride, xs);
   else
     hipLaunchKernelGGL((k_router_logits<XT, 1>), grid, dim3(kBlock), 0, s, p.gate_w, x, logits,
-                       p.E, p.h, zero, nzero, zstride, x_hi, x_lo, split_bf16);
+                       p.E, p.h, zero, nzero, zstride, xs);
   return hipGetLastError();
 }
 
@@ -1099,7 +1145,8 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   hs.rot = w.ctrl + FusedWs::kRotWord;
   hs.n1 = fused_n1(p.I, p.k, RPW);
   hs.chunks = fused_chunks(p.I, p.k, RPW);
-  hs.spin_limit = 1u << 20;
+  hs.spin_limit = p.spin_limit;
+  hs.wait_extra = p.wait_extra;
   // fp8 down blocks take twice the rows and half the chunks in flight: the
   // same weight bytes per tile as fp16, and half the act reads per weight byte.
   // MXFP4 (32 act values per lane and chunk): 8 rows, one chunk in flight.
@@ -1238,9 +1285,10 @@ hipError_t launch_fused_route(const Problem& p, hipStream_t s) { return run_rout
 hipError_t launch_fused_ffn(const Problem& p, hipStream_t s) { return run_ffn_only(p, s); }
 
 hipError_t launch_logits_split(const Problem& p, float* logits, f16* x_hi, f16* x_lo,
-                               int split_bf16, hipStream_t s) {
-  return p.adt == WR_F16 ? logits_t<f16>(p, logits, nullptr, 0, 0, s, x_hi, x_lo, split_bf16)
-                         : logits_t<float>(p, logits, nullptr, 0, 0, s, x_hi, x_lo, split_bf16);
+                               int32_t* x_exp, unsigned* amax, int split_bf16, hipStream_t s) {
+  const XSplit xs{x_hi, x_lo, x_exp, amax, p.k, split_bf16};
+  return p.adt == WR_F16 ? logits_t<f16>(p, logits, nullptr, 0, 0, s, xs)
+                         : logits_t<float>(p, logits, nullptr, 0, 0, s, xs);
 }
 
 hipError_t launch_batched(const Problem& p, hipStream_t s) {

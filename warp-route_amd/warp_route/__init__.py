@@ -6,7 +6,11 @@ plus per-expert gate/up/down parameter lists, dispatched to the fused kernel
 for a single token and to the batched kernel for [B, hidden] inputs.  Unlike
 the reference, which repacks every expert on every forward
 (warp_route/__init__.py:81), the packed buffer is cached and rebuilt only when
-a parameter has changed in place or been replaced.
+a parameter has changed in place or been replaced (its identity, storage
+pointer or version counter differ).  Writes made through ``p.data`` bypass
+the version counter; call ``MoELayer.invalidate_packed()`` after them, or
+construct the layer with ``cache_packed=False`` to repack on every forward
+as the reference does.
 """
 from __future__ import annotations
 
@@ -38,11 +42,16 @@ class MoELayer(nn.Module):
             (torch.float32 as in the reference, torch.float16, torch.bfloat16,
             torch.float8_e4m3fn with per-row fp32 scales, or
             torch.float4_e2m1fn_x2 for MXFP4).
+        cache_packed: keep the packed buffer between forwards, rebuilding it
+            when a parameter is replaced or changed in place through autograd-
+            visible ops (which bump its version counter).  Writes through
+            ``p.data`` are not seen: call ``invalidate_packed()`` after them.
+            False repacks on every forward, as the reference does.
     """
 
     def __init__(self, num_experts: int, hidden_dim: int, intermediate_dim: int,
                  top_k: int = 2, renormalize: bool = False,
-                 weight_dtype: torch.dtype = torch.float32) -> None:
+                 weight_dtype: torch.dtype = torch.float32, cache_packed: bool = True) -> None:
         super().__init__()
         if not 1 <= num_experts <= MAX_EXPERTS:
             raise ValueError(f"num_experts must be in [1, {MAX_EXPERTS}], got {num_experts}")
@@ -57,6 +66,7 @@ class MoELayer(nn.Module):
         self.top_k = top_k
         self.renormalize = renormalize
         self.weight_dtype = weight_dtype
+        self.cache_packed = cache_packed
         self.router = nn.Parameter(torch.empty(num_experts, hidden_dim))
         self.gate_proj = nn.ParameterList(
             [nn.Parameter(torch.empty(intermediate_dim, hidden_dim)) for _ in range(num_experts)])
@@ -83,11 +93,19 @@ class MoELayer(nn.Module):
         return tuple((id(p), p.data_ptr(), p._version, p.device) for p in self._params()) + (
             self.weight_dtype,)
 
+    def invalidate_packed(self) -> None:
+        """Drop the cached packed buffer; the next forward repacks.  Needed
+        after writes through ``p.data`` (e.g. ``p.data.copy_(w)``), which do
+        not bump the version counter the cache is keyed on."""
+        self._packed = None
+        self._packed_key = None
+
     def _pack_weights(self) -> torch.Tensor:
         """Packed expert buffer in ``weight_dtype`` (warp_route/__init__.py:63-69),
-        rebuilt only when a parameter changed since the last pack."""
+        rebuilt when a parameter changed since the last pack, after
+        ``invalidate_packed()``, and on every call with cache_packed=False."""
         key = self._cache_key()
-        if self._packed is None or key != self._packed_key:
+        if not self.cache_packed or self._packed is None or key != self._packed_key:
             with torch.no_grad():
                 self._packed = _pack_expert_weights(
                     [p.data for p in self.gate_proj], [p.data for p in self.up_proj],

@@ -28,6 +28,7 @@ WR_EINVAL_WORKSPACE = 7
 WR_EINVAL_BATCH = 8
 WR_EINVAL_KIND = 9
 WR_EINVAL_BLOCK = 10
+WR_ETIMEOUT = 11
 WR_EHIP = 100
 
 WR_F32 = 0
@@ -51,6 +52,10 @@ class WrLayoutInfo(ctypes.Structure):
                 ("down_proj_offset", ctypes.c_int64), ("scale_offset", ctypes.c_int64),
                 ("expert_stride", ctypes.c_int64), ("elem_bytes", ctypes.c_int32),
                 ("weight_dtype", ctypes.c_int32)]
+
+
+class WrFusedOpts(ctypes.Structure):
+    _fields_ = [("spin_limit", ctypes.c_uint32), ("wait_extra", ctypes.c_uint32)]
 
 
 class WrMoeArgs(ctypes.Structure):
@@ -100,6 +105,11 @@ def lib() -> ctypes.CDLL:
             f = getattr(l, name)
             f.argtypes = [ctypes.POINTER(WrMoeArgs), ctypes.c_void_p]
             f.restype = ctypes.c_int
+        l.wr_fused_moe_opts.argtypes = [ctypes.POINTER(WrMoeArgs), ctypes.POINTER(WrFusedOpts),
+                                        ctypes.c_void_p]
+        l.wr_fused_moe_opts.restype = ctypes.c_int
+        l.wr_fused_moe_status.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        l.wr_fused_moe_status.restype = ctypes.c_int
         _lib = l
     return _lib
 

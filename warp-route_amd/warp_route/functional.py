@@ -350,6 +350,20 @@ def batched_fused_moe(
                                         topk_weights)
 
 
+def set_handoff_check(enabled: bool) -> None:
+    """Make ``fused_moe`` check its kernel's hand-off after every call.
+
+    The single-token kernel hands act from its gate/up blocks to its down
+    blocks through arrival counters, with a bounded wait (about 0.2 s).  A
+    wait that expires makes that block write NaN rows and sets a status word.
+    With the check on, ``fused_moe`` reads that word after the call (a
+    stream synchronisation, so not under graph capture) and raises
+    ``RuntimeError`` if it is set.  ``WARP_ROUTE_CHECK_HANDOFF=1`` in the
+    environment turns it on at import.  The reference has no such wait: its
+    fused kernel is a single warp (src/fused_moe.cu:76-227)."""
+    _load_extension().set_handoff_check(bool(enabled))
+
+
 def gate_topk(
     x: torch.Tensor,
     gate_w: torch.Tensor,
