@@ -55,6 +55,10 @@ extern "C" {
 #define WR_MAX_TOPK 6
 /* Expert stride alignment in bytes: src/expert_layout.cuh:43-45. */
 #define WR_EXPERT_ALIGN 128
+/* Bytes of device scratch wr_fused_moe_noalloc holds per GPU (1 MiB): enough
+ * for wr_workspace_bytes(WR_KIND_FUSED, ...) up to k * roundup(I, 16) =
+ * 253,440 (Mixtral needs 28,672, DBRX 43,008, DeepSeek 8,448). */
+#define WR_NOALLOC_SCRATCH_BYTES (1u << 20)
 
 typedef enum wr_status {
   WR_OK = 0,
@@ -70,6 +74,9 @@ typedef enum wr_status {
   WR_EINVAL_BLOCK = 10,       /* MXFP4 weights need h and I multiples of 32    */
   WR_ETIMEOUT = 11,           /* a single-token hand-off wait expired: the rows
                                  of the blocks that gave up are NaN            */
+  WR_EINVAL_SCRATCH = 12,     /* the problem needs more workspace than the
+                                 allocation-free entry point's fixed scratch
+                                 (WR_NOALLOC_SCRATCH_BYTES)                   */
   WR_EHIP = 100               /* a HIP runtime call failed                     */
 } wr_status;
 
@@ -237,6 +244,23 @@ WR_API int wr_fused_moe_status(const void *workspace, size_t workspace_bytes, vo
  * router inside its one kernel). */
 WR_API int wr_fused_moe_route(const wr_moe_args *args, void *stream);
 WR_API int wr_fused_moe_ffn(const wr_moe_args *args, void *stream);
+
+/* wr_fused_moe without a caller workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * args->workspace and args->workspace_bytes are ignored: the call uses a
+ * fixed WR_NOALLOC_SCRATCH_BYTES device array of the library, one per GPU,
+ * held until the process ends.  It allocates nothing (no hipMalloc, no
+ * hipFree, no allocating library call); the first call on a GPU looks up
+ * that GPU's array address once.  Returns WR_EINVAL_SCRATCH (before any HIP
+ * call) when wr_workspace_bytes(WR_KIND_FUSED, E, h, I, k, 1) exceeds
+ * WR_NOALLOC_SCRATCH_BYTES.  Every call on one GPU shares its array, and the
+ * array keeps the last call's contents (each call's router launch clears the
+ * control words it needs), so calls that overlap on one GPU -- on different
+ * streams, or from different threads -- race and must be serialised by the
+ * caller.  Otherwise identical to wr_fused_moe, with the same kernels and
+ * results. */
+WR_API int wr_fused_moe_noalloc(const wr_moe_args *args, void *stream);
 
 /* B-token fused MoE (batch_size >= 0; 0 is a no-op as in
  * src/fused_moe_batched.cu:201).  Tokens that share an expert share its weight

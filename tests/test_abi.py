@@ -25,7 +25,7 @@ def test_header_declares_the_expected_entry_points():
         "wr_status_str", "wr_layout", "wr_total_weight_bytes", "wr_layout_dtype",
         "wr_weight_bytes", "wr_workspace_bytes", "wr_gate_topk", "wr_fused_moe",
         "wr_fused_moe_route", "wr_fused_moe_ffn", "wr_batched_fused_moe", "wr_naive_moe",
-        "wr_fused_moe_opts", "wr_fused_moe_status"])
+        "wr_fused_moe_opts", "wr_fused_moe_status", "wr_fused_moe_noalloc"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -43,7 +43,7 @@ def test_header_constants_match_binding():
                  "WR_EINVAL_EXPERTS", "WR_EINVAL_DTYPE", "WR_EINVAL_WEIGHT_SIZE",
                  "WR_EINVAL_WORKSPACE", "WR_EINVAL_BATCH", "WR_EINVAL_KIND", "WR_EHIP",
                  "WR_F32", "WR_F16", "WR_BF16", "WR_FP8_E4M3", "WR_MXFP4", "WR_EINVAL_BLOCK",
-                 "WR_ETIMEOUT",
+                 "WR_ETIMEOUT", "WR_EINVAL_SCRATCH",
                  "WR_KIND_FUSED",
                  "WR_KIND_BATCHED", "WR_KIND_NAIVE"):
         m = re.search(rf"\b{name} = (\d+)", text)
@@ -162,7 +162,7 @@ def test_workspace_bytes():
 
 
 def test_status_strings():
-    for s in range(0, 13):
+    for s in range(0, 14):
         assert capi.status_str(s)
     assert capi.status_str(capi.WR_EHIP) == "HIP runtime error"
 
@@ -230,6 +230,33 @@ def test_fused_opts_entry_point_validates_like_wr_fused_moe():
         assert capi.lib().wr_fused_moe_opts(ctypes.byref(a), None, None) == want
     a = valid_args(B=2)
     assert capi.lib().wr_fused_moe_opts(ctypes.byref(a), None, None) == capi.WR_EINVAL_BATCH
+
+
+def test_noalloc_validates_before_hip():
+    """wr_fused_moe_noalloc ignores the workspace fields, runs the other
+    checks of wr_fused_moe, and rejects a problem whose workspace exceeds its
+    fixed scratch before any HIP call."""
+    lib = capi.lib()
+    assert lib.wr_fused_moe_noalloc(None, None) == capi.WR_EINVAL_NULL
+    for field, value, want in CASES:
+        if field.startswith("workspace"):
+            continue
+        a = valid_args()
+        setattr(a, field, value)
+        assert lib.wr_fused_moe_noalloc(ctypes.byref(a), None) == want, field
+    a = valid_args()
+    a.intermediate_dim, a.top_k = 65536, 2
+    a.weight_bytes = 1 << 40
+    assert (lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 64, 65536, 2, 1)
+            <= capi.WR_NOALLOC_SCRATCH_BYTES)
+    a.top_k = 6
+    assert lib.wr_fused_moe_noalloc(ctypes.byref(a), None) == capi.WR_EINVAL_SCRATCH
+    a = valid_args(B=2)
+    assert lib.wr_fused_moe_noalloc(ctypes.byref(a), None) == capi.WR_EINVAL_BATCH
+    text = open(HEADER).read()
+    import re
+    m = re.search(r"#define WR_NOALLOC_SCRATCH_BYTES \(1u << (\d+)\)", text)
+    assert m and (1 << int(m.group(1))) == capi.WR_NOALLOC_SCRATCH_BYTES
 
 
 def test_fused_status_checks_its_workspace_before_hip():

@@ -57,7 +57,8 @@ def kernels(tmp_path_factory):
         # Each kernel is one item of the amdhsa.kernels list, its keys in
         # alphabetical order (.group_segment_fixed_size comes before .name).
         m = re.search(r"^(\s*)amdhsa\.kernels:\s*$", notes, re.M)
-        assert m, "no amdhsa.kernels in the code object notes"
+        if not m:  # a translation unit with device variables but no kernels
+            continue
         item = re.compile(rf"^{m.group(1)}  - \.")
         rec = None
         for line in notes[m.end():].splitlines():

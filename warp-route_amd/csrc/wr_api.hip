@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <mutex>
 
 #include "warp_route.h"
 #include "wr_internal.h"
@@ -165,6 +166,33 @@ int validate(const wr_moe_args* a, int kind, Problem* p) {
 
 int hip_status(hipError_t e) { return e == hipSuccess ? WR_OK : WR_EHIP; }
 
+// The allocation-free entry point's workspace: one array per GPU (a
+// __device__ variable exists once on every device the code object is loaded
+// on), held until the process ends.  In host code `scratch` names a host-side
+// stand-in, not device memory: its device address on the current GPU comes
+// from hipGetSymbolAddress, looked up once per device and kept in
+// g_scratch_ptr.
+static __device__ __align__(256) unsigned char scratch[WR_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// Device address of the current GPU's scratch array, or nullptr on a HIP
+// error.  The first call on a device, with that device current, looks it up.
+void* scratch_ptr() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr)
+      return nullptr;
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -187,6 +215,8 @@ WR_API const char* wr_status_str(int status) {
       return "MXFP4 weights need hidden_dim and intermediate_dim to be multiples of 32";
     case WR_ETIMEOUT:
       return "a fused-kernel hand-off wait expired (the affected output rows are NaN)";
+    case WR_EINVAL_SCRATCH:
+      return "problem needs more workspace than the allocation-free entry point's 1 MiB scratch";
     case WR_EHIP: return "HIP runtime error";
     default: return "unknown status";
   }
@@ -260,6 +290,24 @@ WR_API int wr_fused_moe_opts(const wr_moe_args* args, const wr_fused_opts* opts,
     if (opts->spin_limit != 0) p.spin_limit = opts->spin_limit;
     p.wait_extra = opts->wait_extra;
   }
+  return hip_status(wr::launch_fused(p, static_cast<hipStream_t>(stream)));
+}
+
+WR_API int wr_fused_moe_noalloc(const wr_moe_args* args, void* stream) {
+  if (args == nullptr) return WR_EINVAL_NULL;
+  // Validate against the fixed scratch size first (no HIP call yet): any
+  // workspace complaint is then the problem being too large for it.
+  wr_moe_args a = *args;
+  a.workspace = reinterpret_cast<void*>(uintptr_t{256});  // placeholder, never used
+  a.workspace_bytes = WR_NOALLOC_SCRATCH_BYTES;
+  Problem p{};
+  const int st = validate(&a, WR_KIND_FUSED, &p);
+  if (st == WR_EINVAL_WORKSPACE) return WR_EINVAL_SCRATCH;
+  if (st != WR_OK) return st;
+  void* ws = scratch_ptr();
+  if (ws == nullptr) return WR_EHIP;
+  p.ws = static_cast<char*>(ws);
+  p.ws_bytes = WR_NOALLOC_SCRATCH_BYTES;
   return hip_status(wr::launch_fused(p, static_cast<hipStream_t>(stream)));
 }
 

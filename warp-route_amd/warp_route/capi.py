@@ -29,6 +29,8 @@ WR_EINVAL_BATCH = 8
 WR_EINVAL_KIND = 9
 WR_EINVAL_BLOCK = 10
 WR_ETIMEOUT = 11
+WR_EINVAL_SCRATCH = 12
+WR_NOALLOC_SCRATCH_BYTES = 1 << 20
 WR_EHIP = 100
 
 WR_F32 = 0
@@ -101,7 +103,7 @@ def lib() -> ctypes.CDLL:
         l.wr_workspace_bytes.argtypes = [ctypes.c_int] * 6
         l.wr_workspace_bytes.restype = ctypes.c_size_t
         for name in ("wr_gate_topk", "wr_fused_moe", "wr_fused_moe_route", "wr_fused_moe_ffn",
-                     "wr_batched_fused_moe", "wr_naive_moe"):
+                     "wr_batched_fused_moe", "wr_naive_moe", "wr_fused_moe_noalloc"):
             f = getattr(l, name)
             f.argtypes = [ctypes.POINTER(WrMoeArgs), ctypes.c_void_p]
             f.restype = ctypes.c_int
