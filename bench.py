@@ -54,14 +54,14 @@ METRIC = ("µs per MoE layer at batch=1 (Mixtral shape); "
 
 
 WLABEL = {"fp16": "f16", "bf16": "bf16", "fp8": "fp8 e4m3 (per-row fp32 scales)",
-          "mxfp4": "mxfp4 (e2m1, e8m0 scale per 32)"}
+          "mxfp4": "mxfp4 (e2m1, e8m0 scale per 32)", "fp32": "f32"}
 
 
 def weight_dtype(name: str):
     """torch dtype of a --weights choice."""
     import torch
     return {"fp16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn,
-            "mxfp4": torch.float4_e2m1fn_x2}[name]
+            "mxfp4": torch.float4_e2m1fn_x2, "fp32": torch.float32}[name]
 
 
 def log(msg: str) -> None:
@@ -296,14 +296,21 @@ def probe_lib():
     return lib
 
 
-# (blocks per CU, loads in flight per lane) tried by read_ceiling
-PROBE_SHAPES = [(2, 4), (4, 4), (8, 4), (4, 8), (8, 2), (16, 2)]
+# (blocks per CU, loads in flight per lane) tried by read_ceiling: the best
+# shapes of a wider sweep (1-8 blocks of 4 waves per CU, 1-8 loads in
+# flight) on the Mixtral and DeepSeek selected experts.  24-32 KB in flight
+# per CU streams fastest; 64 KB or more per CU is 10-20% slower.
+PROBE_SHAPES = [(6, 1), (8, 1), (3, 2), (4, 2), (2, 4), (1, 8)]
+# --probe-sweep: the wider sweep those came from
+PROBE_SWEEP = [(1, 1), (1, 2), (1, 4), (1, 8), (2, 1), (2, 2), (2, 4), (2, 8), (3, 2), (3, 4),
+               (4, 1), (4, 2), (4, 4), (6, 1), (8, 1)]
 
 
-def read_ceiling(range_sets, steps: int, warmup: int = 5) -> dict:
+def read_ceiling(range_sets, steps: int, warmup: int = 5, shapes=None) -> dict:
     """Best rate of the read-only streaming probe over range_sets (one list
     of (ptr, bytes) per rotated layer, read in one launch per call, rotating),
-    over PROBE_SHAPES: the achievable HBM read bandwidth for these bytes."""
+    over `shapes` (default PROBE_SHAPES): the achievable HBM read bandwidth
+    for these bytes."""
     import ctypes
     import torch
     lib = probe_lib()
@@ -315,7 +322,7 @@ def read_ceiling(range_sets, steps: int, warmup: int = 5) -> dict:
         nb = (ctypes.c_int64 * len(rs))(*[n for _, n in rs])
         calls.append((ptrs, nb, len(rs), sum(n for _, n in rs)))
     results = []
-    for bpc, unroll in PROBE_SHAPES:
+    for bpc, unroll in (shapes or PROBE_SHAPES):
         def step(i):
             ptrs, nb, n, _ = calls[i % len(calls)]
             if lib.wr_probe_read(ptrs, nb, n, bpc, unroll, ctypes.c_void_p(sink.data_ptr()),
@@ -357,9 +364,11 @@ def read_probe_bench(args) -> int:
     dev = torch.device("cuda:0")
     layers = [make_config_layer(cfg, seed=s, device=dev, gen_device=dev)
               for s in range(args.layers)]
-    sel = read_ceiling(selected_ranges(layers, cfg), args.steps)
+    shapes = PROBE_SWEEP if args.probe_sweep else None
+    sel = read_ceiling(selected_ranges(layers, cfg), args.steps, shapes=shapes)
     flat = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    big = read_ceiling([[(flat.data_ptr(), flat.numel())]], max(20, args.steps // 10))
+    big = read_ceiling([[(flat.data_ptr(), flat.numel())]], max(20, args.steps // 10),
+                       shapes=shapes)
     print(json.dumps({
         "metric": "read-only HBM streaming ceiling (GB/s)", "value": sel["GBps"],
         "unit": "GB/s", "higher_is_better": True, "n_gpus": 1, "steps": args.steps,
@@ -442,13 +451,15 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--config", default="mixtral", choices=["mixtral", "deepseek", "dbrx"])
-    ap.add_argument("--weights", default="fp16", choices=["fp16", "bf16", "fp8", "mxfp4"],
+    ap.add_argument("--weights", default="fp16", choices=["fp16", "bf16", "fp8", "mxfp4", "fp32"],
                     help="expert weight format (the headline is fp16)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true")
     ap.add_argument("--read-probe", action="store_true",
                     help="time the read-only streaming ceiling over the selected experts")
+    ap.add_argument("--probe-sweep", action="store_true",
+                    help="with --read-probe: sweep PROBE_SWEEP instead of PROBE_SHAPES")
     ap.add_argument("--op", default="fused", choices=["fused", "naive"],
                     help="naive: time the naive multi-kernel op (with fused beside it)")
     ap.add_argument("--no-ceiling", action="store_true",

@@ -82,6 +82,26 @@ def test_full_size_batched_clustered_every_row(cuda, mixtral_layer, B):
     check_rows(out, ids, ws, x, gw, buf, E, h, I, k, True, f"mixtral B={B}")
 
 
+@pytest.mark.parametrize("B", [4, 24, 64])
+def test_full_size_batched_fp32_weights_every_row(cuda, B):
+    """fp32 weights (the reference's only format) at Mixtral shape through the
+    grouped path (exact fp32 MFMA products), tokens clustered on one pair:
+    every row against the oracle and the single-token op.  Each selected
+    expert's weights stream once per call, not once per token."""
+    cfg = CONFIGS["mixtral"].with_weights(F32)
+    E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+    _, gw, buf = make_config_layer(cfg, seed=0, device=cuda, gen_device=cuda)
+    x = clustered_batch(gw, B, pair=(3, 5), alpha=4.0, seed=2, device=cuda)
+    print(f"[gpu] full batched mixtral fp32 weights B={B}, every row", flush=True)
+    ids = torch.empty(B, k, dtype=torch.int32, device=cuda)
+    ws = torch.empty(B, k, dtype=torch.float32, device=cuda)
+    out = F.batched_fused_moe(x, gw, buf, E, h, I, k, True, ids, ws)
+    torch.cuda.synchronize()
+    check_rows(out, ids, ws, x, gw, buf, E, h, I, k, True, f"mixtral fp32 B={B}")
+    del buf
+    torch.cuda.empty_cache()
+
+
 @pytest.fixture(scope="module")
 def mixtral_stack(cuda):
     """Four independent full-size Mixtral layers (11.3 GB of fp16 experts)."""
@@ -174,7 +194,7 @@ RANGE = [("x1e5", 1e5, 1e-5, 0.05, F32), ("x1e-6", 1e-6, 1e6, 0.05, F32),
          ("std2e-4", 1.0, 1.0, 2e-4, F32), ("xf16-4096", 4096.0, 1.0 / 4096.0, 2e-4, F16)]
 
 
-@pytest.mark.parametrize("wd", [F16, FP8, BF16, MX4], ids=["f16", "fp8", "bf16", "mxfp4"])
+@pytest.mark.parametrize("wd", [F16, FP8, BF16, MX4, F32], ids=["f16", "fp8", "bf16", "mxfp4", "f32"])
 @pytest.mark.parametrize("B", [5, 40])
 @pytest.mark.parametrize("case", RANGE, ids=[c[0] for c in RANGE])
 def test_grouped_batched_range(cuda, case, B, wd):

@@ -284,15 +284,16 @@ GROUPED = [(8, 256, 512, 2, False), (16, 512, 1024, 2, True), (64, 256, 512, 6, 
            (8, 384, 640, 1, True)]
 
 
-@pytest.mark.parametrize("wd", [F16, FP8, BF16, MX4], ids=["f16", "fp8", "bf16", "mxfp4"])
+@pytest.mark.parametrize("wd", [F16, FP8, BF16, MX4, F32], ids=["f16", "fp8", "bf16", "mxfp4", "f32"])
 @pytest.mark.parametrize("x_dtype", [F32, F16], ids=["xf32", "xf16"])
 @pytest.mark.parametrize("B", [2, 5, 24, 33, 80])  # token tiles of 16, 16, 32, 64, 64
 @pytest.mark.parametrize("cfg", GROUPED,
                          ids=lambda c: f"E{c[0]}-h{c[1]}-I{c[2]}-k{c[3]}" + ("-renorm" if c[4] else ""))
 def test_grouped_batched_parity(cuda, cfg, B, x_dtype, wd):
     """The grouped MFMA batched path (fp16, fp8, bf16 or MXFP4 weights, h and
-    I multiples of 128; fp8 codes are staged as fp16 and scaled in the
-    epilogue, MXFP4 codes staged as bf16 times their block scale;
+    I multiples of 128; fp32 weights with exact fp32 MFMA products; fp8 codes
+    are staged as fp16 and scaled in the epilogue, MXFP4 codes staged as bf16
+    times their block scale;
     bf16 and MXFP4 weights take x and act as two bf16 terms, within 2^-18 of
     them, so their rows are compared with the single-token op at 5e-5 of
     max|out| instead of 1e-5).

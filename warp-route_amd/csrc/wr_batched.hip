@@ -874,6 +874,310 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, B
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp32 weights (the reference's only format): v_mfma_f32_16x16x4f32, exact
+// fp32 products accumulated in fp32, so x and act need no splitting and no
+// scaling.  A K step is 64 columns (256 bytes of a row, as the 16-bit types'
+// 128), so the weight loads, tile shapes and LDS footprint match the fp16
+// kernels: a wave loads its rows 4 x 256 bytes per instruction into a padded
+// tile of 16-byte pieces.  MFMA t = 4 s + m of a K step takes, in lane l
+// (quadrant q = l / 16), column 4 (4 s + q) + m for A (weight row l % 16) and
+// B (token l % 16) alike: a permutation of the step's 64 columns, the same
+// for both operands, so every product is still summed exactly once, and each
+// lane's operands for four MFMAs are one 16-byte LDS read.
+// ---------------------------------------------------------------------------
+constexpr int kBKF = 64;           // K step, fp32 columns
+constexpr int kPF = kBKF / 4;      // 16-byte pieces per row of a step
+constexpr int kRowF = kPF + 1;     // padded row (bank spread)
+
+template <int ROWS>
+struct TileF {
+  f32x4 v[ROWS][kRowF];
+};
+
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// One thread's pieces of a TOK-token tile (TOK * kPF / kBlk of them): token
+// n = i / kPF, piece c = i % kPF; off = the token row's element offset plus
+// 4 c, or -1 for a padding token.
+template <int TOK>
+constexpr int f32_tile_pieces() {
+  static_assert(TOK * kPF % kBlk == 0, "whole pieces per thread");
+  return TOK * kPF / kBlk;
+}
+template <int TP>
+__device__ __forceinline__ void f32_tile_rows(int64_t (&off)[TP], const int32_t* rows,
+                                              int direct0, int mt, int ld) {
+#pragma unroll
+  for (int q = 0; q < TP; ++q) {
+    const int i = threadIdx.x + kBlk * q;
+    const int n = i / kPF, c = i % kPF;
+    const int row = rows != nullptr ? (n < mt ? rows[n] : 0) : direct0 + n;
+    off[q] = n < mt ? (int64_t)row * ld + c * 4 : -1;
+  }
+}
+template <typename XT, int TP>
+__device__ __forceinline__ void f32_tile_load(f32x4 (&t)[TP], const XT* __restrict__ src,
+                                              const int64_t (&off)[TP], int kb) {
+#pragma unroll
+  for (int q = 0; q < TP; ++q) {
+    t[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (off[q] >= 0) {
+      float v[4];
+      load_x<XT, 4>(src + off[q] + kb, v);
+      t[q] = f32x4{v[0], v[1], v[2], v[3]};
+    }
+  }
+}
+template <int TOK, int TP>
+__device__ __forceinline__ void f32_tile_store(TileF<TOK>& xs, const f32x4 (&t)[TP]) {
+#pragma unroll
+  for (int q = 0; q < TP; ++q) {
+    const int i = threadIdx.x + kBlk * q;
+    xs.v[i / kPF][i % kPF] = t[q];
+  }
+}
+
+// A wave's weight rows: ROWS / 4 loads per K step, lane l: row 4 i + l / 16,
+// columns 4 (l % 16) .. + 4 of the step.
+template <int ROWS>
+struct WRegsF {
+  static constexpr int N = ROWS / 4;
+  f32x4 v[N];
+};
+template <int ROWS>
+__device__ __forceinline__ void f32_w_load(WRegsF<ROWS>& r, const float* const (&base)[ROWS / 4],
+                                           int kb) {
+#pragma unroll
+  for (int i = 0; i < ROWS / 4; ++i)
+    r.v[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(base[i] + kb));
+}
+template <int ROWS>
+__device__ __forceinline__ void f32_w_store(TileF<ROWS>& t, const WRegsF<ROWS>& r, int lane) {
+#pragma unroll
+  for (int i = 0; i < ROWS / 4; ++i) t.v[4 * i + lane / 16][lane % 16] = r.v[i];
+}
+
+// Gate/up pass over up to TOK tokens (NT tiles of 16) of one expert, rows
+// row0 .. + 16 of its gate and up matrices (tile rows 0-15 and 16-31).
+template <typename XT, int NT, int TOK>
+__device__ __forceinline__ void gu_pass_f32(TileF<TOK>& xs, TileF<32>& wt,
+                                            const float* const (&wbase)[8],
+                                            const XT* __restrict__ x, const BatchRoute& r,
+                                            int p0, int mt, float* __restrict__ act, int row0,
+                                            const Geom& g, int lane) {
+  f32x4 ag[NT], au[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) ag[n] = au[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr int TP = f32_tile_pieces<TOK>();
+  int64_t off[TP];
+  f32_tile_rows(off, r.pair_tok + p0, 0, mt, g.h);
+  const int ns = g.h / kBKF;
+  const int q = lane >> 4, rl = lane & 15;
+  WRegsF<32> wr;
+  f32x4 tv[TP];
+  f32_w_load<32>(wr, wbase, 0);
+  f32_tile_load(tv, x, off, 0);
+  for (int s = 0; s < ns; ++s) {
+    __syncthreads();  // every wave is done reading the previous tiles
+    f32_tile_store(xs, tv);
+    f32_w_store<32>(wt, wr, lane);
+    __syncthreads();
+    if (s + 1 < ns) {
+      f32_w_load<32>(wr, wbase, (s + 1) * kBKF);
+      f32_tile_load(tv, x, off, (s + 1) * kBKF);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 ga = wt.v[rl][4 * j + q];
+      const f32x4 ua = wt.v[16 + rl][4 * j + q];
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        const f32x4 b = xs.v[n * 16 + rl][4 * j + q];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          ag[n] = mfma_f32(ga[m], b[m], ag[n]);
+          au[n] = mfma_f32(ua[m], b[m], au[n]);
+        }
+      }
+    }
+  }
+  // D layout: lane holds token n*16 + (lane % 16), rows 4 (lane / 16) .. +4.
+  const int rq = row0 + q * 4;
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int tn = n * 16 + rl;
+    if (tn < mt) {
+      const int p = p0 + tn;
+      const float w = r.pair_w[p];
+      f32x4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = w * (silu(ag[n][i]) * au[n][i]);
+      *reinterpret_cast<f32x4*>(act + (int64_t)p * g.I + rq) = v;
+    }
+  }
+}
+
+// grid (I / 64, expert slots); as k_gu_mfma, with x read as it is (fp32 or
+// fp16) and no scaling.
+template <typename XT, int TOK, bool ROUTE>
+__global__ __launch_bounds__(kBlk) void k_gu_f32(const float* __restrict__ wbuf,
+                                                 const XT* __restrict__ x, BatchRoute r,
+                                                 float* __restrict__ act, Geom g,
+                                                 const float* __restrict__ logits,
+                                                 int32_t* __restrict__ ids_out,
+                                                 float* __restrict__ w_out) {
+  __shared__ TileF<TOK> xs;
+  __shared__ TileF<32> wts[kBlk / kWave];
+  __shared__ GuRouteLds<ROUTE> rl;
+  const int slot = blockIdx.y;
+  int e, pbeg, M;
+  if constexpr (ROUTE) {
+    route_small(rl.sr, logits, g.B, g.E, g.k, g.renorm);
+    if (blockIdx.x == 0 && blockIdx.y == 0)
+      route_small_publish(rl.sr, g.B, g.E, g.k, r, ids_out, w_out);
+    if (slot >= rl.sr.na) return;  // block-uniform
+    e = rl.sr.active[slot];
+    pbeg = rl.sr.off[e];
+    M = rl.sr.off[e + 1] - pbeg;
+    r.pair_tok = rl.sr.pair_tok;
+    r.pair_w = rl.sr.pair_w;
+  } else {
+    (void)logits;
+    (void)ids_out;
+    (void)w_out;
+    if (slot >= *r.n_active) return;  // block-uniform
+    e = r.active[slot];
+    pbeg = r.off[e];
+    M = r.off[e + 1] - pbeg;
+  }
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int row0 = blockIdx.x * kBM + wave * 16;
+  const float* blk = wbuf + (int64_t)e * g.stride;
+  const float* G = blk + (int64_t)(row0 + lane / 16) * g.h + 4 * (lane % 16);
+  const float* wbase[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) wbase[i] = G + (i < 4 ? 0 : g.off_up) + (int64_t)(4 * (i % 4)) * g.h;
+  TileF<32>& wt = wts[wave];
+  for (int m0 = 0; m0 < M; m0 += TOK) {
+    const int mt = min(TOK, M - m0);
+    const int p0 = pbeg + m0;
+    if constexpr (TOK == 16) {
+      gu_pass_f32<XT, 1, TOK>(xs, wt, wbase, x, r, p0, mt, act, row0, g, lane);
+    } else if constexpr (TOK == 32) {
+      if (mt <= 16)
+        gu_pass_f32<XT, 1, TOK>(xs, wt, wbase, x, r, p0, mt, act, row0, g, lane);
+      else
+        gu_pass_f32<XT, 2, TOK>(xs, wt, wbase, x, r, p0, mt, act, row0, g, lane);
+    } else {
+      switch ((mt + 15) / 16) {
+        case 1: gu_pass_f32<XT, 1, TOK>(xs, wt, wbase, x, r, p0, mt, act, row0, g, lane); break;
+        case 2: gu_pass_f32<XT, 2, TOK>(xs, wt, wbase, x, r, p0, mt, act, row0, g, lane); break;
+        case 3: gu_pass_f32<XT, 3, TOK>(xs, wt, wbase, x, r, p0, mt, act, row0, g, lane); break;
+        default: gu_pass_f32<XT, 4, TOK>(xs, wt, wbase, x, r, p0, mt, act, row0, g, lane); break;
+      }
+    }
+  }
+}
+
+// Down pass: K steps [sb, se) of 64 columns, rows row0 .. + 16 of the down
+// matrix against the pass's act rows (fp32, as written by the gate/up pass).
+template <int NT, int TOK>
+__device__ __forceinline__ void dn_pass_f32(TileF<TOK>& xs, TileF<16>& wt,
+                                            const float* const (&wbase)[4],
+                                            const float* __restrict__ act, int p0, int mt,
+                                            int sb, int se, float* __restrict__ y, int row0,
+                                            const Geom& g, int lane) {
+  f32x4 acc[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int q = lane >> 4, rl = lane & 15;
+  if (sb < se) {
+    constexpr int TP = f32_tile_pieces<TOK>();
+    int64_t off[TP];
+    f32_tile_rows(off, nullptr, p0, mt, g.I);
+    WRegsF<16> wr;
+    f32x4 tv[TP];
+    f32_w_load<16>(wr, wbase, sb * kBKF);
+    f32_tile_load(tv, act, off, sb * kBKF);
+    for (int s = sb; s < se; ++s) {
+      __syncthreads();
+      f32_tile_store(xs, tv);
+      f32_w_store<16>(wt, wr, lane);
+      __syncthreads();
+      if (s + 1 < se) {
+        f32_w_load<16>(wr, wbase, (s + 1) * kBKF);
+        f32_tile_load(tv, act, off, (s + 1) * kBKF);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 da = wt.v[rl][4 * j + q];
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+          const f32x4 b = xs.v[n * 16 + rl][4 * j + q];
+#pragma unroll
+          for (int m = 0; m < 4; ++m) acc[n] = mfma_f32(da[m], b[m], acc[n]);
+        }
+      }
+    }
+  }
+  const int rq = row0 + q * 4;
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int tn = n * 16 + rl;
+    if (tn < mt) *reinterpret_cast<f32x4*>(y + (int64_t)(p0 + tn) * g.h + rq) = acc[n];
+  }
+}
+
+// grid (h / 64, kKSplit, expert slots); K slice ks covers steps
+// [nsteps ks / kKSplit, nsteps (ks + 1) / kKSplit) of I / 64.
+template <int TOK>
+__global__ __launch_bounds__(kBlk) void k_dn_f32(const float* __restrict__ wbuf, BatchRoute r,
+                                                 const float* __restrict__ act,
+                                                 float* __restrict__ ypart, Geom g, int P) {
+  __shared__ TileF<TOK> xs;
+  __shared__ TileF<16> wts[kBlk / kWave];
+  const int slot = blockIdx.z;
+  if (slot >= *r.n_active) return;
+  const int e = r.active[slot];
+  const int pbeg = r.off[e], M = r.off[e + 1] - pbeg;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int row0 = blockIdx.x * kBM + wave * 16;
+  const int ks = blockIdx.y;
+  const int nsteps = g.I / kBKF;
+  const int sb = nsteps * ks / BatchWs::kKSplit;
+  const int se = nsteps * (ks + 1) / BatchWs::kKSplit;
+  const float* D = wbuf + (int64_t)e * g.stride + g.off_down +
+                   (int64_t)(row0 + lane / 16) * g.I + 4 * (lane % 16);
+  const float* wbase[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wbase[i] = D + (int64_t)(4 * i) * g.I;
+  float* y = ypart + (int64_t)ks * P * g.h;
+  TileF<16>& wt = wts[wave];
+  for (int m0 = 0; m0 < M; m0 += TOK) {
+    const int mt = min(TOK, M - m0);
+    if constexpr (TOK == 16) {
+      dn_pass_f32<1, TOK>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane);
+    } else if constexpr (TOK == 32) {
+      if (mt <= 16)
+        dn_pass_f32<1, TOK>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane);
+      else
+        dn_pass_f32<2, TOK>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane);
+    } else {
+      switch ((mt + 15) / 16) {
+        case 1: dn_pass_f32<1, TOK>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
+        case 2: dn_pass_f32<2, TOK>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
+        case 3: dn_pass_f32<3, TOK>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
+        default: dn_pass_f32<4, TOK>(xs, wt, wbase, act, pbeg + m0, mt, sb, se, y, row0, g, lane); break;
+      }
+    }
+  }
+}
+
 // out[t][row]: grid (ceil(h / 256), B); K = k, so that every loop is exact.
 // Every pair index, then every partial, is loaded before the first add (two
 // round trips instead of 2 K); the adds keep their order (experts in
@@ -971,16 +1275,77 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
   }
 }
 
+template <typename XT>
+hipError_t grouped_f32(const Problem& p, const BatchWs& w, hipStream_t s) {
+  Geom g;
+  g.E = p.E;
+  g.h = p.h;
+  g.I = p.I;
+  g.k = p.k;
+  g.renorm = p.renorm;
+  g.B = p.B;
+  g.stride = p.stride_b / 4;
+  g.off_up = p.off_up_b / 4;
+  g.off_down = p.off_down_b / 4;
+  g.off_scale = -1;
+  const int P = p.B * p.k;
+  const int slots = std::min(p.E, P);
+  const float* wb = static_cast<const float*>(p.wbuf);
+  const XT* x = static_cast<const XT*>(p.x);
+  hipError_t err = hipSuccess;
+  if (p.B > WR_SMALL_TILE_MAX_B) {
+    hipLaunchKernelGGL(k_route, dim3(1), dim3(1024), 0, s, w.logits, p.B, p.E, p.k, p.renorm,
+                       p.topk_ids, p.topk_w, w.route);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
+  if (p.B <= WR_SMALL_TILE_MAX_B) {
+    hipLaunchKernelGGL((k_gu_f32<XT, 16, true>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s, wb, x,
+                       w.route, w.act, g, w.logits, p.topk_ids, p.topk_w);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    hipLaunchKernelGGL((k_dn_f32<16>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s,
+                       wb, w.route, w.act, w.ypart, g, P);
+  } else if (p.B <= WR_MID_TILE_MAX_B) {
+    hipLaunchKernelGGL((k_gu_f32<XT, 32, false>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s, wb, x,
+                       w.route, w.act, g, nullptr, nullptr, nullptr);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    hipLaunchKernelGGL((k_dn_f32<32>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s,
+                       wb, w.route, w.act, w.ypart, g, P);
+  } else {
+    hipLaunchKernelGGL((k_gu_f32<XT, kMaxTok, false>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s,
+                       wb, x, w.route, w.act, g, nullptr, nullptr, nullptr);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    hipLaunchKernelGGL((k_dn_f32<kMaxTok>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk),
+                       0, s, wb, w.route, w.act, w.ypart, g, P);
+  }
+  if ((err = hipGetLastError()) != hipSuccess) return err;
+  switch (p.k) {
+    case 1: return launch_combine<XT, 1>(w, p, s);
+    case 2: return launch_combine<XT, 2>(w, p, s);
+    case 3: return launch_combine<XT, 3>(w, p, s);
+    case 4: return launch_combine<XT, 4>(w, p, s);
+    case 5: return launch_combine<XT, 5>(w, p, s);
+    default: return launch_combine<XT, 6>(w, p, s);
+  }
+}
+
 }  // namespace
 
 bool grouped_ok(const Problem& p) {
+  if (p.B <= 1) return false;
+  if (p.wdt == WR_F32)  // 64-column K steps, 16-byte rows
+    return p.vec == 4 && p.h % kBKF == 0 && p.I % kBKF == 0;
   const bool wt = ((p.wdt == WR_F16 || p.wdt == WR_BF16) && p.vec == 8) ||
                   (p.wdt == WR_FP8_E4M3 && p.vec == 16) || (p.wdt == WR_MXFP4 && p.vec == 32);
-  return p.B > 1 && wt && p.h % kBK == 0 && p.I % kBK == 0;
+  return wt && p.h % kBK == 0 && p.I % kBK == 0;
 }
 
 hipError_t launch_grouped(const Problem& p, hipStream_t s) {
   const BatchWs w = BatchWs::carve(p.ws, p.E, p.h, p.I, p.k, p.B);
+  if (p.wdt == WR_F32) {  // exact fp32 products: x as it is, logits only
+    hipError_t err = launch_logits(p, w.logits, s);
+    if (err != hipSuccess) return err;
+    return p.adt == WR_F16 ? grouped_f32<f16>(p, w, s) : grouped_f32<float>(p, w, s);
+  }
   // bf16 operands (bf16 and MXFP4 weights): bf16 terms, no scaling.
   const bool bf = p.wdt == WR_BF16 || p.wdt == WR_MXFP4;
   hipError_t err = launch_logits_split(p, w.logits, w.x_hi, w.x_lo, w.x_exp,
