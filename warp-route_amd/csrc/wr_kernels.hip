@@ -107,6 +107,11 @@
 #ifndef WR_F4_U2
 #define WR_F4_U2 1   // column chunks per down tile
 #endif
+// MXFP4 block scales staged in LDS (x-in-LDS variant) from this intermediate
+// size up; smaller layers keep the per-load scale bytes.
+#ifndef WR_F4_STG_MIN_I
+#define WR_F4_STG_MIN_I 4096
+#endif
 
 namespace wr {
 
@@ -668,8 +673,26 @@ struct XlLayout {
   __host__ __device__ static constexpr size_t bytes(int h) { return (size_t)slots(h) * 16; }
 };
 
+// MXFP4 with its block-scale bytes staged in LDS (STG): the weight loads
+// fetch only the codes, and the scale byte is filled in from the LDS copy
+// before the codes are decoded.
+template <typename WT, int VEC, bool STG>
+__device__ __forceinline__ typename WVec<WT, VEC>::type load_wq_or_codes(const WT* p,
+                                                                        const uint8_t* sc) {
+  if constexpr (STG) {
+    static_assert(std::is_same<WT, fp4x2>::value && VEC == 32, "codes-only loads are MXFP4");
+    (void)sc;
+    typename WVec<WT, VEC>::type v;
+    v.q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    v.e = 127u;
+    return v;
+  } else {
+    return load_wq<WT, VEC>(p, sc);
+  }
+}
+
 // Loads of round c0 of rows [r0, r0 + nrows) of one gate/up item.
-template <typename WT, int VEC, int RPW, int U>
+template <typename WT, int VEC, int RPW, int U, bool STG = false>
 __device__ __forceinline__ void gateup_issue(typename WVec<WT, VEC>::type (&wg)[U][RPW],
                                              typename WVec<WT, VEC>::type (&wu)[U][RPW],
                                              const WT* blk, const WT* G, const WT* Up,
@@ -683,13 +706,29 @@ __device__ __forceinline__ void gateup_issue(typename WVec<WT, VEC>::type (&wg)[
 #pragma unroll
     for (int j = 0; j < RPW; ++j) {
       const bool okj = ok && j < nrows;
-      wg[u][j] = okj ? load_wq<WT, VEC>(G + eoff<WT>((int64_t)j * g.h + c),
-                                        mx_at<WT>(mx_row(blk, g, 0, r0 + j), c))
+      wg[u][j] = okj ? load_wq_or_codes<WT, VEC, STG>(G + eoff<WT>((int64_t)j * g.h + c),
+                                                      STG ? nullptr
+                                                          : mx_at<WT>(mx_row(blk, g, 0, r0 + j), c))
                      : vzero<V>();
-      wu[u][j] = okj ? load_wq<WT, VEC>(Up + eoff<WT>((int64_t)j * g.h + c),
-                                        mx_at<WT>(mx_row(blk, g, 1, r0 + j), c))
+      wu[u][j] = okj ? load_wq_or_codes<WT, VEC, STG>(Up + eoff<WT>((int64_t)j * g.h + c),
+                                                      STG ? nullptr
+                                                          : mx_at<WT>(mx_row(blk, g, 1, r0 + j), c))
                      : vzero<V>();
     }
+  }
+}
+
+// MXFP4 scale staging: n bytes (a multiple of 4, 4-byte aligned at both ends)
+// from global src to LDS dst with direct global-to-LDS dword loads, issued by
+// one wave (its 64-dword runs; the LDS base of each load is wave-uniform).
+__device__ __forceinline__ void stage_bytes_lds(const uint8_t* src, unsigned char* dst, int n,
+                                                int lane) {
+  const int ndw = n / 4;
+  for (int s0 = 0; s0 < ndw; s0 += kWave) {
+    if (s0 + lane < ndw)
+      __builtin_amdgcn_global_load_lds(
+          static_cast<const void*>(src + 4 * (s0 + lane)),
+          (__attribute__((address_space(3))) void*)(dst + 4 * s0), 4, 0, 0);
   }
 }
 
@@ -699,15 +738,14 @@ __device__ __forceinline__ void gateup_issue(typename WVec<WT, VEC>::type (&wg)[
 // global-to-LDS loads (no registers), issued before the first round of
 // weight loads; one wait covers both, so the weights are the only
 // long-lived registers and the copy costs no extra round trip.
-template <typename WT, typename XT, int VEC, int RPW, int U>
+template <typename WT, typename XT, int VEC, int RPW, int U, bool STG>
 __device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
                                                const XT* __restrict__ xb, float* a,
                                                const Geom& g, int eid, float wk, int r0,
-                                               int nrows, int lane) {
+                                               int nrows, int lane, unsigned char* xs_raw) {
   typedef typename WVec<WT, VEC>::type V;
   typedef XlLayout<XT, VEC> L;
   constexpr int CH = kWave * VEC;
-  __shared__ __align__(16) unsigned char xs_raw[L::bytes(xl_max_h<WT>())];
   const WT* blk = wbuf + (int64_t)eid * g.stride;
   const WT* G = blk + eoff<WT>((int64_t)r0 * g.h);
   const WT* Up = G + g.off_up;
@@ -728,8 +766,23 @@ __device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
           0, 0);
     }
   }
+  // STG (MXFP4 with h a multiple of 128): this wave's rows' block-scale
+  // bytes, gate then up, [m][j][h / 32], copied to its own LDS area beside x
+  // with the same kind of loads, so that each code load needs no scale load.
+  const int hb = g.h / 32;
+  unsigned char* scl =
+      STG ? xs_raw + L::bytes(xl_max_h<WT>()) + wave * 2 * RPW * (xl_max_h<WT>() / 32) : xs_raw;
+  if constexpr (STG) {
+    if (nrows > 0) {
+      stage_bytes_lds(mx_row(blk, g, 0, r0), scl, nrows * hb, lane);
+      stage_bytes_lds(mx_row(blk, g, 1, r0), scl + RPW * hb, nrows * hb, lane);
+    }
+  } else {
+    (void)hb;
+    (void)scl;
+  }
   V wg[U][RPW], wu[U][RPW];
-  gateup_issue<WT, VEC, RPW, U>(wg, wu, blk, G, Up, g, r0, nrows, lane * VEC);
+  gateup_issue<WT, VEC, RPW, U, STG>(wg, wu, blk, G, Up, g, r0, nrows, lane * VEC);
   RowScales<WT, RPW> rs;
   load_row_scales<WT, RPW>(rs, blk, g, r0, nrows);
   __builtin_amdgcn_s_waitcnt(0);  // the copy's loads (and the weights) have landed
@@ -739,11 +792,25 @@ __device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
 #pragma unroll
   for (int j = 0; j < RPW; ++j) ag[j] = au[j] = 0.0f;
   for (int c0 = lane * VEC; c0 < g.h; c0 += U * CH) {
-    if (c0 != lane * VEC) gateup_issue<WT, VEC, RPW, U>(wg, wu, blk, G, Up, g, r0, nrows, c0);
+    if (c0 != lane * VEC)
+      gateup_issue<WT, VEC, RPW, U, STG>(wg, wu, blk, G, Up, g, r0, nrows, c0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = c0 + u * CH;
       float xv[VEC];
+      if constexpr (STG) {
+        // Only rows that were loaded: the other rows' vectors are zero codes
+        // with scale 1, and their LDS bytes were never written.
+        if (c < g.h) {
+#pragma unroll
+          for (int j = 0; j < RPW; ++j) {
+            if (j < nrows) {
+              wg[u][j].e = scl[j * hb + c / 32];
+              wu[u][j].e = scl[(RPW + j) * hb + c / 32];
+            }
+          }
+        }
+      }
       if (c < g.h) {
         const unsigned char* xp = xs_raw + (size_t)(c / VEC) * L::kGS * 16;
 #pragma unroll
@@ -784,7 +851,7 @@ __device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
 // Down tile of a fused down block: U column chunks q = q0 + 4 u (chunk q is
 // columns [(q mod nch) * 64 VEC, +64 VEC) of selected expert q / nch), RPD rows
 // from r0.
-template <typename WT, int VEC, int RPD, int U>
+template <typename WT, int VEC, int RPD, int U, bool STG = false>
 __device__ __forceinline__ void down_tile_load(typename WVec<WT, VEC>::type (&wv)[U][RPD],
                                                const WT* __restrict__ wbuf, const Geom& g,
                                                const TopK& t, int r0, int nrows, int q0,
@@ -802,9 +869,32 @@ __device__ __forceinline__ void down_tile_load(typename WVec<WT, VEC>::type (&wv
     const WT* D = blk + g.off_down + eoff<WT>((int64_t)r0 * g.I + c);
 #pragma unroll
     for (int j = 0; j < RPD; ++j)
-      wv[u][j] = (ok && j < nrows) ? load_wq<WT, VEC>(D + eoff<WT>((int64_t)j * g.I),
-                                                      mx_at<WT>(mx_row(blk, g, 2, r0 + j), c))
-                                   : vzero<V>();
+      wv[u][j] = (ok && j < nrows)
+                     ? load_wq_or_codes<WT, VEC, STG>(
+                           D + eoff<WT>((int64_t)j * g.I),
+                           STG ? nullptr : mx_at<WT>(mx_row(blk, g, 2, r0 + j), c))
+                     : vzero<V>();
+  }
+}
+
+// MXFP4 down tile with staged scales: the scale byte of each loaded vector
+// from the block's LDS copy, [kk][j][I / 32] (rows that were not loaded keep
+// the zero vector's scale 1).
+template <typename WT, int VEC, int RPD, int U>
+__device__ __forceinline__ void down_tile_scales(typename WVec<WT, VEC>::type (&wv)[U][RPD],
+                                                 const unsigned char* scl, const Geom& g,
+                                                 int nrows, int q0, int nch, int lane) {
+  const int C = g.k * nch, ib = g.I / 32;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int q = q0 + u * kWavesPerBlock;
+    const int kk = q < C ? q / nch : 0;
+    const int c = (q - kk * nch) * kWave * VEC + lane * VEC;
+    if (q < C && c < g.I) {
+#pragma unroll
+      for (int j = 0; j < RPD; ++j)
+        if (j < nrows) wv[u][j].e = scl[(kk * RPD + j) * ib + c / 32];
+    }
   }
 }
 
@@ -853,7 +943,21 @@ __device__ __forceinline__ void down_tile_fma(float (&acc)[RPD], const V (&wv)[U
   }
 }
 
-template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2, bool XL>
+// MXFP4 block-scale staging in LDS (STG): bytes of the kernel-wide LDS
+// buffer beyond the x copy, per gate/up wave (2 RPW rows of the largest h).
+template <typename WT, int RPW, bool STG>
+constexpr size_t stg_gu_bytes() {
+  return STG ? (size_t)kWavesPerBlock * 2 * RPW * (xl_max_h<WT>() / 32) : 0;
+}
+// Bytes of the kernel-wide LDS buffer of k_fused_ffn.
+template <typename WT, typename XT, int VEC, int RPW, bool XL, bool STG>
+constexpr size_t fused_raw_bytes() {
+  if constexpr (XL) return XlLayout<XT, VEC>::bytes(xl_max_h<WT>()) + stg_gu_bytes<WT, RPW, STG>();
+  else return 16;
+}
+
+template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2, bool XL,
+          bool STG>
 __global__ __launch_bounds__(kBlock) void k_fused_ffn(
     const WT* __restrict__ wbuf, const XT* __restrict__ x, const float* __restrict__ logits,
     float* act, XT* __restrict__ out, int32_t* __restrict__ ids_out, float* __restrict__ w_out,
@@ -871,6 +975,10 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
 
   TopK t;
   block_select_topk(logits, g.E, g.k, g.renorm, t);
+  // The x-in-LDS variant's buffer: the gate/up role's x copy (and, with
+  // STG, its waves' scale bytes); the down role's scale copy with STG.
+  static_assert(!STG || XL, "scale staging lives in the x-in-LDS variant's buffer");
+  __shared__ __align__(16) unsigned char lds_raw[fused_raw_bytes<WT, XT, VEC, RPW, XL, STG>()];
 
   if ((int)blockIdx.x < hs.n1) {
     // ---- gate/up block ----
@@ -892,9 +1000,9 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
       const int kk = __builtin_amdgcn_readfirstlane(G < hs.chunks ? G / bpk : 0);
       const int it = (G - kk * bpk) * kWavesPerBlock + wave;
       const int nrows = (G < hs.chunks && it < items) ? min(RPW, g.I - it * RPW) : 0;
-      gateup_item_xl<WT, XT, VEC, RPW, U1>(wbuf, x, act + kk * act_row + it * RPW, g,
-                                           topk_id(t, kk), topk_w(t, kk),
-                                           nrows > 0 ? it * RPW : 0, nrows, lane);
+      gateup_item_xl<WT, XT, VEC, RPW, U1, STG>(wbuf, x, act + kk * act_row + it * RPW, g,
+                                                topk_id(t, kk), topk_w(t, kk),
+                                                nrows > 0 ? it * RPW : 0, nrows, lane, lds_raw);
     } else if (G < hs.chunks) {
       const int kk = G / bpk;
       const int it = (G - kk * bpk) * kWavesPerBlock + wave;
@@ -924,8 +1032,18 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   const int nch = (g.I + kWave * VEC - 1) / (kWave * VEC);
   const int C = g.k * nch;
 
+  // STG: every selected expert's block-scale bytes of rows r0 .. r0 + nrows,
+  // [kk][j][I / 32], into lds_raw before the wait (they do not depend on act);
+  // wave w copies experts w, w + 4, ...
+  if constexpr (STG) {
+    const int ib = g.I / 32;
+    const int wu0 = __builtin_amdgcn_readfirstlane(wave);
+    for (int kk = wu0; kk < g.k; kk += kWavesPerBlock)
+      stage_bytes_lds(mx_row(wbuf + (int64_t)topk_id(t, kk) * g.stride, g, 2, r0),
+                      lds_raw + (size_t)kk * RPD * ib, nrows * ib, lane);
+  }
   V pre[U2][RPD];
-  down_tile_load<WT, VEC, RPD, U2>(pre, wbuf, g, t, r0, nrows, wave, nch, lane);
+  down_tile_load<WT, VEC, RPD, U2, STG>(pre, wbuf, g, t, r0, nrows, wave, nch, lane);
   // The next PRE chunks of this wave (after the U2 in registers) go to LDS:
   // the tail after the hand-off then has one dependent load round fewer, and
   // those bytes stream during the end of the gate/up phase.  Slot (v, j)
@@ -998,11 +1116,13 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
     else
       invalidate_l1();
   }
+  if constexpr (STG) __builtin_amdgcn_s_waitcnt(0);  // this wave's scale copies have landed
   __syncthreads();
 
   float acc[RPD];
 #pragma unroll
   for (int j = 0; j < RPD; ++j) acc[j] = 0.0f;
+  if constexpr (STG) down_tile_scales<WT, VEC, RPD, U2>(pre, lds_raw, g, nrows, wave, nch, lane);
   down_tile_fma<WT, V, VEC, RPD, U2>(acc, pre, act, g, act_row, wave, nch, lane, sdn);
   if constexpr (PRE > 0) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's global-to-LDS loads have landed
@@ -1026,7 +1146,8 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   }
   for (int q0 = wave + kWavesPerBlock * (U2 + PRE); q0 < C; q0 += kWavesPerBlock * U2) {
     V wv[U2][RPD];
-    down_tile_load<WT, VEC, RPD, U2>(wv, wbuf, g, t, r0, nrows, q0, nch, lane);
+    down_tile_load<WT, VEC, RPD, U2, STG>(wv, wbuf, g, t, r0, nrows, q0, nch, lane);
+    if constexpr (STG) down_tile_scales<WT, VEC, RPD, U2>(wv, lds_raw, g, nrows, q0, nch, lane);
     down_tile_fma<WT, V, VEC, RPD, U2>(acc, wv, act, g, act_row, q0, nch, lane, sdn);
   }
 #pragma unroll
@@ -1162,14 +1283,31 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   if constexpr (kXl) {
     constexpr int kBpc = kFp8 ? WR_XL_FP8_BPC : WR_XL_F16_BPC;  // MXFP4: no bound
     if (p.h <= kXlMax && (kFp4 || hs.n1 <= kBpc * cu_count())) {
-      hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true>),
+      // MXFP4: block-scale bytes staged in LDS when rows hold whole dwords of
+      // them (h and I multiples of 128), the down role's copy fits the buffer
+      // (k RPD I / 32 bytes), and the down rows are long enough for the copy
+      // to pay (I >= WR_F4_STG_MIN_I).  Measured: Mixtral 57.5 -> 55.7 us,
+      // DBRX 105.0 -> 102.0 us; DeepSeek (I = 1408) 18.7 -> 19.0 us.
+      if constexpr (kFp4 && RPW == 4) {
+        constexpr size_t kRaw = fused_raw_bytes<WT, XT, VEC, RPW, true, true>();
+        if (p.h % 128 == 0 && p.I % 128 == 0 && p.I >= WR_F4_STG_MIN_I &&
+            (size_t)p.k * RPD * (p.I / 32) <= kRaw) {
+          hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, true>),
+                             dim3(hs.n1 + n2), dim3(kBlock), 0, s,
+                             static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x),
+                             w.logits, w.act, static_cast<XT*>(p.out), p.topk_ids, p.topk_w, g,
+                             hs);
+          return hipGetLastError();
+        }
+      }
+      hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, false>),
                          dim3(hs.n1 + n2), dim3(kBlock), 0, s,
                          static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x), w.logits,
                          w.act, static_cast<XT*>(p.out), p.topk_ids, p.topk_w, g, hs);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, false>),
+  hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, false, false>),
                      dim3(hs.n1 + n2), dim3(kBlock), 0, s, static_cast<const WT*>(p.wbuf),
                      static_cast<const XT*>(p.x), w.logits, w.act, static_cast<XT*>(p.out),
                      p.topk_ids, p.topk_w, g, hs);
