@@ -353,32 +353,49 @@ __device__ __forceinline__ void gu_tile_load(H8 (&hi)[TP], H8 (&lo)[TP],
   }
 }
 
-// Down: act rows, fp32, split into two bf16 terms (BF), or two fp16 terms of
-// act 2^sx[q] (sx: the piece's pair exponent, split_exp).
-template <bool BF, int TP>
-__device__ __forceinline__ void dn_tile_load(H8 (&hi)[TP], H8 (&lo)[TP],
-                                             const float* __restrict__ act,
-                                             const int64_t (&off)[TP], const int (&sx)[TP],
-                                             int kb) {
+// Down: act rows, fp32, loaded raw (8 values per piece, zero for padding
+// tokens) and split only when stored (dn_tile_split): a split right after the
+// loads would wait for them, and, the load counter being in order, for the
+// same K step's weight loads issued before them, so no step's loads would be
+// in flight during the previous step's MFMAs.
+template <int TP>
+struct ActRaw {
+  f32x4 v[TP][2];
+};
+
+template <int TP>
+__device__ __forceinline__ void dn_tile_load(ActRaw<TP>& t, const float* __restrict__ act,
+                                             const int64_t (&off)[TP], int kb) {
 #pragma unroll
   for (int q = 0; q < TP; ++q) {
-    hi[q] = lo[q] = h8zero();
+    t.v[q][0] = t.v[q][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if (off[q] >= 0) {
       const float* a = act + off[q] + kb;
-      const f32x4 v0 = *reinterpret_cast<const f32x4*>(a);
-      const f32x4 v1 = *reinterpret_cast<const f32x4*>(a + 4);
+      t.v[q][0] = *reinterpret_cast<const f32x4*>(a);
+      t.v[q][1] = *reinterpret_cast<const f32x4*>(a + 4);
+    }
+  }
+}
+
+// The two terms of a raw act piece: bf16 terms (BF), or fp16 terms of
+// act 2^sx[q] (sx: the piece's pair exponent, split_exp).
+template <bool BF, int TP>
+__device__ __forceinline__ void dn_tile_split(H8 (&hi)[TP], H8 (&lo)[TP], const ActRaw<TP>& t,
+                                              const int (&sx)[TP]) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const float v = BF ? (t < 4 ? v0[t] : v1[t - 4]) : ldexpf(t < 4 ? v0[t] : v1[t - 4], sx[q]);
-        if constexpr (BF) {
-          const __bf16 vh = (__bf16)v;
-          hi[q][t] = __builtin_bit_cast(f16, vh);
-          lo[q][t] = __builtin_bit_cast(f16, (__bf16)(v - (float)vh));
-        } else {
-          const f16 vh = (f16)v;
-          hi[q][t] = vh;
-          lo[q][t] = (f16)(v - (float)vh);
-        }
+  for (int q = 0; q < TP; ++q) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float r = t.v[q][i / 4][i % 4];
+      const float v = BF ? r : ldexpf(r, sx[q]);
+      if constexpr (BF) {
+        const __bf16 vh = (__bf16)v;
+        hi[q][i] = __builtin_bit_cast(f16, vh);
+        lo[q][i] = __builtin_bit_cast(f16, (__bf16)(v - (float)vh));
+      } else {
+        const f16 vh = (f16)v;
+        hi[q][i] = vh;
+        lo[q][i] = (f16)(v - (float)vh);
       }
     }
   }
@@ -770,17 +787,21 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK>& xs, WTile<16>& wt,
       sx[q] = n < mt ? pair_exp<WT>(amax, p0 + n) : 0;
     }
     WRegs<WT, 16> wr;
-    H8 th[TP], tl[TP];
+    ActRaw<TP> ar;
     w_load<WT, 16>(wr, wbase, wsc, sb * kBK);
-    dn_tile_load<bf16_ops<WT>()>(th, tl, act, off, sx, sb * kBK);
+    dn_tile_load(ar, act, off, sb * kBK);
     for (int s = sb; s < se; ++s) {
       __syncthreads();
-      tile_store(xs, th, tl, true);
+      {
+        H8 th[TP], tl[TP];
+        dn_tile_split<bf16_ops<WT>()>(th, tl, ar, sx);
+        tile_store(xs, th, tl, true);
+      }
       w_store<WT, 16>(wt, wr, lane);
       __syncthreads();
       if (s + 1 < se) {
         w_load<WT, 16>(wr, wbase, wsc, (s + 1) * kBK);
-        dn_tile_load<bf16_ops<WT>()>(th, tl, act, off, sx, (s + 1) * kBK);
+        dn_tile_load(ar, act, off, (s + 1) * kBK);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
