@@ -21,6 +21,7 @@ bounded sample of the same layer.
   python bench.py --copy-probe     # plain device copy, for counter calibration
   python bench.py --op naive       # the naive multi-kernel path, with fused beside it
   python bench.py --read-probe     # read-only streaming ceiling over the same bytes
+  python bench.py --throughput     # batched vs a loop of single-token calls (Mixtral, DBRX)
 
 The headline line also carries roofline.read_ceiling: the best rate of a
 plain read-only streaming kernel (libwr_probe.so) over exactly the selected
@@ -230,6 +231,61 @@ def batched_bench(args) -> int:
                          "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
                          "bytes": f"distinct selected experts' {args.weights} weights"},
         }), flush=True)
+    return 0
+
+
+def throughput_bench(args) -> int:
+    """Batched against a loop of single-token calls, as the reference's
+    benchmarks/bench_throughput.py:60-118 times them: Mixtral (top-2) and
+    DBRX with top-2 (the reference's throughput configs), B in 1..64 (or
+    --batch), uniformly random tokens (no clustering), the layers rotated.
+    The loop makes B fused_moe calls, one per token of the batch (the
+    reference repeats token 0 B times; distinct tokens route like a real
+    batch).  One JSON line per model."""
+    import torch
+    from warp_route import functional as F
+    from warp_route.synthetic import CONFIGS, make_config_layer
+    sizes = [int(v) for v in args.batch.split(",")] if args.batch else [1, 2, 4, 8, 16, 32, 64]
+    dev = torch.device("cuda:0")
+    for name in ("mixtral", "dbrx"):
+        cfg = dataclasses.replace(CONFIGS[name], top_k=2).with_weights(weight_dtype(args.weights))
+        E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+        log(f"[bench] throughput: {args.layers} {name} {args.weights} layers, top-{k}")
+        layers = [make_config_layer(cfg, seed=s, batch=max(sizes), device=dev, gen_device=dev)
+                  for s in range(args.layers)]
+        L = len(layers)
+        rows = []
+        for B in sizes:
+            xs = [x[:B].contiguous() for x, _, _ in layers]
+            batched = _timed(lambda i: F.batched_fused_moe(xs[i % L], layers[i % L][1],
+                                                           layers[i % L][2], E, h, I, k,
+                                                           cfg.renormalize),
+                             args.steps, args.warmup)
+
+            def loop(i):
+                x, gw, buf = xs[i % L], layers[i % L][1], layers[i % L][2]
+                for b in range(B):
+                    F.fused_moe(x[b], gw, buf, E, h, I, k, cfg.renormalize)
+
+            iters = max(10, args.steps // B)
+            looped = _timed(loop, iters, max(2, args.warmup // B))
+            rows.append({"batch": B, "batched_us": round(batched, 2), "loop_us": round(looped, 2),
+                         "batched_tok_per_s": round(B / batched * 1e6, 1),
+                         "loop_tok_per_s": round(B / looped * 1e6, 1),
+                         "us_per_tok_batched": round(batched / B, 3),
+                         "us_per_tok_loop": round(looped / B, 3),
+                         "speedup": round(looped / batched, 3)})
+        print(json.dumps({
+            "metric": "batched vs single-token loop, µs per call (benchmarks/bench_throughput.py)",
+            "unit": "us/call", "higher_is_better": False, "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "dtype": f"{WLABEL[args.weights]} weights, f32 accumulate",
+            "data": "synthetic (seeded random-init layers, x ~ N(0, 1), unclustered)",
+            "config": {"workload": f"{name} MoE layer, top-{k}", "experts": E, "hidden": h,
+                       "intermediate": I, "layers_rotated": L},
+            "rows": rows,
+        }), flush=True)
+        del layers
+        torch.cuda.empty_cache()
     return 0
 
 
@@ -466,6 +522,9 @@ def main() -> int:
                     help="skip the streaming-ceiling measurement in the headline line")
     ap.add_argument("--batch", default=None,
                     help="comma-separated batch sizes: time batched decode instead")
+    ap.add_argument("--throughput", action="store_true",
+                    help="batched against a loop of single-token calls, Mixtral and DBRX, "
+                         "top-2, B = 1..64 (or --batch)")
     ap.add_argument("--stack", type=int, default=0,
                     help="time one token through this many layers instead")
     ap.add_argument("--graph", action="store_true",
@@ -494,6 +553,8 @@ def main() -> int:
         return read_probe_bench(args)
     if args.op == "naive":
         return naive_bench(args)
+    if args.throughput:
+        return throughput_bench(args)
     if args.batch:
         return batched_bench(args)
     if args.stack:
