@@ -8,7 +8,12 @@ The kernels' speed rests on properties the source does not show:
 - the fp16 / bf16 / MXFP4 single-token kernels must fit 128 VGPRs (4 waves
   per SIMD), as the kernel descriptor allocates them: the metadata's
   vgpr_count can be lower than the allocation, which is rounded up from the
-  accumulation-register offset (124 listed and 136 allocated has happened).
+  accumulation-register offset (124 listed and 136 allocated has happened);
+- in the batched kernels' K loops, a K step's weight loads must still be in
+  flight when the previous step's MFMAs run.  The load counter is in order,
+  so any use of a value loaded after the weights (a conversion of the act or
+  x tile, a mask of an MXFP4 scale byte) placed before the MFMAs waits for
+  the weights too; that has happened three times, invisible in the source.
 The compiler has broken the first two silently, by folding a select chain
 over the TopK arrays back into a runtime-indexed array (in scratch memory in
 the x-in-LDS kernels, in LDS in the others).  These tests read the kernel
@@ -50,6 +55,57 @@ def _descriptor_vgprs(elf_path, readelf):
                 out[f[-1][:-3]] = ((rsrc1 & 0x3F) + 1) * 8
                 break
     return out
+
+
+def _branch_target(addr, op, args):
+    if not (op == "s_branch" or op.startswith("s_cbranch")):
+        return None
+    imm = int(args.split()[0])
+    return addr + 4 + 4 * (imm - 65536 if imm > 32767 else imm)
+
+
+def _walk(insns, idx, i):
+    """Instruction indices executed after instruction i: fall-through at
+    conditional branches, unconditional branches followed."""
+    j, n = i + 1, 0
+    while j < len(insns) and n < 4000:
+        n += 1
+        yield j
+        addr, op, args = insns[j]
+        if op == "s_endpgm":
+            return
+        if op == "s_branch":
+            t = _branch_target(addr, op, args)
+            if t not in idx:
+                return
+            j = idx[t]
+        else:
+            j += 1
+
+
+def _waits_before_mfma(insns):
+    """Weight loads (global_load_dwordx4 ... nt) inside a loop whose forward
+    path reaches a wait that needs them before any MFMA: [(load, wait)]."""
+    idx = {a: i for i, (a, _, _) in enumerate(insns)}
+    bad = []
+    for i, (addr, op, args) in enumerate(insns):
+        if not (op.startswith("global_load_dwordx4") and args.endswith(" nt")):
+            continue
+        path = list(_walk(insns, idx, i))
+        if i not in path:  # not in a loop: a prologue load, awaited before the first step
+            continue
+        after = 0  # vector-memory instructions issued after this load
+        for j in path:
+            a, opj, argj = insns[j]
+            if opj.startswith("v_mfma") or j == i:
+                break
+            if re.match(r"(global|buffer)_(load|store|atomic)", opj):
+                after += 1
+            m = re.search(r"vmcnt\((\d+)\)", argj) if opj == "s_waitcnt" else None
+            if m and int(m.group(1)) <= after:
+                bad.append((hex(addr), hex(a)))
+                break
+    return bad
 
 
 def _tool(name):
@@ -104,6 +160,44 @@ def kernels(tmp_path_factory):
     assert any("k_fused_ffn" in k for k in out) and any("k_gu_mfma" in k for k in out), \
         f"expected kernels missing from the code object ({len(out)} found)"
     return out
+
+
+@pytest.fixture(scope="module")
+def batched_isa(kernels, tmp_path_factory):
+    """{kernel symbol: [(address, mnemonic, operands)]} of the batched MFMA
+    kernels, disassembled from the code objects the kernels fixture unpacked."""
+    d = tmp_path_factory.getbasetemp()
+    out = {}
+    for co in sorted(d.glob("codeobj*/gfx950_*.elf")):
+        text = subprocess.run([_tool("llvm-objdump"), "-d", "--no-show-raw-insn", str(co)],
+                              check=True, capture_output=True, text=True).stdout
+        name = None
+        for line in text.splitlines():
+            m = re.match(r"^[0-9a-f]+ <(\S+)>:$", line)
+            if m:
+                name = m.group(1) if re.search(r"k_(gu|dn)_(mfma|f32)", m.group(1)) else None
+                if name:
+                    out[name] = []
+                continue
+            m = re.match(r"^\s+(\S+)\s*(.*?)\s*//\s*([0-9A-F]+):", line)
+            if name and m:
+                out[name].append((int(m.group(3), 16), m.group(1), m.group(2)))
+    return out
+
+
+def test_batched_k_loops_keep_weight_loads_in_flight_over_mfmas(batched_isa):
+    assert len(batched_isa) >= 30, sorted(batched_isa)
+    looped = 0
+    bad = {}
+    for name, insns in batched_isa.items():
+        idx = {a: i for i, (a, _, _) in enumerate(insns)}
+        looped += any(op.startswith("global_load_dwordx4") and args.endswith(" nt")
+                      and i in _walk(insns, idx, i) for i, (_, op, args) in enumerate(insns))
+        b = _waits_before_mfma(insns)
+        if b:
+            bad[name] = b[:3]
+    assert looped == len(batched_isa), "a kernel's K loop was not found"
+    assert not bad, f"K-loop weight loads awaited before the MFMAs: {bad}"
 
 
 def test_no_kernel_uses_scratch_memory_or_spills(kernels):

@@ -459,7 +459,7 @@ template <typename WT, int ROWS>
 struct WRegs {
   static constexpr int N = ROWS / WGeo<WT>::kRowsPer;  // load instructions per K step
   u32x4 v[N];
-  uint32_t e[std::is_same<WT, fp4x2>::value ? N : 1];  // MXFP4 E8M0 scale bytes
+  uint8_t e[std::is_same<WT, fp4x2>::value ? N : 1];  // MXFP4 E8M0 scale bytes
 };
 
 // Loads of one K step: base[i] is this lane's address for row group i at
@@ -578,6 +578,10 @@ __device__ __forceinline__ void gu_pass(TokTile<TOK>& xs, WTile<32>& wt,
       w_load<WT, 32>(wr, wbase, wsc, (s + 1) * kBK);
       gu_tile_load(th, tl, x_hi, x_lo, off, (s + 1) * kBK, LO);
     }
+    // MXFP4: the next step's loads stay ahead of this step's MFMAs (the
+    // scheduler sank them below the MFMAs at 32 and 64 tokens, so each step's
+    // loads were awaited with no MFMA work in flight).
+    if constexpr (std::is_same<WT, fp4x2>::value) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int c = 4 * j + (lane >> 4);
@@ -803,6 +807,8 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK>& xs, WTile<16>& wt,
         w_load<WT, 16>(wr, wbase, wsc, (s + 1) * kBK);
         dn_tile_load(ar, act, off, (s + 1) * kBK);
       }
+      if constexpr (std::is_same<WT, fp4x2>::value)
+        __builtin_amdgcn_sched_barrier(0);  // loads ahead of the MFMAs, as in gu_pass
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int c = 4 * j + (lane >> 4);
@@ -939,25 +945,35 @@ __device__ __forceinline__ void f32_tile_rows(int64_t (&off)[TP], const int32_t*
     off[q] = n < mt ? (int64_t)row * ld + c * 4 : -1;
   }
 }
+// A piece as loaded: four values of the source's own type (zero for a
+// padding token).  fp16 x is widened only when stored (f32_tile_store): a
+// conversion right after the loads would wait for them and, the load counter
+// being in order, for the same K step's weight loads issued before them.
+template <typename XT>
+struct RawX4 {
+  typedef f32x4 type;
+};
+template <>
+struct RawX4<f16> {
+  typedef f16x4 type;
+};
 template <typename XT, int TP>
-__device__ __forceinline__ void f32_tile_load(f32x4 (&t)[TP], const XT* __restrict__ src,
+__device__ __forceinline__ void f32_tile_load(typename RawX4<XT>::type (&t)[TP],
+                                              const XT* __restrict__ src,
                                               const int64_t (&off)[TP], int kb) {
+  typedef typename RawX4<XT>::type R;
 #pragma unroll
   for (int q = 0; q < TP; ++q) {
-    t[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (off[q] >= 0) {
-      float v[4];
-      load_x<XT, 4>(src + off[q] + kb, v);
-      t[q] = f32x4{v[0], v[1], v[2], v[3]};
-    }
+    t[q] = R{0, 0, 0, 0};
+    if (off[q] >= 0) t[q] = *reinterpret_cast<const R*>(src + off[q] + kb);
   }
 }
-template <int TOK, int TP>
-__device__ __forceinline__ void f32_tile_store(TileF<TOK>& xs, const f32x4 (&t)[TP]) {
+template <int TOK, typename R, int TP>
+__device__ __forceinline__ void f32_tile_store(TileF<TOK>& xs, const R (&t)[TP]) {
 #pragma unroll
   for (int q = 0; q < TP; ++q) {
     const int i = threadIdx.x + kBlk * q;
-    xs.v[i / kPF][i % kPF] = t[q];
+    xs.v[i / kPF][i % kPF] = f32x4{(float)t[q][0], (float)t[q][1], (float)t[q][2], (float)t[q][3]};
   }
 }
 
@@ -998,7 +1014,7 @@ __device__ __forceinline__ void gu_pass_f32(TileF<TOK>& xs, TileF<32>& wt,
   const int ns = g.h / kBKF;
   const int q = lane >> 4, rl = lane & 15;
   WRegsF<32> wr;
-  f32x4 tv[TP];
+  typename RawX4<XT>::type tv[TP];
   f32_w_load<32>(wr, wbase, 0);
   f32_tile_load(tv, x, off, 0);
   for (int s = 0; s < ns; ++s) {
