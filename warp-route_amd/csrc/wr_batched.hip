@@ -64,11 +64,9 @@ namespace {
 #endif
 
 constexpr int kBlk = 256;       // 4 waves
-constexpr int kBK = 128;        // K step (columns per LDS tile)
+constexpr int kBK = 128;        // the base K step (columns); every step width is a multiple
 constexpr int kBM = 64;         // rows per block: 4 waves x 16
 constexpr int kMaxTok = 64;     // tokens per pass, at most: 4 MFMA N tiles
-constexpr int kPieces = kBK / 8;        // 16-byte pieces per token row of a tile
-constexpr int kLdsRow = kPieces + 1;    // padded row: spreads lanes over the LDS banks
 
 typedef f16x8 H8;  // eight 16-bit operands: fp16, or bf16 bit patterns
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -302,36 +300,55 @@ __device__ __forceinline__ void route_small_publish(const SmallRoute& sr, int B,
 }
 
 // ---------------------------------------------------------------------------
-// Token tiles in LDS.  xs[0] holds the hi terms, xs[1] the lo terms; row n is
-// token n of the pass, piece c covers columns [8 c, 8 c + 8) of the K step.
+// K steps.  A step covers KC columns of the K dimension.  Weight rows are
+// staged in LDS as the bytes they are and decoded per MFMA fragment, so a
+// step's tile costs KC times the weight's bits, not 16 bits per weight.  With
+// 16-token tiles every weight type takes a step of 256 bytes of row (KC =
+// 128 fp16 / bf16, 256 fp8, 512 MXFP4): each wave then has 8 KB of weights
+// in flight per step and every load instruction reads 4 rows x 256 bytes
+// (with 128-column steps fp8 had half of that in flight, in 8 x 128-byte
+// pieces, and MXFP4 a quarter, in 16 x 64 bytes).  Larger token tiles, and K
+// dimensions that the wide step does not divide, take KC = 128.
 // ---------------------------------------------------------------------------
-// TOK tokens per pass (16, 32 or 64): a launch whose experts have at most 16
-// (32) tokens each takes the smaller tile, whose LDS and registers leave room
-// for more blocks per CU.
-template <int TOK>
+template <typename WT>
+constexpr int wbits() {  // bits per stored weight
+  return std::is_same<WT, fp4x2>::value ? 4 : (std::is_same<WT, fp8w>::value ? 8 : 16);
+}
+template <typename WT>
+constexpr int kc_wide() {  // the 256-byte step, in columns
+  return 256 * 8 / wbits<WT>();
+}
+
+// Token tiles in LDS: hi holds the hi terms, lo the lo terms; row n is token
+// n of the pass, piece c covers columns [8 c, 8 c + 8) of the K step.  TOK
+// tokens per pass (16, 32 or 64): a launch whose experts have at most 16 (32)
+// tokens each takes the smaller tile, whose LDS and registers leave room for
+// more blocks per CU.
+template <int TOK, int KC>
 struct TokTile {
-  H8 hi[TOK][kLdsRow];
-  H8 lo[TOK][kLdsRow];
+  static constexpr int kP = KC / 8;  // 16-byte pieces per token row
+  H8 hi[TOK][kP + 1];                // rows padded by a piece: spread over the LDS banks
+  H8 lo[TOK][kP + 1];
 };
 
 // One thread's share of a token tile, held in registers between the global
 // loads and the LDS stores: pieces i = threadIdx.x + kBlk * q, token row
-// n = i / kPieces, 8 columns at 8 (i % kPieces) of the K step.
-template <int TOK>
+// n = i / (KC / 8), 8 columns at 8 (i % (KC / 8)) of the K step.
+template <int TOK, int KC>
 constexpr int tile_pieces() {
-  static_assert(TOK * kPieces % kBlk == 0, "whole pieces per thread");
-  return TOK * kPieces / kBlk;  // 1 or 4
+  static_assert(TOK * (KC / 8) % kBlk == 0, "whole pieces per thread");
+  return TOK * (KC / 8) / kBlk;  // 1, 2 or 4
 }
 
 // Element offset of each piece's row start (plus its column), or -1 for a
 // padding token; fixed for a whole pass.
-template <int TP>
+template <int KC, int TP>
 __device__ __forceinline__ void tile_rows(int64_t (&off)[TP], const int32_t* rows, int direct0,
                                           int mt, int ld) {
 #pragma unroll
   for (int q = 0; q < TP; ++q) {
     const int i = threadIdx.x + kBlk * q;
-    const int n = i / kPieces, c = i % kPieces;
+    const int n = i / (KC / 8), c = i % (KC / 8);
     const int row = rows != nullptr ? (n < mt ? rows[n] : 0) : direct0 + n;
     off[q] = n < mt ? (int64_t)row * ld + c * 8 : -1;
   }
@@ -401,63 +418,69 @@ __device__ __forceinline__ void dn_tile_split(H8 (&hi)[TP], H8 (&lo)[TP], const 
   }
 }
 
-template <int TOK, int TP>
-__device__ __forceinline__ void tile_store(TokTile<TOK>& xs, const H8 (&hi)[TP],
+template <int TOK, int KC, int TP>
+__device__ __forceinline__ void tile_store(TokTile<TOK, KC>& xs, const H8 (&hi)[TP],
                                            const H8 (&lo)[TP], bool with_lo) {
-  static_assert(TP == tile_pieces<TOK>(), "tile shares");
+  static_assert(TP == tile_pieces<TOK, KC>(), "tile shares");
 #pragma unroll
   for (int q = 0; q < TP; ++q) {
     const int i = threadIdx.x + kBlk * q;
-    const int n = i / kPieces, c = i % kPieces;
+    const int n = i / (KC / 8), c = i % (KC / 8);
     xs.hi[n][c] = hi[q];
     if (with_lo) xs.lo[n][c] = lo[q];
   }
 }
 
-// Weight tiles.  A wave's rows are loaded 16 bytes per lane, a K step of a
-// row (128 columns) per group of lanes: fp16 4 rows x 256 bytes per
-// instruction (lane l: row 4 i + l / 16 of group i, columns 8 (l % 16) ..
-// + 8), fp8 8 rows x 128 bytes (lane l: row 8 i + l / 8, columns 16 (l % 8)
-// .. + 16).  A streaming probe measured these patterns at 6.2 and 6.1 TB/s
+// Weight tiles.  A wave's rows are loaded 16 bytes per lane, KC columns of a
+// row per group of LR = KC / E lanes (E weights per 16 bytes: 8 fp16 / bf16,
+// 16 fp8, 32 MXFP4), RP = 64 / LR rows per instruction: lane l takes row
+// RP i + l / LR of group i, the 16 bytes at piece l % LR of the step.  A
+// streaming probe measured 4 rows x 256 bytes per instruction at 6.2 TB/s
 // against 5.5 TB/s for MFMA fragments loaded straight from memory (16 rows x
-// 64 bytes per instruction).  The wave stores its rows, as fp16, into its own
-// LDS tile (rows padded to 17 pieces, so the fragment reads below are free of
-// bank conflicts) and reads the MFMA A fragments from there: for MFMA j of
-// the K step, lane l takes row l % 16, columns 32 j + 8 (l / 16) .. + 8.
-// fp8 codes become fp16 with v_cvt_scalef32_pk_f16_fp8 (scale 1: every E4M3
-// value is an fp16 value), two per instruction.
-template <int ROWS>
-struct WTile {
-  H8 w[ROWS][kLdsRow];
+// 64 bytes).  The wave stores the bytes as they are into its own LDS tile
+// (rows padded by one piece, so the fragment reads below are free of bank
+// conflicts), MXFP4's E8M0 scale bytes (one per piece: a piece is one
+// 32-code block) beside them.  MFMA j of the step reads, in lane l, the 8
+// weights of row l % 16 at columns 32 j + 8 (l / 16) and decodes them:
+// fp16 and bf16 as they are, fp8 E4M3 codes to fp16 with
+// v_cvt_scalef32_pk_f16_fp8 (scale 1: every E4M3 value is an fp16 value),
+// MXFP4 codes times their block scale to bf16.
+template <typename WT, int KC>
+struct WGeo {
+  static constexpr int kElems = 128 / wbits<WT>();   // weights per 16 bytes: 8, 16, 32
+  static constexpr int kLaneRow = KC / kElems;       // lanes (16-byte pieces) per row
+  static constexpr int kRowsPer = kWave / kLaneRow;  // rows per instruction
+  static_assert(KC % kElems == 0 && kWave % kLaneRow == 0, "whole pieces, whole rows");
 };
 
-template <typename WT>
-struct WGeo {
-  static constexpr int kElems = 16 / (int)sizeof(WT) * epu<WT>();  // per lane: 8, 16, 32 (mxfp4)
-  static constexpr int kLaneRow = kBK / kElems;                     // lanes per row: 16, 8, 4
-  static constexpr int kRowsPer = kWave / kLaneRow;                 // rows per instruction: 4, 8, 16
+template <typename WT, int ROWS, int KC>
+struct WTile {
+  static constexpr int kP = WGeo<WT, KC>::kLaneRow;
+  H8 w[ROWS][kP + 1];
+  uint8_t s[std::is_same<WT, fp4x2>::value ? ROWS : 1][KC / 32];  // MXFP4 scale bytes
 };
 
 // This lane's address of row group 0 at column 0 of the K loop, for the tile
 // whose first row is `row` of a matrix with row length ld (elements).
-template <typename WT>
+template <typename WT, int KC>
 __device__ __forceinline__ const WT* w_lane_base(const WT* mat, int row, int64_t ld, int lane) {
-  return mat + eoff<WT>((int64_t)(row + lane / WGeo<WT>::kLaneRow) * ld +
-                        (lane % WGeo<WT>::kLaneRow) * WGeo<WT>::kElems);
+  typedef WGeo<WT, KC> G;
+  return mat + eoff<WT>((int64_t)(row + lane / G::kLaneRow) * ld + (lane % G::kLaneRow) * G::kElems);
 }
 
 // MXFP4: this lane's E8M0 byte of the same block at column 0 of the K loop,
 // for a matrix whose block scales start at sc ([rows][ld / 32] bytes).
-template <typename WT>
+template <typename WT, int KC>
 __device__ __forceinline__ const uint8_t* w_lane_scale(const uint8_t* sc, int row, int64_t ld,
                                                        int lane) {
-  return sc + (int64_t)(row + lane / WGeo<WT>::kLaneRow) * (ld / 32) +
-         (lane % WGeo<WT>::kLaneRow) * WGeo<WT>::kElems / 32;
+  typedef WGeo<WT, KC> G;
+  return sc + (int64_t)(row + lane / G::kLaneRow) * (ld / 32) +
+         (lane % G::kLaneRow) * G::kElems / 32;
 }
 
-template <typename WT, int ROWS>
+template <typename WT, int ROWS, int KC>
 struct WRegs {
-  static constexpr int N = ROWS / WGeo<WT>::kRowsPer;  // load instructions per K step
+  static constexpr int N = ROWS / WGeo<WT, KC>::kRowsPer;  // load instructions per K step
   u32x4 v[N];
   uint8_t e[std::is_same<WT, fp4x2>::value ? N : 1];  // MXFP4 E8M0 scale bytes
 };
@@ -465,12 +488,13 @@ struct WRegs {
 // Loads of one K step: base[i] is this lane's address for row group i at
 // column 0 of the K loop (sc[i] its MXFP4 scale byte); kb is the step's
 // first column.
-template <typename WT, int ROWS>
-__device__ __forceinline__ void w_load(WRegs<WT, ROWS>& r,
-                                       const WT* const (&base)[WRegs<WT, ROWS>::N],
-                                       const uint8_t* const (&sc)[WRegs<WT, ROWS>::N], int kb) {
+template <typename WT, int ROWS, int KC>
+__device__ __forceinline__ void w_load(WRegs<WT, ROWS, KC>& r,
+                                       const WT* const (&base)[WRegs<WT, ROWS, KC>::N],
+                                       const uint8_t* const (&sc)[WRegs<WT, ROWS, KC>::N],
+                                       int kb) {
 #pragma unroll
-  for (int i = 0; i < WRegs<WT, ROWS>::N; ++i) {
+  for (int i = 0; i < WRegs<WT, ROWS, KC>::N; ++i) {
     r.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base[i] + eoff<WT>(kb)));
     if constexpr (std::is_same<WT, fp4x2>::value) r.e[i] = sc[i][kb / 32];
   }
@@ -500,24 +524,32 @@ __device__ __forceinline__ H8 fp4x8_to_bf8(uint32_t w, float s) {
   return __builtin_bit_cast(H8, bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]});
 }
 
-template <typename WT, int ROWS>
-__device__ __forceinline__ void w_store(WTile<ROWS>& t, const WRegs<WT, ROWS>& r, int lane) {
-  constexpr int LR = WGeo<WT>::kLaneRow, RP = WGeo<WT>::kRowsPer;
+template <typename WT, int ROWS, int KC>
+__device__ __forceinline__ void w_store(WTile<WT, ROWS, KC>& t, const WRegs<WT, ROWS, KC>& r,
+                                        int lane) {
+  constexpr int LR = WGeo<WT, KC>::kLaneRow, RP = WGeo<WT, KC>::kRowsPer;
 #pragma unroll
-  for (int i = 0; i < WRegs<WT, ROWS>::N; ++i) {
+  for (int i = 0; i < WRegs<WT, ROWS, KC>::N; ++i) {
     const int row = RP * i + lane / LR;
-    if constexpr (std::is_same<WT, fp4x2>::value) {
-      const int c = 4 * (lane % LR);
-      const float s = e8m0_value(r.e[i]);
-#pragma unroll
-      for (int p = 0; p < 4; ++p) t.w[row][c + p] = fp4x8_to_bf8(r.v[i][p], s);
-    } else if constexpr (std::is_same<WT, fp8w>::value) {
-      const int c = 2 * (lane % LR);
-      t.w[row][c] = fp8x8_to_h8(r.v[i][0], r.v[i][1]);
-      t.w[row][c + 1] = fp8x8_to_h8(r.v[i][2], r.v[i][3]);
-    } else {
-      t.w[row][lane % LR] = __builtin_bit_cast(H8, r.v[i]);
-    }
+    t.w[row][lane % LR] = __builtin_bit_cast(H8, r.v[i]);
+    if constexpr (std::is_same<WT, fp4x2>::value) t.s[row][lane % LR] = r.e[i];
+  }
+}
+
+// The A operand of MFMA j of a step, in a lane of quadrant q (l / 16): the 8
+// weights of tile row `row` at columns 32 j + 8 q, decoded.
+template <typename WT, int ROWS, int KC>
+__device__ __forceinline__ H8 a_frag(const WTile<WT, ROWS, KC>& t, int row, int j, int q) {
+  if constexpr (wbits<WT>() == 16) {
+    return t.w[row][4 * j + q];
+  } else if constexpr (wbits<WT>() == 8) {
+    // 16 codes per piece: piece 2 j + q / 2, bytes 8 (q % 2) ..
+    const uint2 v = reinterpret_cast<const uint2*>(&t.w[row][2 * j + (q >> 1)])[q & 1];
+    return fp8x8_to_h8(v.x, v.y);
+  } else {
+    // 32 codes (one block) per piece: piece j, dword q
+    const uint32_t v = reinterpret_cast<const uint32_t*>(&t.w[row][j])[q];
+    return fp4x8_to_bf8(v, e8m0_value(t.s[row][j]));
   }
 }
 
@@ -537,10 +569,10 @@ struct GuScale {
   unsigned* s_amax;
 };
 
-template <typename WT, bool LO, int NT, int TOK>
-__device__ __forceinline__ void gu_pass(TokTile<TOK>& xs, WTile<32>& wt,
-                                        const WT* const (&wbase)[WRegs<WT, 32>::N],
-                                        const uint8_t* const (&wsc)[WRegs<WT, 32>::N],
+template <typename WT, bool LO, int NT, int TOK, int KC>
+__device__ __forceinline__ void gu_pass(TokTile<TOK, KC>& xs, WTile<WT, 32, KC>& wt,
+                                        const WT* const (&wbase)[WRegs<WT, 32, KC>::N],
+                                        const uint8_t* const (&wsc)[WRegs<WT, 32, KC>::N],
                                         const f16* __restrict__ x_hi,
                                         const f16* __restrict__ x_lo, const BatchRoute& r,
                                         int p0, int mt, float* __restrict__ act, int row0,
@@ -549,10 +581,10 @@ __device__ __forceinline__ void gu_pass(TokTile<TOK>& xs, WTile<32>& wt,
   f32x4 ag[NT], au[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) ag[n] = au[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  constexpr int TP = tile_pieces<TOK>();
+  constexpr int TP = tile_pieces<TOK, KC>();
   int64_t off[TP];
-  tile_rows(off, r.pair_tok + p0, 0, mt, g.h);
-  const int ns = g.h / kBK;
+  tile_rows<KC>(off, r.pair_tok + p0, 0, mt, g.h);
+  const int ns = g.h / KC;
   // fp16 operands: the epilogue tokens' x exponents, loaded here so that the
   // loads are in flight with the first K step's.
   constexpr bool SC = !bf16_ops<WT>();
@@ -565,28 +597,28 @@ __device__ __forceinline__ void gu_pass(TokTile<TOK>& xs, WTile<32>& wt,
 
   // Software pipeline, one K step deep: step s+1's weight and token loads are
   // issued before step s's MFMAs.
-  WRegs<WT, 32> wr;
+  WRegs<WT, 32, KC> wr;
   H8 th[TP], tl[TP];
-  w_load<WT, 32>(wr, wbase, wsc, 0);
+  w_load<WT, 32, KC>(wr, wbase, wsc, 0);
   gu_tile_load(th, tl, x_hi, x_lo, off, 0, LO);
   for (int s = 0; s < ns; ++s) {
     __syncthreads();  // every wave is done reading the previous tiles
     tile_store(xs, th, tl, LO);
-    w_store<WT, 32>(wt, wr, lane);
+    w_store<WT, 32, KC>(wt, wr, lane);
     __syncthreads();
     if (s + 1 < ns) {
-      w_load<WT, 32>(wr, wbase, wsc, (s + 1) * kBK);
-      gu_tile_load(th, tl, x_hi, x_lo, off, (s + 1) * kBK, LO);
+      w_load<WT, 32, KC>(wr, wbase, wsc, (s + 1) * KC);
+      gu_tile_load(th, tl, x_hi, x_lo, off, (s + 1) * KC, LO);
     }
     // MXFP4: the next step's loads stay ahead of this step's MFMAs (the
     // scheduler sank them below the MFMAs at 32 and 64 tokens, so each step's
     // loads were awaited with no MFMA work in flight).
     if constexpr (std::is_same<WT, fp4x2>::value) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < KC / 32; ++j) {
       const int c = 4 * j + (lane >> 4);
-      const H8 ga = wt.w[lane & 15][c];
-      const H8 ua = wt.w[16 + (lane & 15)][c];
+      const H8 ga = a_frag(wt, lane & 15, j, lane >> 4);
+      const H8 ua = a_frag(wt, 16 + (lane & 15), j, lane >> 4);
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
         const int tn = n * 16 + (lane & 15);
@@ -666,7 +698,7 @@ struct GuRouteLds<false> {};
 
 // ROUTE: the block routes the batch itself (route_small) instead of reading
 // k_route's output; block (0, 0) publishes the routing for the later kernels.
-template <typename WT, bool LO, int TOK, bool ROUTE>
+template <typename WT, bool LO, int TOK, bool ROUTE, int KC>
 __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
                                                   const f16* __restrict__ x_hi,
                                                   const f16* __restrict__ x_lo,
@@ -676,8 +708,8 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
                                                   const float* __restrict__ logits,
                                                   int32_t* __restrict__ ids_out,
                                                   float* __restrict__ w_out) {
-  __shared__ TokTile<TOK> xs;
-  __shared__ WTile<32> wts[kBlk / kWave];
+  __shared__ TokTile<TOK, KC> xs;
+  __shared__ WTile<WT, 32, KC> wts[kBlk / kWave];
   __shared__ GuRouteLds<ROUTE> rl;
   __shared__ unsigned s_amax[bf16_ops<WT>() ? 1 : TOK];
   if (!bf16_ops<WT>() && (int)threadIdx.x < TOK) s_amax[threadIdx.x] = 0u;
@@ -707,9 +739,9 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
   const int wave = threadIdx.x / kWave;
   const int row0 = blockIdx.x * kBM + wave * 16;
   const WT* blk = wbuf + (int64_t)e * g.stride;
-  const WT* G = w_lane_base(blk, row0, g.h, lane);
+  const WT* G = w_lane_base<WT, KC>(blk, row0, g.h, lane);
   // Tile rows 0-15: gate rows row0 ..; rows 16-31: the same up rows.
-  constexpr int N = WRegs<WT, 32>::N, RP = WGeo<WT>::kRowsPer;
+  constexpr int N = WRegs<WT, 32, KC>::N, RP = WGeo<WT, KC>::kRowsPer;
   const WT* wbase[N];
   const uint8_t* wsc[N];
   // MXFP4 block scales: gate [I][h/32], then up [I][h/32]
@@ -717,28 +749,29 @@ __global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     wbase[i] = G + (i < N / 2 ? 0 : g.off_up) + eoff<WT>((int64_t)(RP * (i % (N / 2))) * g.h);
-    wsc[i] = w_lane_scale<WT>(mxs + (i < N / 2 ? 0 : (int64_t)g.I * g.h / 32), row0, g.h, lane) +
+    wsc[i] = w_lane_scale<WT, KC>(mxs + (i < N / 2 ? 0 : (int64_t)g.I * g.h / 32), row0, g.h,
+                                  lane) +
              (int64_t)(RP * (i % (N / 2))) * (g.h / 32);
   }
   const float* sc = nullptr;
   if constexpr (std::is_same<WT, fp8w>::value) sc = wscales(blk, g.off_scale);
-  WTile<32>& wt = wts[wave];
+  WTile<WT, 32, KC>& wt = wts[wave];
   for (int m0 = 0; m0 < M; m0 += TOK) {
     const int mt = min(TOK, M - m0);
     const int p0 = pbeg + m0;
     if constexpr (TOK == 16) {
-      gu_pass<WT, LO, 1, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
+      gu_pass<WT, LO, 1, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
     } else if constexpr (TOK == 32) {
       if (mt <= 16)
-        gu_pass<WT, LO, 1, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
+        gu_pass<WT, LO, 1, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
       else
-        gu_pass<WT, LO, 2, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
+        gu_pass<WT, LO, 2, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
     } else {
       switch ((mt + 15) / 16) {
-        case 1: gu_pass<WT, LO, 1, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
-        case 2: gu_pass<WT, LO, 2, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
-        case 3: gu_pass<WT, LO, 3, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
-        default: gu_pass<WT, LO, 4, TOK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
+        case 1: gu_pass<WT, LO, 1, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
+        case 2: gu_pass<WT, LO, 2, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
+        case 3: gu_pass<WT, LO, 3, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
+        default: gu_pass<WT, LO, 4, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
       }
     }
   }
@@ -761,10 +794,10 @@ __device__ __forceinline__ int pair_exp(const unsigned* __restrict__ amax, int p
   }
 }
 
-template <typename WT, int NT, int TOK>
-__device__ __forceinline__ void dn_pass(TokTile<TOK>& xs, WTile<16>& wt,
-                                        const WT* const (&wbase)[WRegs<WT, 16>::N],
-                                        const uint8_t* const (&wsc)[WRegs<WT, 16>::N],
+template <typename WT, int NT, int TOK, int KC>
+__device__ __forceinline__ void dn_pass(TokTile<TOK, KC>& xs, WTile<WT, 16, KC>& wt,
+                                        const WT* const (&wbase)[WRegs<WT, 16, KC>::N],
+                                        const uint8_t* const (&wsc)[WRegs<WT, 16, KC>::N],
                                         const float* __restrict__ act,
                                         const unsigned* __restrict__ amax, int p0, int mt,
                                         int sb, int se, float* __restrict__ y, int row0,
@@ -781,19 +814,19 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK>& xs, WTile<16>& wt,
     ae[n] = tn < mt ? pair_exp<WT>(amax, p0 + tn) : 0;
   }
   if (sb < se) {
-    constexpr int TP = tile_pieces<TOK>();
+    constexpr int TP = tile_pieces<TOK, KC>();
     int64_t off[TP];
-    tile_rows(off, nullptr, p0, mt, g.I);
+    tile_rows<KC>(off, nullptr, p0, mt, g.I);
     int sx[TP];  // each staged piece's pair exponent
 #pragma unroll
     for (int q = 0; q < TP; ++q) {
-      const int n = ((int)threadIdx.x + kBlk * q) / kPieces;
+      const int n = ((int)threadIdx.x + kBlk * q) / (KC / 8);
       sx[q] = n < mt ? pair_exp<WT>(amax, p0 + n) : 0;
     }
-    WRegs<WT, 16> wr;
+    WRegs<WT, 16, KC> wr;
     ActRaw<TP> ar;
-    w_load<WT, 16>(wr, wbase, wsc, sb * kBK);
-    dn_tile_load(ar, act, off, sb * kBK);
+    w_load<WT, 16, KC>(wr, wbase, wsc, sb * KC);
+    dn_tile_load(ar, act, off, sb * KC);
     for (int s = sb; s < se; ++s) {
       __syncthreads();
       {
@@ -801,18 +834,18 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK>& xs, WTile<16>& wt,
         dn_tile_split<bf16_ops<WT>()>(th, tl, ar, sx);
         tile_store(xs, th, tl, true);
       }
-      w_store<WT, 16>(wt, wr, lane);
+      w_store<WT, 16, KC>(wt, wr, lane);
       __syncthreads();
       if (s + 1 < se) {
-        w_load<WT, 16>(wr, wbase, wsc, (s + 1) * kBK);
-        dn_tile_load(ar, act, off, (s + 1) * kBK);
+        w_load<WT, 16, KC>(wr, wbase, wsc, (s + 1) * KC);
+        dn_tile_load(ar, act, off, (s + 1) * KC);
       }
       if constexpr (std::is_same<WT, fp4x2>::value)
         __builtin_amdgcn_sched_barrier(0);  // loads ahead of the MFMAs, as in gu_pass
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < KC / 32; ++j) {
         const int c = 4 * j + (lane >> 4);
-        const H8 da = wt.w[lane & 15][c];
+        const H8 da = a_frag(wt, lane & 15, j, lane >> 4);
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
           const int tn = n * 16 + (lane & 15);
@@ -845,13 +878,13 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK>& xs, WTile<16>& wt,
   }
 }
 
-template <typename WT, int TOK>
+template <typename WT, int TOK, int KC>
 __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, BatchRoute r,
                                                   const float* __restrict__ act,
                                                   const unsigned* __restrict__ amax,
                                                   float* __restrict__ ypart, Geom g, int P) {
-  __shared__ TokTile<TOK> xs;
-  __shared__ WTile<16> wts[kBlk / kWave];
+  __shared__ TokTile<TOK, KC> xs;
+  __shared__ WTile<WT, 16, KC> wts[kBlk / kWave];
   const int slot = blockIdx.z;
   if (slot >= *r.n_active) return;
   const int e = r.active[slot];
@@ -860,14 +893,14 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, B
   const int wave = threadIdx.x / kWave;
   const int row0 = blockIdx.x * kBM + wave * 16;
   const int ks = blockIdx.y;
-  const int nsteps = g.I / kBK;
+  const int nsteps = g.I / KC;
   const int sb = nsteps * ks / BatchWs::kKSplit;
   const int se = nsteps * (ks + 1) / BatchWs::kKSplit;
   const WT* blk = wbuf + (int64_t)e * g.stride;
-  const WT* D = w_lane_base(blk + g.off_down, row0, g.I, lane);
+  const WT* D = w_lane_base<WT, KC>(blk + g.off_down, row0, g.I, lane);
   const float* sdown = nullptr;  // fp8: s_down[h] follows the I gate and I up scales
   if constexpr (std::is_same<WT, fp8w>::value) sdown = wscales(blk, g.off_scale) + 2 * g.I;
-  constexpr int N = WRegs<WT, 16>::N;
+  constexpr int N = WRegs<WT, 16, KC>::N;
   const WT* wbase[N];
   const uint8_t* wsc[N];
   // MXFP4 down block scales [h][I/32], after the gate and up scales
@@ -875,27 +908,27 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, B
       reinterpret_cast<const uint8_t*>(blk) + g.off_scale + 2 * ((int64_t)g.I * g.h / 32);
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    wbase[i] = D + eoff<WT>((int64_t)(WGeo<WT>::kRowsPer * i) * g.I);
-    wsc[i] = w_lane_scale<WT>(mxs, row0, g.I, lane) +
-             (int64_t)(WGeo<WT>::kRowsPer * i) * (g.I / 32);
+    wbase[i] = D + eoff<WT>((int64_t)(WGeo<WT, KC>::kRowsPer * i) * g.I);
+    wsc[i] = w_lane_scale<WT, KC>(mxs, row0, g.I, lane) +
+             (int64_t)(WGeo<WT, KC>::kRowsPer * i) * (g.I / 32);
   }
   float* y = ypart + (int64_t)ks * P * g.h;
-  WTile<16>& wt = wts[wave];
+  WTile<WT, 16, KC>& wt = wts[wave];
   for (int m0 = 0; m0 < M; m0 += TOK) {
     const int mt = min(TOK, M - m0);
     if constexpr (TOK == 16) {
-      dn_pass<WT, 1, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+      dn_pass<WT, 1, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
     } else if constexpr (TOK == 32) {
       if (mt <= 16)
-        dn_pass<WT, 1, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+        dn_pass<WT, 1, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
       else
-        dn_pass<WT, 2, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+        dn_pass<WT, 2, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
     } else {
       switch ((mt + 15) / 16) {
-        case 1: dn_pass<WT, 1, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-        case 2: dn_pass<WT, 2, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-        case 3: dn_pass<WT, 3, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-        default: dn_pass<WT, 4, TOK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 1: dn_pass<WT, 1, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 2: dn_pass<WT, 2, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 3: dn_pass<WT, 3, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        default: dn_pass<WT, 4, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
       }
     }
   }
@@ -1279,25 +1312,37 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
   // An expert has at most B tokens (a token selects it at most once), so
   // small batches take token tiles of 16 or 32.
   if (p.B <= WR_SMALL_TILE_MAX_B) {
-    hipLaunchKernelGGL((k_gu_mfma<WT, LO, 16, true>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s,
-                       wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, w.logits,
-                       p.topk_ids, p.topk_w);
+    // 16-token tiles: 256-byte K steps where the K dimension (h for gate/up,
+    // I for down) is a multiple of them.
+    constexpr int KW = kc_wide<WT>();
+    if (p.h % KW == 0)
+      hipLaunchKernelGGL((k_gu_mfma<WT, LO, 16, true, KW>), dim3(p.I / kBM, slots), dim3(kBlk), 0,
+                         s, wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, w.logits,
+                         p.topk_ids, p.topk_w);
+    else
+      hipLaunchKernelGGL((k_gu_mfma<WT, LO, 16, true, kBK>), dim3(p.I / kBM, slots), dim3(kBlk), 0,
+                         s, wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, w.logits,
+                         p.topk_ids, p.topk_w);
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    hipLaunchKernelGGL((k_dn_mfma<WT, 16>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk),
-                       0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
+    if (p.I % KW == 0)
+      hipLaunchKernelGGL((k_dn_mfma<WT, 16, KW>), dim3(p.h / kBM, BatchWs::kKSplit, slots),
+                         dim3(kBlk), 0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
+    else
+      hipLaunchKernelGGL((k_dn_mfma<WT, 16, kBK>), dim3(p.h / kBM, BatchWs::kKSplit, slots),
+                         dim3(kBlk), 0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
   } else if (p.B <= WR_MID_TILE_MAX_B) {
-    hipLaunchKernelGGL((k_gu_mfma<WT, LO, 32, false>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s,
+    hipLaunchKernelGGL((k_gu_mfma<WT, LO, 32, false, kBK>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s,
                        wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, nullptr, nullptr,
                        nullptr);
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    hipLaunchKernelGGL((k_dn_mfma<WT, 32>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk),
+    hipLaunchKernelGGL((k_dn_mfma<WT, 32, kBK>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk),
                        0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
   } else {
-    hipLaunchKernelGGL((k_gu_mfma<WT, LO, kMaxTok, false>), dim3(p.I / kBM, slots), dim3(kBlk),
+    hipLaunchKernelGGL((k_gu_mfma<WT, LO, kMaxTok, false, kBK>), dim3(p.I / kBM, slots), dim3(kBlk),
                        0, s, wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, nullptr,
                        nullptr, nullptr);
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    hipLaunchKernelGGL((k_dn_mfma<WT, kMaxTok>), dim3(p.h / kBM, BatchWs::kKSplit, slots),
+    hipLaunchKernelGGL((k_dn_mfma<WT, kMaxTok, kBK>), dim3(p.h / kBM, BatchWs::kKSplit, slots),
                        dim3(kBlk), 0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
   }
   if ((err = hipGetLastError()) != hipSuccess) return err;
