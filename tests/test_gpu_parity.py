@@ -291,9 +291,12 @@ GROUPED = [(8, 256, 512, 2, False), (16, 512, 1024, 2, True), (64, 256, 512, 6, 
                          ids=lambda c: f"E{c[0]}-h{c[1]}-I{c[2]}-k{c[3]}" + ("-renorm" if c[4] else ""))
 def test_grouped_batched_parity(cuda, cfg, B, x_dtype, wd):
     """The grouped MFMA batched path (fp16, fp8, bf16 or MXFP4 weights, h and
-    I multiples of 128; fp32 weights with exact fp32 MFMA products; fp8 codes
-    are staged as fp16 and scaled in the epilogue, MXFP4 codes staged as bf16
-    times their block scale;
+    I multiples of 128; fp32 weights with exact fp32 MFMA products; fp8 and
+    MXFP4 codes are staged raw and decoded per MFMA fragment, fp8 to fp16
+    (row scales in the epilogue), MXFP4 to bf16 times its block scale; with
+    16-token tiles (B <= 16) gate/up and down each take 256-byte K steps when
+    h, respectively I, is a multiple of them: the shapes here give fp8 and
+    MXFP4 both widths on both kernels;
     bf16 and MXFP4 weights take x and act as two bf16 terms, within 2^-18 of
     them, so their rows are compared with the single-token op at 5e-5 of
     max|out| instead of 1e-5).
