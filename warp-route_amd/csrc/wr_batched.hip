@@ -20,8 +20,9 @@
 //      the same 16 up rows each, all of the expert's tokens (up to 64 per
 //      pass); the token tile is staged in LDS and shared by the 4 waves.
 //      v_mfma_f32_16x16x32_f16 with A = weight rows (fp16, or fp8 E4M3 codes
-//      converted exactly to fp16 while staging) and B = the hi and lo terms
-//      of x; products are exact and accumulate in fp32, and the epilogue
+//      staged as they are and converted exactly to fp16 per fragment) and
+//      B = the hi and lo terms of x; products are exact and accumulate in
+//      fp32, and the epilogue
 //      multiplies by 2^-e_b.  bf16 and MXFP4 weights (E2M1 codes times their
 //      E8M0 block scale are exact in bf16 at every scale) use
 //      v_mfma_f32_16x16x32_bf16 with x in two bf16 terms instead
@@ -72,7 +73,7 @@ typedef f16x8 H8;  // eight 16-bit operands: fp16, or bf16 bit patterns
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // MFMA operand type of a weight type: bf16 for bf16 and MXFP4 weights, fp16
-// otherwise (fp8 codes are staged as fp16).
+// otherwise (fp8 codes are decoded to fp16).
 template <typename WT>
 constexpr bool bf16_ops() {
   return std::is_same<WT, bf16w>::value || std::is_same<WT, fp4x2>::value;
