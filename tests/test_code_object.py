@@ -240,3 +240,18 @@ def test_register_path_kernels_hold_no_per_thread_arrays_in_lds(kernels):
     assert len(reg) >= 16, sorted(reg)
     big = {k: n for k, n in reg.items() if n > limit(k)}
     assert not big, f"register-path kernels with more LDS than their buffers: {big}"
+
+
+def test_x_in_lds_kernels_fit_four_blocks_per_cu(kernels):
+    # The x-in-LDS single-token kernels (k_fused_ffn<..., true, STG>) size their
+    # buffer for 4 blocks of 4 waves per CU: at most 40 KB of the CU's 160 KB
+    # each.  The MXFP4 staged-scale kernels fill that budget (their down
+    # blocks stage one more weight chunk per wave in the x copy's bytes).
+    xl = {k: v.get("group_segment_fixed_size", 0) for k, v in kernels.items()
+          if "k_fused_ffn" in k and re.search(r"ELb1ELb[01]EEEv", k)}
+    assert len(xl) >= 8, sorted(xl)
+    assert all(n > 0 for n in xl.values()), xl
+    big = {k: n for k, n in xl.items() if n > 40 * 1024}
+    assert not big, f"x-in-LDS kernels over 40 KB of LDS: {big}"
+    stg = [n for k, n in xl.items() if re.search(r"ELb1ELb1EEEv", k)]
+    assert stg and min(stg) > 36 * 1024, f"staged-scale kernels without their chunk buffer: {stg}"

@@ -112,6 +112,13 @@
 #ifndef WR_F4_STG_MIN_I
 #define WR_F4_STG_MIN_I 4096
 #endif
+// LDS buffer of the MXFP4 staged-scale kernel, in bytes: the gate/up role's x
+// copy and scale bytes, or the down role's scale copy followed by one 8-row
+// chunk per wave staged before the hand-off wait.  39 KB keeps 4 blocks per
+// CU (160 KB) with the kernel's other shared words.
+#ifndef WR_F4_STG_RAW
+#define WR_F4_STG_RAW 39936
+#endif
 
 namespace wr {
 
@@ -952,8 +959,13 @@ constexpr size_t stg_gu_bytes() {
 // Bytes of the kernel-wide LDS buffer of k_fused_ffn.
 template <typename WT, typename XT, int VEC, int RPW, bool XL, bool STG>
 constexpr size_t fused_raw_bytes() {
-  if constexpr (XL) return XlLayout<XT, VEC>::bytes(xl_max_h<WT>()) + stg_gu_bytes<WT, RPW, STG>();
-  else return 16;
+  if constexpr (XL) {
+    constexpr size_t gu = XlLayout<XT, VEC>::bytes(xl_max_h<WT>()) + stg_gu_bytes<WT, RPW, STG>();
+    static_assert(!STG || gu <= WR_F4_STG_RAW, "the staged-scale buffer holds the gate/up copy");
+    return STG ? (size_t)WR_F4_STG_RAW : gu;
+  } else {
+    return 16;
+  }
 }
 
 template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2, bool XL,
@@ -1074,6 +1086,34 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
       }
     }
   }
+  // STG: the down role does not use the x copy's bytes of lds_raw, so after
+  // the scale copy they hold one more 8-row chunk for each wave there is room
+  // for (spre = 1): chunk wave + 4 U2, codes only, staged the same way.
+  int spre = 0;
+  const unsigned char* sp = lds_raw;
+  if constexpr (STG) {
+    constexpr int kChunk = RPD * kWave * 16;
+    const int sbytes = (g.k * RPD * (g.I / 32) + 255) & ~255;
+    const int npre = ((int)sizeof(lds_raw) - sbytes) / kChunk;
+    const int q = wu + kWavesPerBlock * U2;
+    if (wu < npre && q < C) {  // wave-uniform
+      spre = 1;
+      sp = lds_raw + sbytes + wu * kChunk;
+      const int kk = q / nch;
+      const int c = (q - kk * nch) * kWave * VEC + lane * VEC;
+      const WT* D = wbuf + (int64_t)topk_id(t, kk) * g.stride + g.off_down +
+                    eoff<WT>((int64_t)r0 * g.I + c);
+#pragma unroll
+      for (int j = 0; j < RPD; ++j) {
+        if (j < nrows && c < g.I)
+          __builtin_amdgcn_global_load_lds(
+              static_cast<const void*>(D + eoff<WT>((int64_t)j * g.I)),
+              (__attribute__((address_space(3))) void*)(lds_raw + sbytes + wu * kChunk +
+                                                        j * kWave * 16),
+              16, 0, 0);
+      }
+    }
+  }
   if constexpr (kFp8) {
     // Published to the block by the __syncthreads after the wait below.
     const int i = threadIdx.x, kk = i / RPD, j = i % RPD;
@@ -1144,7 +1184,24 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
       }
     }
   }
-  for (int q0 = wave + kWavesPerBlock * (U2 + PRE); q0 < C; q0 += kWavesPerBlock * U2) {
+  if constexpr (STG) {
+    // The staged chunk landed before the barrier after the wait (the wave
+    // waited for all of its loads there).
+    if (spre) {
+      const int q = wu + kWavesPerBlock * U2;
+      const int kk = q / nch;
+      const int c = (q - kk * nch) * kWave * VEC + lane * VEC;
+      V lw[1][RPD];
+#pragma unroll
+      for (int j = 0; j < RPD; ++j)
+        lw[0][j] = (j < nrows && c < g.I)
+                       ? V{*reinterpret_cast<const u32x4*>(sp + j * kWave * 16 + lane * 16), 127u}
+                       : vzero<V>();
+      down_tile_scales<WT, VEC, RPD, 1>(lw, lds_raw, g, nrows, q, nch, lane);
+      down_tile_fma<WT, V, VEC, RPD, 1>(acc, lw, act, g, act_row, q, nch, lane, sdn);
+    }
+  }
+  for (int q0 = wave + kWavesPerBlock * (U2 + PRE + spre); q0 < C; q0 += kWavesPerBlock * U2) {
     V wv[U2][RPD];
     down_tile_load<WT, VEC, RPD, U2, STG>(wv, wbuf, g, t, r0, nrows, q0, nch, lane);
     if constexpr (STG) down_tile_scales<WT, VEC, RPD, U2>(wv, lds_raw, g, nrows, q0, nch, lane);
