@@ -170,6 +170,12 @@ typedef struct wr_fused_opts {
                            nonzero value makes every wait expire after
                            spin_limit polls, so that tests can exercise the
                            expiry path while every kernel still exits normally */
+  uint32_t gu_blocks;   /* gate/up blocks to launch, rounded down to a multiple
+                           of 32; 0 = the default (as many as the GPU holds at
+                           once, the remaining gate/up chunks taken by the
+                           blocks that finish first).  Fewer blocks than the
+                           layer's chunks exercise that path at small shapes
+                           (tests)                                            */
 } wr_fused_opts;
 
 /* Human-readable name of a status code (never NULL). */

@@ -56,6 +56,9 @@ def test_struct_layout_matches_header_order():
     assert capi.WrMoeArgs.x.offset == 56
     assert ctypes.sizeof(capi.WrOffsets) == 32
     assert ctypes.sizeof(capi.WrLayoutInfo) == 48
+    # spin_limit, wait_extra, gu_blocks
+    assert ctypes.sizeof(capi.WrFusedOpts) == 12
+    assert capi.WrFusedOpts.gu_blocks.offset == 8
 
 
 FMT = {capi.WR_F32: "f32", capi.WR_F16: "f16", capi.WR_BF16: "bf16", capi.WR_FP8_E4M3: "fp8",
@@ -131,10 +134,11 @@ def test_layout_rejects_bad_arguments():
 def test_workspace_bytes():
     lib = capi.lib()
     # fused: control block (64 arrival counters, a timeout flag, an unused
-    # word and 64 XCD-rotation masks, one 256-byte line each) + 64 fp32 logits
-    # per token (E padded to 64) + act: single token k rows of I rounded up to
-    # 16 columns, B > 1 B*k*I; fp32, rounded up to 256 bytes.
-    ctrl = 130 * 256
+    # word, 64 XCD-rotation masks and 8 gate/up claim counters, one 256-byte
+    # line each) + 64 fp32 logits per token (E padded to 64) + act: single
+    # token k rows of I rounded up to 16 columns, B > 1 B*k*I; fp32, rounded up
+    # to 256 bytes.
+    ctrl = 138 * 256
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 4096, 14336, 2, 1) == (
         ctrl + 256 + 2 * 14336 * 4)
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 64, 100, 3, 1) == (
@@ -262,8 +266,8 @@ def test_noalloc_validates_before_hip():
 def test_fused_status_checks_its_workspace_before_hip():
     lib = capi.lib()
     assert lib.wr_fused_moe_status(None, 1 << 20, None) == capi.WR_EINVAL_NULL
-    # smaller than the control block (130 lines of 256 bytes)
-    assert lib.wr_fused_moe_status(FAKE, 130 * 256 - 1, None) == capi.WR_EINVAL_WORKSPACE
+    # smaller than the control block (138 lines of 256 bytes)
+    assert lib.wr_fused_moe_status(FAKE, 138 * 256 - 1, None) == capi.WR_EINVAL_WORKSPACE
     assert "NaN" in capi.status_str(capi.WR_ETIMEOUT)
 
 

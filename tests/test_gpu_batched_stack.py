@@ -296,3 +296,69 @@ def test_fused_handoff_expiry_is_reported(cuda, shape):
     assert torch.equal(again, want)
     del buf
     torch.cuda.empty_cache()
+
+
+# Byte offset of the single-token workspace's 8 claim counters (one 256-byte
+# line each): after 64 arrival counters, the timeout word, one unused word
+# and 64 rotation masks.
+CLAIM_OFFSET = (2 * 64 + 2) * 256
+
+
+@pytest.mark.parametrize("shape,gu", [((8, 512, 8192, 2, F16), 64), ((8, 512, 8192, 2, F16), 992),
+                                      ((8, 256, 2048, 2, F32), 32),
+                                      ((8, 512, 8192, 2, BF16), 256),
+                                      ((64, 2048, 1408, 6, F16), 0),
+                                      ((64, 2048, 1408, 6, BF16), 0)],
+                         ids=["f16-64", "f16-992", "f32-32", "bf16-256", "deepseek-f16",
+                              "deepseek-bf16"])
+def test_fused_claimed_gateup_slots(cuda, shape, gu):
+    """Fewer gate/up blocks launched than the layer has chunk slots: the
+    blocks claim the remaining slots as they finish (one claim counter per
+    class of 8 blocks).  Forced with wr_fused_opts.gu_blocks at shapes that
+    take the register path (1,024 slots over 64, 992 or 256 blocks, 256 over
+    32), and the default at DeepSeek's shape (1,056 slots, one
+    round of 1,024 resident blocks on a 256-CU GPU).  The output must be
+    bit-identical to a call that launches every slot as a block (each act
+    value is computed by one wave either way), match the oracle, and the
+    claim counters must show n1 claims: every slot beyond the launched blocks
+    once, plus one unsuccessful claim per block."""
+    E, h, I, k, wd = shape
+    x, gw, buf = make_layer(E, h, I, wd, router_std=h ** -0.5, seed=4, device=cuda,
+                            gen_device=cuda)
+    nws = capi.lib().wr_workspace_bytes(capi.WR_KIND_FUSED, E, h, I, k, 1)
+    work = torch.empty(nws, dtype=torch.uint8, device=cuda)
+    out = torch.zeros_like(x)
+    stream = torch.cuda.current_stream().cuda_stream
+    a = _fused_args(x, gw, buf, E, h, I, k, out, work)
+    print(f"[gpu] claimed gate/up slots {shape} gu_blocks={gu}", flush=True)
+    st = capi.lib().wr_fused_moe_opts(ctypes.byref(a), ctypes.byref(capi.WrFusedOpts(gu_blocks=gu)),
+                                      ctypes.c_void_p(stream))
+    assert st == capi.WR_OK, capi.status_str(st)
+    st = capi.lib().wr_fused_moe_status(ctypes.c_void_p(work.data_ptr()), nws,
+                                        ctypes.c_void_p(stream))
+    assert st == capi.WR_OK, capi.status_str(st)
+    claims = int(work[CLAIM_OFFSET:CLAIM_OFFSET + 8 * 256].view(torch.int32)[::64].sum())
+    got = out.clone()
+
+    # every slot launched as a block of its own (gu_blocks above the slot count)
+    st = capi.lib().wr_fused_moe_opts(ctypes.byref(a),
+                                      ctypes.byref(capi.WrFusedOpts(gu_blocks=1 << 20)),
+                                      ctypes.c_void_p(stream))
+    assert st == capi.WR_OK, capi.status_str(st)
+    torch.cuda.synchronize()
+    assert int(work[CLAIM_OFFSET:CLAIM_OFFSET + 8 * 256].view(torch.int32)[::64].sum()) == 0
+    assert torch.equal(got, out), "claimed slots changed the output"
+    ref = oracle_token(x, gw, buf, E, h, I, k, False)
+    np.testing.assert_allclose(f64(got), ref["out"], rtol=1e-2, atol=1e-2)
+
+    # n1: chunk slots, k * ceil(ceil(I / rpw) / 4) rounded up to 8 * 32 / (4 rpw)
+    rpw = 2 if (h * buf.element_size() > 2048 and wd != FP8) else 4
+    group = 8 * (32 // (4 * rpw))
+    chunks = k * (-(-(-(-I // rpw)) // 4))
+    n1 = -(-chunks // group) * group
+    if gu > 0:
+        assert claims == n1, (claims, n1)
+    elif torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert claims == n1 == 1056, (claims, n1)
+    del buf
+    torch.cuda.empty_cache()

@@ -161,6 +161,7 @@ int validate(const wr_moe_args* a, int kind, Problem* p) {
   p->vec = kind < 0 ? 1 : choose_vec(a);
   p->spin_limit = wr::kDefaultSpinLimit;
   p->wait_extra = 0;
+  p->gu_blocks = 0;
   return WR_OK;
 }
 
@@ -289,6 +290,7 @@ WR_API int wr_fused_moe_opts(const wr_moe_args* args, const wr_fused_opts* opts,
   if (opts != nullptr) {
     if (opts->spin_limit != 0) p.spin_limit = opts->spin_limit;
     p.wait_extra = opts->wait_extra;
+    p.gu_blocks = (int)(opts->gu_blocks & 0x7fffffe0u);  // a multiple of 32, or 0
   }
   return hip_status(wr::launch_fused(p, static_cast<hipStream_t>(stream)));
 }

@@ -30,6 +30,10 @@ struct Problem {
   // count added to every arrival target (nonzero only to force the expiry
   // path from the host in tests: the wait then cannot complete).
   unsigned spin_limit, wait_extra;
+  // Single-token gate/up blocks launched: 0 = as many as are resident at once
+  // (the rest of the gate/up chunks are claimed by the blocks that finish
+  // first), else this many (tests).
+  int gu_blocks;
 };
 
 // Polls of the single-token hand-off wait before it expires (about 0.2 s).
@@ -41,15 +45,18 @@ constexpr size_t kWsAlign = 256;
 // Workspace carving.  Every region starts on a 256-byte boundary.
 struct FusedWs {
   // Single-token hand-off, one 256-byte line per word: kCounters arrival
-  // counters, the wait-timeout flag, an unused word, then kCounters XCD-
-  // rotation masks (gate/up block b ORs bit (its XCD - b) mod 8 into mask
-  // b mod kCounters).  The router kernel of each single-token call zeroes
-  // them.
+  // counters, the wait-timeout flag, an unused word, kCounters XCD-rotation
+  // masks (gate/up block b ORs bit (its XCD - b) mod 8 into mask
+  // b mod kCounters), then kClasses claim counters of the gate/up chunks
+  // beyond the launched blocks (class b mod 8).  The router kernel of each
+  // single-token call zeroes them.
   static constexpr int kCounters = 64;
+  static constexpr int kClasses = 8;
   static constexpr int kCounterStride = 64;  // words (256 bytes)
   static constexpr int kTimeoutWord = kCounters * kCounterStride;
   static constexpr int kRotWord = kTimeoutWord + 2 * kCounterStride;
-  static constexpr int kCtrlWords = 2 * kCounters + 2;  // zeroed words, kCounterStride apart
+  static constexpr int kClaimWord = kRotWord + kCounters * kCounterStride;
+  static constexpr int kCtrlWords = 2 * kCounters + 2 + kClasses;  // zeroed words, kCounterStride apart
   static constexpr size_t kCtrlBytes = (size_t)kCtrlWords * kCounterStride * 4;
   // Single-token act rows: I rounded up to whole chunks of `cols` columns, the
   // columns one gate/up block computes (4 waves x rows per wave: 8 or 16).

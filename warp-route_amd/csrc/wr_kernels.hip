@@ -26,10 +26,23 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
+#include <unordered_map>
 
 #include "wr_device.h"
 #include "wr_internal.h"
+
+// Single-token gate/up chunk slots beyond one round of resident blocks, up to
+// this percentage of the round, are claimed by the launched blocks instead of
+// being launched as blocks of their own.
+#ifndef WR_GU_CLAIM_PCT
+#define WR_GU_CLAIM_PCT 25
+#endif
+// Gate/up blocks per CU that make up that round: 0 = as many as are resident.
+#ifndef WR_GU_BLOCKS_PER_CU
+#define WR_GU_BLOCKS_PER_CU 0
+#endif
 
 #ifndef WR_GU_RPW
 #define WR_GU_RPW 2  // gate/up rows per matrix in flight per wave
@@ -579,7 +592,10 @@ struct Handoff {
   unsigned* cnt;        // FusedWs::kCounters counters, FusedWs::kCounterStride words apart
   unsigned* timeout;    // set to 1 if a wait expired (that block's rows are then NaN)
   unsigned* rot;        // FusedWs::kCounters rotation masks, FusedWs::kCounterStride words apart
-  int n1;               // gate/up blocks (the first n1 block ids), a multiple of 8 LB
+  unsigned* claim;      // FusedWs::kClasses claim counters, FusedWs::kCounterStride words apart
+  int n1;               // gate/up chunk slots, a multiple of 8 LB: one arrival each
+  int n1b;              // gate/up blocks launched (the first n1b block ids), a multiple of
+                        // 8 LB, at most n1; slots n1b .. n1 - 1 are claimed by them
   int chunks;           // k * bpk
   unsigned spin_limit;  // polls before a wait gives up
   unsigned wait_extra;  // added to every arrival target: 0, or (tests) a wait that cannot complete
@@ -969,7 +985,7 @@ constexpr size_t fused_raw_bytes() {
 }
 
 template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2, bool XL,
-          bool STG>
+          bool STG, bool CLAIM = false>
 __global__ __launch_bounds__(kBlock) void k_fused_ffn(
     const WT* __restrict__ wbuf, const XT* __restrict__ x, const float* __restrict__ logits,
     float* act, XT* __restrict__ out, int32_t* __restrict__ ids_out, float* __restrict__ w_out,
@@ -992,7 +1008,7 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   static_assert(!STG || XL, "scale staging lives in the x-in-LDS variant's buffer");
   __shared__ __align__(16) unsigned char lds_raw[fused_raw_bytes<WT, XT, VEC, RPW, XL, STG>()];
 
-  if ((int)blockIdx.x < hs.n1) {
+  if ((int)blockIdx.x < hs.n1b) {
     // ---- gate/up block ----
     if (blockIdx.x == 0 && wave == 0) {
 #pragma unroll
@@ -1005,32 +1021,55 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
     }
     const int items = (g.I + RPW - 1) / RPW;
     const int bpk = (items + kWavesPerBlock - 1) / kWavesPerBlock;  // chunks per expert
-    const int G = chunk_of_block<LB>(blockIdx.x);
-    if constexpr (XL) {
-      // Wave-uniform by construction; readfirstlane keeps them in SGPRs (the
-      // TopK reads below take a scalar slot index).
-      const int kk = __builtin_amdgcn_readfirstlane(G < hs.chunks ? G / bpk : 0);
-      const int it = (G - kk * bpk) * kWavesPerBlock + wave;
-      const int nrows = (G < hs.chunks && it < items) ? min(RPW, g.I - it * RPW) : 0;
-      gateup_item_xl<WT, XT, VEC, RPW, U1, STG>(wbuf, x, act + kk * act_row + it * RPW, g,
-                                                topk_id(t, kk), topk_w(t, kk),
-                                                nrows > 0 ? it * RPW : 0, nrows, lane, lds_raw);
-    } else if (G < hs.chunks) {
-      const int kk = G / bpk;
-      const int it = (G - kk * bpk) * kWavesPerBlock + wave;
-      if (it < items)
-        gateup_item<WT, XT, VEC, RPW, U1>(wbuf, x, act + kk * act_row + it * RPW, g, t, kk,
-                                          it * RPW, lane);
+    // Slot v = this block's id; with CLAIM (fewer blocks launched than slots)
+    // then slots n1b + c + 8 i of this block's class c = id mod 8, claimed one
+    // at a time until none is left.  A claimed slot's act line is then written
+    // only by blocks of one class, as a launched slot's is.  The claiming loop
+    // is a separate instantiation: it changes the register allocation of the
+    // gate/up role.
+    __shared__ int s_claim;
+    const int cls = (int)blockIdx.x % FusedWs::kClasses;
+    for (int v = blockIdx.x;;) {
+      const int G = chunk_of_block<LB>(v);
+      if constexpr (XL) {
+        // Wave-uniform by construction; readfirstlane keeps them in SGPRs (the
+        // TopK reads below take a scalar slot index).
+        const int kk = __builtin_amdgcn_readfirstlane(G < hs.chunks ? G / bpk : 0);
+        const int it = (G - kk * bpk) * kWavesPerBlock + wave;
+        const int nrows = (G < hs.chunks && it < items) ? min(RPW, g.I - it * RPW) : 0;
+        gateup_item_xl<WT, XT, VEC, RPW, U1, STG>(wbuf, x, act + kk * act_row + it * RPW, g,
+                                                  topk_id(t, kk), topk_w(t, kk),
+                                                  nrows > 0 ? it * RPW : 0, nrows, lane, lds_raw);
+      } else if (G < hs.chunks) {
+        const int kk = G / bpk;
+        const int it = (G - kk * bpk) * kWavesPerBlock + wave;
+        if (it < items)
+          gateup_item<WT, XT, VEC, RPW, U1>(wbuf, x, act + kk * act_row + it * RPW, g, t, kk,
+                                            it * RPW, lane);
+      }
+      if (threadIdx.x == 0 && v == (int)blockIdx.x)
+        __hip_atomic_fetch_or(hs.rot + (blockIdx.x % FusedWs::kCounters) * FusedWs::kCounterStride,
+                              1u << ((xcc_id() - blockIdx.x) & 7u), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's act stores have completed
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        __hip_atomic_fetch_add(hs.cnt + (v % FusedWs::kCounters) * FusedWs::kCounterStride, 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (CLAIM)
+          s_claim = hs.n1b + cls +
+                    FusedWs::kClasses *
+                        (int)__hip_atomic_fetch_add(hs.claim + cls * FusedWs::kCounterStride, 1u,
+                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if constexpr (!CLAIM) {
+        break;
+      } else {
+        __syncthreads();
+        v = s_claim;  // rewritten only after the next pass's barrier above
+        if (v >= hs.n1) break;
+      }
     }
-    if (threadIdx.x == 0)
-      __hip_atomic_fetch_or(hs.rot + (blockIdx.x % FusedWs::kCounters) * FusedWs::kCounterStride,
-                            1u << ((xcc_id() - blockIdx.x) & 7u), __ATOMIC_RELAXED,
-                            __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's act stores have completed
-    __syncthreads();
-    if (threadIdx.x == 0)
-      __hip_atomic_fetch_add(hs.cnt + (blockIdx.x % FusedWs::kCounters) * FusedWs::kCounterStride,
-                             1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
 
@@ -1039,7 +1078,7 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   __shared__ float part[kWavesPerBlock][RPD];
   __shared__ float sdn[kFp8 ? WR_MAX_TOPK * RPD : 1];  // fp8 row scales [kk][j]
   __shared__ int expired;  // this block's wait gave up
-  const int r0 = ((int)blockIdx.x - hs.n1) * RPD;
+  const int r0 = ((int)blockIdx.x - hs.n1b) * RPD;
   const int nrows = min(RPD, g.h - r0);
   const int nch = (g.I + kWave * VEC - 1) / (kWave * VEC);
   const int C = g.k * nch;
@@ -1314,6 +1353,36 @@ int fused_n1(int I, int k, int rpw) {
   return (fused_chunks(I, k, rpw) + group - 1) / group * group;
 }
 
+// Blocks of `kernel` resident per CU (occupancy query, cached per kernel).
+int blocks_per_cu(const void* kernel) {
+  static std::mutex mu;
+  static std::unordered_map<const void*, int> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(kernel);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kBlock, 0) != hipSuccess || n < 0)
+    n = 0;
+  cache.emplace(kernel, n);
+  return n;
+}
+
+// Gate/up blocks to launch for n1 chunk slots (a multiple of 32): all of
+// them, unless they overflow one round of resident blocks by at most
+// WR_GU_CLAIM_PCT percent of it.  Then one round (rounded down to a multiple
+// of 32) is launched and its blocks claim the remaining slots as they finish:
+// the overflow runs on the first blocks to end, instead of as a second round
+// of blocks that starts after them (DeepSeek: 1,056 slots for 1,024 resident
+// blocks, the last 32 ending about 7 us after the others).
+int gu_launch_blocks(const Problem& p, int n1, const void* kernel) {
+  if (p.gu_blocks > 0) return std::min(n1, p.gu_blocks);
+  const int bpc = WR_GU_BLOCKS_PER_CU > 0 ? WR_GU_BLOCKS_PER_CU : blocks_per_cu(kernel);
+  const int slots = bpc * cu_count() / 32 * 32;
+  if (slots >= 32 && n1 > slots && (int64_t)(n1 - slots) * 100 <= (int64_t)slots * WR_GU_CLAIM_PCT)
+    return slots;
+  return n1;
+}
+
 template <typename WT, typename XT, int VEC, int RPW, int U1>
 hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   const Geom g = make_geom(p);
@@ -1321,7 +1390,9 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
   hs.cnt = w.ctrl;
   hs.timeout = w.ctrl + FusedWs::kTimeoutWord;
   hs.rot = w.ctrl + FusedWs::kRotWord;
+  hs.claim = w.ctrl + FusedWs::kClaimWord;
   hs.n1 = fused_n1(p.I, p.k, RPW);
+  hs.n1b = hs.n1;
   hs.chunks = fused_chunks(p.I, p.k, RPW);
   hs.spin_limit = p.spin_limit;
   hs.wait_extra = p.wait_extra;
@@ -1359,6 +1430,21 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
       }
       hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, false>),
                          dim3(hs.n1 + n2), dim3(kBlock), 0, s,
+                         static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x), w.logits,
+                         w.act, static_cast<XT*>(p.out), p.topk_ids, p.topk_w, g, hs);
+      return hipGetLastError();
+    }
+  }
+  // Register path: gate/up chunk slots that overflow one round of resident
+  // blocks by a little are claimed by the launched blocks (CLAIM variant;
+  // 16-bit and fp32 weights, whose small layers such as DeepSeek's take this
+  // path; fp8 and MXFP4 layers of that size stage x in LDS).
+  if constexpr (VEC > 1 && (sizeof(WT) == 2 || std::is_same<WT, float>::value)) {
+    auto kc = k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, false, false, true>;
+    const int n1b = gu_launch_blocks(p, hs.n1, reinterpret_cast<const void*>(kc));
+    if (n1b < hs.n1) {
+      hs.n1b = n1b;
+      hipLaunchKernelGGL(kc, dim3(hs.n1b + n2), dim3(kBlock), 0, s,
                          static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x), w.logits,
                          w.act, static_cast<XT*>(p.out), p.topk_ids, p.topk_w, g, hs);
       return hipGetLastError();

@@ -57,7 +57,8 @@ class WrLayoutInfo(ctypes.Structure):
 
 
 class WrFusedOpts(ctypes.Structure):
-    _fields_ = [("spin_limit", ctypes.c_uint32), ("wait_extra", ctypes.c_uint32)]
+    _fields_ = [("spin_limit", ctypes.c_uint32), ("wait_extra", ctypes.c_uint32),
+                ("gu_blocks", ctypes.c_uint32)]
 
 
 class WrMoeArgs(ctypes.Structure):
