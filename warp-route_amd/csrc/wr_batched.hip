@@ -35,7 +35,9 @@
 //      the down rows against act, split into two terms while staging (fp16
 //      terms of act 2^e_p, e_p from the pair's maximum, undone in the
 //      epilogue), four K slices so that the grid has enough blocks; partial
-//      sums per slice.
+//      sums per slice.  With 64-token tiles (and 32-token tiles of 8- and
+//      4-bit weights) k_act_split makes the two terms once, in place, between
+//      steps 3 and 4, instead of every row tile's blocks making them again.
 //   5. k_combine: out[t] = sum over t's experts (selection order) and K
 //      slices (ascending) of the partials, in that fixed order.
 // Every sum has a fixed order, so results are deterministic.  The MFMA work
@@ -419,6 +421,24 @@ __device__ __forceinline__ void dn_tile_split(H8 (&hi)[TP], H8 (&lo)[TP], const 
   }
 }
 
+// Down with act split ahead of the kernel (k_act_split): each piece of 8
+// values holds, in place of their 32 fp32 bytes, their 8 hi terms then their
+// 8 lo terms.
+template <int TP>
+__device__ __forceinline__ void dn_tile_load_split(H8 (&hi)[TP], H8 (&lo)[TP],
+                                                   const float* __restrict__ act,
+                                                   const int64_t (&off)[TP], int kb) {
+#pragma unroll
+  for (int q = 0; q < TP; ++q) {
+    hi[q] = lo[q] = h8zero();
+    if (off[q] >= 0) {
+      const H8* a = reinterpret_cast<const H8*>(act + off[q] + kb);
+      hi[q] = a[0];
+      lo[q] = a[1];
+    }
+  }
+}
+
 template <int TOK, int KC, int TP>
 __device__ __forceinline__ void tile_store(TokTile<TOK, KC>& xs, const H8 (&hi)[TP],
                                            const H8 (&lo)[TP], bool with_lo) {
@@ -795,7 +815,7 @@ __device__ __forceinline__ int pair_exp(const unsigned* __restrict__ amax, int p
   }
 }
 
-template <typename WT, int NT, int TOK, int KC>
+template <typename WT, int NT, int TOK, int KC, bool PRE>
 __device__ __forceinline__ void dn_pass(TokTile<TOK, KC>& xs, WTile<WT, 16, KC>& wt,
                                         const WT* const (&wbase)[WRegs<WT, 16, KC>::N],
                                         const uint8_t* const (&wsc)[WRegs<WT, 16, KC>::N],
@@ -818,19 +838,25 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK, KC>& xs, WTile<WT, 16, KC>&
     constexpr int TP = tile_pieces<TOK, KC>();
     int64_t off[TP];
     tile_rows<KC>(off, nullptr, p0, mt, g.I);
-    int sx[TP];  // each staged piece's pair exponent
+    int sx[TP];  // each staged piece's pair exponent (act split here)
 #pragma unroll
     for (int q = 0; q < TP; ++q) {
       const int n = ((int)threadIdx.x + kBlk * q) / (KC / 8);
-      sx[q] = n < mt ? pair_exp<WT>(amax, p0 + n) : 0;
+      sx[q] = (!PRE && n < mt) ? pair_exp<WT>(amax, p0 + n) : 0;
     }
     WRegs<WT, 16, KC> wr;
-    ActRaw<TP> ar;
+    ActRaw<PRE ? 1 : TP> ar;  // act split here: raw pieces
+    H8 ph[TP], pl[TP];        // act split ahead: the two terms
     w_load<WT, 16, KC>(wr, wbase, wsc, sb * KC);
-    dn_tile_load(ar, act, off, sb * KC);
+    if constexpr (PRE)
+      dn_tile_load_split(ph, pl, act, off, sb * KC);
+    else
+      dn_tile_load(ar, act, off, sb * KC);
     for (int s = sb; s < se; ++s) {
       __syncthreads();
-      {
+      if constexpr (PRE) {
+        tile_store(xs, ph, pl, true);
+      } else {
         H8 th[TP], tl[TP];
         dn_tile_split<bf16_ops<WT>()>(th, tl, ar, sx);
         tile_store(xs, th, tl, true);
@@ -839,7 +865,10 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK, KC>& xs, WTile<WT, 16, KC>&
       __syncthreads();
       if (s + 1 < se) {
         w_load<WT, 16, KC>(wr, wbase, wsc, (s + 1) * KC);
-        dn_tile_load(ar, act, off, (s + 1) * KC);
+        if constexpr (PRE)
+          dn_tile_load_split(ph, pl, act, off, (s + 1) * KC);
+        else
+          dn_tile_load(ar, act, off, (s + 1) * KC);
       }
       if constexpr (std::is_same<WT, fp4x2>::value)
         __builtin_amdgcn_sched_barrier(0);  // loads ahead of the MFMAs, as in gu_pass
@@ -879,7 +908,8 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK, KC>& xs, WTile<WT, 16, KC>&
   }
 }
 
-template <typename WT, int TOK, int KC>
+// PRE: act was split into its two terms by k_act_split.
+template <typename WT, int TOK, int KC, bool PRE = false>
 __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, BatchRoute r,
                                                   const float* __restrict__ act,
                                                   const unsigned* __restrict__ amax,
@@ -918,20 +948,49 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, B
   for (int m0 = 0; m0 < M; m0 += TOK) {
     const int mt = min(TOK, M - m0);
     if constexpr (TOK == 16) {
-      dn_pass<WT, 1, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+      dn_pass<WT, 1, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
     } else if constexpr (TOK == 32) {
       if (mt <= 16)
-        dn_pass<WT, 1, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+        dn_pass<WT, 1, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
       else
-        dn_pass<WT, 2, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+        dn_pass<WT, 2, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
     } else {
       switch ((mt + 15) / 16) {
-        case 1: dn_pass<WT, 1, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-        case 2: dn_pass<WT, 2, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-        case 3: dn_pass<WT, 3, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-        default: dn_pass<WT, 4, TOK, KC>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 1: dn_pass<WT, 1, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 2: dn_pass<WT, 2, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 3: dn_pass<WT, 3, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        default: dn_pass<WT, 4, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
       }
     }
+  }
+}
+
+// act [P][I] (fp32, I a multiple of 8) split into its two 16-bit terms once,
+// in place: each piece of 8 values becomes their 8 hi terms followed by their
+// 8 lo terms (bf16 terms with BF, else fp16 terms of act 2^e_p with the
+// pair's exponent), the same terms k_dn_mfma's staging makes.  For 32- and
+// 64-token tiles, where every 64-row tile's blocks would otherwise split the
+// same values again (the down kernel's VALU work was about 2.3 times its
+// gate/up kernel's at B = 64).
+template <bool BF>
+__global__ __launch_bounds__(kBlk) void k_act_split(float* __restrict__ act,
+                                                    const unsigned* __restrict__ amax, int P,
+                                                    int I) {
+  const int pp = I / 8;  // pieces per pair
+  const int64_t n = (int64_t)P * pp;
+  for (int64_t i = (int64_t)blockIdx.x * kBlk + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kBlk) {
+    const int p = (int)(i / pp);
+    float* a = act + i * 8;
+    ActRaw<1> t;
+    t.v[0][0] = *reinterpret_cast<const f32x4*>(a);
+    t.v[0][1] = *reinterpret_cast<const f32x4*>(a + 4);
+    const int sx[1] = {
+        BF ? 0 : split_exp(__uint_as_float(amax[(int64_t)p * BatchWs::kAmaxStride]), false)};
+    H8 hi[1], lo[1];
+    dn_tile_split<BF>(hi, lo, t, sx);
+    reinterpret_cast<H8*>(a)[0] = hi[0];
+    reinterpret_cast<H8*>(a)[1] = lo[0];
   }
 }
 
@@ -1331,20 +1390,38 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
     else
       hipLaunchKernelGGL((k_dn_mfma<WT, 16, kBK>), dim3(p.h / kBM, BatchWs::kKSplit, slots),
                          dim3(kBlk), 0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
-  } else if (p.B <= WR_MID_TILE_MAX_B) {
-    hipLaunchKernelGGL((k_gu_mfma<WT, LO, 32, false, kBK>), dim3(p.I / kBM, slots), dim3(kBlk), 0, s,
-                       wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, nullptr, nullptr,
-                       nullptr);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
-    hipLaunchKernelGGL((k_dn_mfma<WT, 32, kBK>), dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk),
-                       0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
   } else {
-    hipLaunchKernelGGL((k_gu_mfma<WT, LO, kMaxTok, false, kBK>), dim3(p.I / kBM, slots), dim3(kBlk),
-                       0, s, wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, nullptr,
-                       nullptr, nullptr);
+    // 64-token tiles, and 32-token tiles of 8- and 4-bit weights: act split
+    // once between the two GEMMs (k_act_split).  Measured, per call: B = 64
+    // fp16 281 -> 275 us, fp8 226 -> 213 us, MXFP4 218 -> 215 us, bf16
+    // unchanged; B = 32 fp8 125 -> 123 us, MXFP4 124 -> 122 us, but fp16 164 ->
+    // 168 us and bf16 161 -> 165 us (the launch costs more than the repeated
+    // splits of 32-token tiles).
+    constexpr bool kPre32 = wbits<WT>() < 16;
+    const bool mid = p.B <= WR_MID_TILE_MAX_B;
+    if (mid)
+      hipLaunchKernelGGL((k_gu_mfma<WT, LO, 32, false, kBK>), dim3(p.I / kBM, slots), dim3(kBlk),
+                         0, s, wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, nullptr,
+                         nullptr, nullptr);
+    else
+      hipLaunchKernelGGL((k_gu_mfma<WT, LO, kMaxTok, false, kBK>), dim3(p.I / kBM, slots),
+                         dim3(kBlk), 0, s, wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g,
+                         nullptr, nullptr, nullptr);
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    hipLaunchKernelGGL((k_dn_mfma<WT, kMaxTok, kBK>), dim3(p.h / kBM, BatchWs::kKSplit, slots),
-                       dim3(kBlk), 0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
+    if (!mid || kPre32) {
+      const int64_t pieces = (int64_t)P * (p.I / 8);
+      const int split_blocks = (int)std::min<int64_t>((pieces + kBlk - 1) / kBlk, 4096);
+      hipLaunchKernelGGL((k_act_split<bf16_ops<WT>()>), dim3(split_blocks), dim3(kBlk), 0, s,
+                         w.act, w.amax, P, p.I);
+      if ((err = hipGetLastError()) != hipSuccess) return err;
+    }
+    if (mid)
+      hipLaunchKernelGGL((k_dn_mfma<WT, 32, kBK, kPre32>), dim3(p.h / kBM, BatchWs::kKSplit, slots),
+                         dim3(kBlk), 0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
+    else
+      hipLaunchKernelGGL((k_dn_mfma<WT, kMaxTok, kBK, true>),
+                         dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s, wb, w.route,
+                         w.act, w.amax, w.ypart, g, P);
   }
   if ((err = hipGetLastError()) != hipSuccess) return err;
   static_assert(WR_MAX_TOPK == 6, "one combine instantiation per k");
