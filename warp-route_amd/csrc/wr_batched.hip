@@ -330,8 +330,12 @@ constexpr int kc_wide() {  // the 256-byte step, in columns
 template <int TOK, int KC>
 struct TokTile {
   static constexpr int kP = KC / 8;  // 16-byte pieces per token row
-  H8 hi[TOK][kP + 1];                // rows padded by a piece: spread over the LDS banks
-  H8 lo[TOK][kP + 1];
+  // Rows padded by two pieces: the MFMA B-fragment reads (ds_read_b128, lane
+  // l at row l % 16, piece 4 j + l / 16) are then free of bank conflicts.  A
+  // one-piece pad measured 4 conflict cycles per read on gfx950 (an LDS probe:
+  // 1.7x the conflict-free time); a two-piece pad or an XOR swizzle, none.
+  H8 hi[TOK][kP + 2];
+  H8 lo[TOK][kP + 2];
 };
 
 // One thread's share of a token tile, held in registers between the global
@@ -459,9 +463,8 @@ __device__ __forceinline__ void tile_store(TokTile<TOK, KC>& xs, const H8 (&hi)[
 // streaming probe measured 4 rows x 256 bytes per instruction at 6.2 TB/s
 // against 5.5 TB/s for MFMA fragments loaded straight from memory (16 rows x
 // 64 bytes).  The wave stores the bytes as they are into its own LDS tile
-// (rows padded by one piece, so the fragment reads below are free of bank
-// conflicts), MXFP4's E8M0 scale bytes (one per piece: a piece is one
-// 32-code block) beside them.  MFMA j of the step reads, in lane l, the 8
+// (WTile: rows swizzled or padded for the fragment reads below), MXFP4's
+// E8M0 scale bytes (one per piece: a piece is one 32-code block) beside them.  MFMA j of the step reads, in lane l, the 8
 // weights of row l % 16 at columns 32 j + 8 (l / 16) and decodes them:
 // fp16 and bf16 as they are, fp8 E4M3 codes to fp16 with
 // v_cvt_scalef32_pk_f16_fp8 (scale 1: every E4M3 value is an fp16 value),
@@ -474,12 +477,24 @@ struct WGeo {
   static_assert(KC % kElems == 0 && kWave % kLaneRow == 0, "whole pieces, whole rows");
 };
 
+// 16-bit weights are read as whole pieces (ds_read_b128): their rows are not
+// padded but XOR-swizzled, piece c of row r at slot c ^ (r mod 16), which an
+// LDS probe measured free of bank conflicts (a one-piece pad: 4 conflict
+// cycles per read).  fp8 and MXFP4 fragments are 8- and 4-byte reads, for
+// which the one-piece pad measured faster than a two-piece one.
 template <typename WT, int ROWS, int KC>
 struct WTile {
   static constexpr int kP = WGeo<WT, KC>::kLaneRow;
-  H8 w[ROWS][kP + 1];
+  static constexpr bool kSwz = wbits<WT>() == 16;
+  static_assert(!kSwz || kP == 16, "the swizzle permutes 16 pieces");
+  H8 w[ROWS][kP + (kSwz ? 0 : 1)];
   uint8_t s[std::is_same<WT, fp4x2>::value ? ROWS : 1][KC / 32];  // MXFP4 scale bytes
 };
+
+template <typename WT, int ROWS, int KC>
+__device__ __forceinline__ int wslot(int row, int c) {
+  return WTile<WT, ROWS, KC>::kSwz ? (c ^ (row & 15)) : c;
+}
 
 // This lane's address of row group 0 at column 0 of the K loop, for the tile
 // whose first row is `row` of a matrix with row length ld (elements).
@@ -552,7 +567,7 @@ __device__ __forceinline__ void w_store(WTile<WT, ROWS, KC>& t, const WRegs<WT, 
 #pragma unroll
   for (int i = 0; i < WRegs<WT, ROWS, KC>::N; ++i) {
     const int row = RP * i + lane / LR;
-    t.w[row][lane % LR] = __builtin_bit_cast(H8, r.v[i]);
+    t.w[row][wslot<WT, ROWS, KC>(row, lane % LR)] = __builtin_bit_cast(H8, r.v[i]);
     if constexpr (std::is_same<WT, fp4x2>::value) t.s[row][lane % LR] = r.e[i];
   }
 }
@@ -562,7 +577,7 @@ __device__ __forceinline__ void w_store(WTile<WT, ROWS, KC>& t, const WRegs<WT, 
 template <typename WT, int ROWS, int KC>
 __device__ __forceinline__ H8 a_frag(const WTile<WT, ROWS, KC>& t, int row, int j, int q) {
   if constexpr (wbits<WT>() == 16) {
-    return t.w[row][4 * j + q];
+    return t.w[row][wslot<WT, ROWS, KC>(row, 4 * j + q)];
   } else if constexpr (wbits<WT>() == 8) {
     // 16 codes per piece: piece 2 j + q / 2, bytes 8 (q % 2) ..
     const uint2 v = reinterpret_cast<const uint2*>(&t.w[row][2 * j + (q >> 1)])[q & 1];
