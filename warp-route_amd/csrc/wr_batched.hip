@@ -1023,12 +1023,15 @@ __global__ __launch_bounds__(kBlk) void k_act_split(float* __restrict__ act,
 // ---------------------------------------------------------------------------
 constexpr int kBKF = 64;           // K step, fp32 columns
 constexpr int kPF = kBKF / 4;      // 16-byte pieces per row of a step
-constexpr int kRowF = kPF + 1;     // padded row (bank spread)
 
+// Rows of 16 pieces, XOR-swizzled: piece c of row r at slot c ^ (r mod 16),
+// which keeps the 16-byte operand reads (lane l at row l % 16, piece 4 j + l / 16)
+// free of LDS bank conflicts, as for the 16-bit weight tiles.
 template <int ROWS>
 struct TileF {
-  f32x4 v[ROWS][kRowF];
+  f32x4 v[ROWS][kPF];
 };
+__device__ __forceinline__ int fslot(int row, int c) { return c ^ (row & 15); }
 
 __device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -1081,7 +1084,8 @@ __device__ __forceinline__ void f32_tile_store(TileF<TOK>& xs, const R (&t)[TP])
 #pragma unroll
   for (int q = 0; q < TP; ++q) {
     const int i = threadIdx.x + kBlk * q;
-    xs.v[i / kPF][i % kPF] = f32x4{(float)t[q][0], (float)t[q][1], (float)t[q][2], (float)t[q][3]};
+    xs.v[i / kPF][fslot(i / kPF, i % kPF)] =
+        f32x4{(float)t[q][0], (float)t[q][1], (float)t[q][2], (float)t[q][3]};
   }
 }
 
@@ -1102,7 +1106,8 @@ __device__ __forceinline__ void f32_w_load(WRegsF<ROWS>& r, const float* const (
 template <int ROWS>
 __device__ __forceinline__ void f32_w_store(TileF<ROWS>& t, const WRegsF<ROWS>& r, int lane) {
 #pragma unroll
-  for (int i = 0; i < ROWS / 4; ++i) t.v[4 * i + lane / 16][lane % 16] = r.v[i];
+  for (int i = 0; i < ROWS / 4; ++i)
+    t.v[4 * i + lane / 16][fslot(4 * i + lane / 16, lane % 16)] = r.v[i];
 }
 
 // Gate/up pass over up to TOK tokens (NT tiles of 16) of one expert, rows
@@ -1136,11 +1141,11 @@ __device__ __forceinline__ void gu_pass_f32(TileF<TOK>& xs, TileF<32>& wt,
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const f32x4 ga = wt.v[rl][4 * j + q];
-      const f32x4 ua = wt.v[16 + rl][4 * j + q];
+      const f32x4 ga = wt.v[rl][fslot(rl, 4 * j + q)];
+      const f32x4 ua = wt.v[16 + rl][fslot(rl, 4 * j + q)];
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
-        const f32x4 b = xs.v[n * 16 + rl][4 * j + q];
+        const f32x4 b = xs.v[n * 16 + rl][fslot(rl, 4 * j + q)];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           ag[n] = mfma_f32(ga[m], b[m], ag[n]);
@@ -1259,10 +1264,10 @@ __device__ __forceinline__ void dn_pass_f32(TileF<TOK>& xs, TileF<16>& wt,
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const f32x4 da = wt.v[rl][4 * j + q];
+        const f32x4 da = wt.v[rl][fslot(rl, 4 * j + q)];
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
-          const f32x4 b = xs.v[n * 16 + rl][4 * j + q];
+          const f32x4 b = xs.v[n * 16 + rl][fslot(rl, 4 * j + q)];
 #pragma unroll
           for (int m = 0; m < 4; ++m) acc[n] = mfma_f32(da[m], b[m], acc[n]);
         }
