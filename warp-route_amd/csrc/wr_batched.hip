@@ -330,13 +330,24 @@ constexpr int kc_wide() {  // the 256-byte step, in columns
 template <int TOK, int KC>
 struct TokTile {
   static constexpr int kP = KC / 8;  // 16-byte pieces per token row
-  // Rows padded by two pieces: the MFMA B-fragment reads (ds_read_b128, lane
-  // l at row l % 16, piece 4 j + l / 16) are then free of bank conflicts.  A
-  // one-piece pad measured 4 conflict cycles per read on gfx950 (an LDS probe:
-  // 1.7x the conflict-free time); a two-piece pad or an XOR swizzle, none.
-  H8 hi[TOK][kP + 2];
-  H8 lo[TOK][kP + 2];
+  // The MFMA B-fragment reads (ds_read_b128, lane l at row l % 16, piece
+  // 4 j + l / 16) are free of bank conflicts with rows padded by two pieces,
+  // or unpadded with piece c of row n at slot c ^ (n mod 16); a one-piece pad
+  // measured 4 conflict cycles per read on gfx950 (an LDS probe: 1.7x the
+  // conflict-free time).  64-token tiles take the swizzle (4 KB less LDS per
+  // block: B = 64 2-5 us faster per call), the others the pad (the swizzle
+  // measured up to 1 us slower at B = 4 and 16 with fp8 and MXFP4 weights).
+  static constexpr bool kSwz = TOK == 64;
+  static_assert(!kSwz || kP % 16 == 0, "the swizzle permutes pieces within a row");
+  H8 hi[TOK][kP + (kSwz ? 0 : 2)];
+  H8 lo[TOK][kP + (kSwz ? 0 : 2)];
 };
+
+// Slot of piece c of token row n of a TokTile.
+template <int TOK, int KC>
+__device__ __forceinline__ int tslot(int n, int c) {
+  return TokTile<TOK, KC>::kSwz ? (c ^ (n & 15)) : c;
+}
 
 // One thread's share of a token tile, held in registers between the global
 // loads and the LDS stores: pieces i = threadIdx.x + kBlk * q, token row
@@ -451,8 +462,8 @@ __device__ __forceinline__ void tile_store(TokTile<TOK, KC>& xs, const H8 (&hi)[
   for (int q = 0; q < TP; ++q) {
     const int i = threadIdx.x + kBlk * q;
     const int n = i / (KC / 8), c = i % (KC / 8);
-    xs.hi[n][c] = hi[q];
-    if (with_lo) xs.lo[n][c] = lo[q];
+    xs.hi[n][tslot<TOK, KC>(n, c)] = hi[q];
+    if (with_lo) xs.lo[n][tslot<TOK, KC>(n, c)] = lo[q];
   }
 }
 
@@ -659,11 +670,11 @@ __device__ __forceinline__ void gu_pass(TokTile<TOK, KC>& xs, WTile<WT, 32, KC>&
       for (int n = 0; n < NT; ++n) {
         const int tn = n * 16 + (lane & 15);
         constexpr bool BF = bf16_ops<WT>();
-        const H8 bh = xs.hi[tn][c];
+        const H8 bh = xs.hi[tn][tslot<TOK, KC>(tn, c)];
         ag[n] = mfma<BF>(ga, bh, ag[n]);
         au[n] = mfma<BF>(ua, bh, au[n]);
         if (LO) {
-          const H8 bl = xs.lo[tn][c];
+          const H8 bl = xs.lo[tn][tslot<TOK, KC>(tn, c)];
           ag[n] = mfma<BF>(ga, bl, ag[n]);
           au[n] = mfma<BF>(ua, bl, au[n]);
         }
@@ -894,8 +905,8 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK, KC>& xs, WTile<WT, 16, KC>&
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
           const int tn = n * 16 + (lane & 15);
-          acc[n] = mfma<bf16_ops<WT>()>(da, xs.hi[tn][c], acc[n]);
-          acc[n] = mfma<bf16_ops<WT>()>(da, xs.lo[tn][c], acc[n]);
+          acc[n] = mfma<bf16_ops<WT>()>(da, xs.hi[tn][tslot<TOK, KC>(tn, c)], acc[n]);
+          acc[n] = mfma<bf16_ops<WT>()>(da, xs.lo[tn][tslot<TOK, KC>(tn, c)], acc[n]);
         }
       }
     }
