@@ -256,3 +256,18 @@ def test_x_in_lds_kernels_fit_four_blocks_per_cu(kernels):
     assert not big, f"x-in-LDS kernels over 40 KB of LDS: {big}"
     stg = [n for k, n in xl.items() if re.search(r"ELb1ELb1ELb0EEEv", k)]
     assert stg and min(stg) > 36 * 1024, f"staged-scale kernels without their chunk buffer: {stg}"
+
+
+def test_bounded_gateup_tiles_fit_their_blocks_per_cu(kernels):
+    # k_gu_mfma<WT, LO, TOK, ROUTE, KC> with a minimum-blocks launch bound:
+    # 64-token tiles of fp8 and MXFP4 weights at 3 blocks of 4 waves per CU
+    # (168 VGPRs, 3 x LDS <= 160 KB), 32-token tiles of fp8 weights with the lo
+    # term of x at 4 (128 VGPRs, 4 x LDS <= 160 KB).
+    want = {r"k_gu_mfmaINS_4fp8wELb[01]ELi64E": 3, r"k_gu_mfmaINS_5fp4x2ELb1ELi64E": 3,
+            r"k_gu_mfmaINS_4fp8wELb1ELi32E": 4}
+    for pat, blocks in want.items():
+        ks = {k: v for k, v in kernels.items() if re.search(pat, k)}
+        assert ks, pat
+        for k, v in ks.items():
+            assert 0 < v["vgpr_alloc"] <= 512 // blocks // 8 * 8, (k, v["vgpr_alloc"])
+            assert blocks * v.get("group_segment_fixed_size", 0) <= 160 * 1024, (k, v)

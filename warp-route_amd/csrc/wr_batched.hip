@@ -743,10 +743,23 @@ struct GuRouteLds {
 template <>
 struct GuRouteLds<false> {};
 
+// Blocks per CU the compiler is asked to fit (a VGPR bound; 1 = none), where
+// LDS already allows that many and the kernels needed 8 VGPRs more: 64-token
+// tiles of fp8 (176 -> 168) and MXFP4 (176 -> 160) weights, 3 blocks instead
+// of 2 (B = 64: fp8 201 -> 195 us, MXFP4 202.5 -> 198 us per call); 32-token
+// tiles of fp8 weights with fp32 x (136 -> 128), 4 blocks instead of 3 (B = 32
+// unchanged).  Neither spills.
+template <typename WT, bool LO, int TOK, int KC>
+constexpr int gu_min_blocks() {
+  if (TOK == 64 && wbits<WT>() < 16) return 3;
+  if (TOK == 32 && wbits<WT>() == 8 && LO) return 4;
+  return 1;
+}
+
 // ROUTE: the block routes the batch itself (route_small) instead of reading
 // k_route's output; block (0, 0) publishes the routing for the later kernels.
 template <typename WT, bool LO, int TOK, bool ROUTE, int KC>
-__global__ __launch_bounds__(kBlk) void k_gu_mfma(const WT* __restrict__ wbuf,
+__global__ __launch_bounds__(kBlk, (gu_min_blocks<WT, LO, TOK, KC>())) void k_gu_mfma(const WT* __restrict__ wbuf,
                                                   const f16* __restrict__ x_hi,
                                                   const f16* __restrict__ x_lo,
                                                   const int32_t* __restrict__ x_exp,
