@@ -262,9 +262,11 @@ def test_bounded_gateup_tiles_fit_their_blocks_per_cu(kernels):
     # k_gu_mfma<WT, LO, TOK, ROUTE, KC> with a minimum-blocks launch bound:
     # 64-token tiles of fp8 and MXFP4 weights at 3 blocks of 4 waves per CU
     # (168 VGPRs, 3 x LDS <= 160 KB), 32-token tiles of fp8 weights with the lo
-    # term of x at 4 (128 VGPRs, 4 x LDS <= 160 KB).
+    # term of x at 4 (128 VGPRs, 4 x LDS <= 160 KB), 16-token tiles of fp8
+    # weights in 256-column steps at 3 (their weight tiles swizzled, not
+    # padded, to fit the LDS).
     want = {r"k_gu_mfmaINS_4fp8wELb[01]ELi64E": 3, r"k_gu_mfmaINS_5fp4x2ELb1ELi64E": 3,
-            r"k_gu_mfmaINS_4fp8wELb1ELi32E": 4}
+            r"k_gu_mfmaINS_4fp8wELb1ELi32E": 4, r"k_gu_mfmaINS_4fp8wELb[01]ELi16ELb1ELi256E": 3}
     for pat, blocks in want.items():
         ks = {k: v for k, v in kernels.items() if re.search(pat, k)}
         assert ks, pat

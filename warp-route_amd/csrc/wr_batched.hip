@@ -491,12 +491,14 @@ struct WGeo {
 // 16-bit weights are read as whole pieces (ds_read_b128): their rows are not
 // padded but XOR-swizzled, piece c of row r at slot c ^ (r mod 16), which an
 // LDS probe measured free of bank conflicts (a one-piece pad: 4 conflict
-// cycles per read).  fp8 and MXFP4 fragments are 8- and 4-byte reads, for
-// which the one-piece pad measured faster than a two-piece one.
+// cycles per read).  fp8 fragments are 8-byte reads, conflict-free both with
+// the one-piece pad and, in rows of 16 pieces (the 256-byte step), with the
+// swizzle, which those tiles take (2 KB less LDS per block).  MXFP4's 4-byte
+// reads keep the pad (about 2 conflict cycles per read in every layout tried).
 template <typename WT, int ROWS, int KC>
 struct WTile {
   static constexpr int kP = WGeo<WT, KC>::kLaneRow;
-  static constexpr bool kSwz = wbits<WT>() == 16;
+  static constexpr bool kSwz = wbits<WT>() == 16 || (wbits<WT>() == 8 && kP == 16);
   static_assert(!kSwz || kP == 16, "the swizzle permutes 16 pieces");
   H8 w[ROWS][kP + (kSwz ? 0 : 1)];
   uint8_t s[std::is_same<WT, fp4x2>::value ? ROWS : 1][KC / 32];  // MXFP4 scale bytes
@@ -591,7 +593,8 @@ __device__ __forceinline__ H8 a_frag(const WTile<WT, ROWS, KC>& t, int row, int 
     return t.w[row][wslot<WT, ROWS, KC>(row, 4 * j + q)];
   } else if constexpr (wbits<WT>() == 8) {
     // 16 codes per piece: piece 2 j + q / 2, bytes 8 (q % 2) ..
-    const uint2 v = reinterpret_cast<const uint2*>(&t.w[row][2 * j + (q >> 1)])[q & 1];
+    const uint2 v = reinterpret_cast<const uint2*>(
+        &t.w[row][wslot<WT, ROWS, KC>(row, 2 * j + (q >> 1))])[q & 1];
     return fp8x8_to_h8(v.x, v.y);
   } else {
     // 32 codes (one block) per piece: piece j, dword q
@@ -748,11 +751,14 @@ struct GuRouteLds<false> {};
 // tiles of fp8 (176 -> 168) and MXFP4 (176 -> 160) weights, 3 blocks instead
 // of 2 (B = 64: fp8 201 -> 195 us, MXFP4 202.5 -> 198 us per call); 32-token
 // tiles of fp8 weights with fp32 x (136 -> 128), 4 blocks instead of 3 (B = 32
-// unchanged).  Neither spills.
+// unchanged); 16-token tiles of fp8 weights in 256-byte steps, with the
+// swizzled weight tiles (53 KB of LDS), 3 blocks instead of 2 (176 -> 168;
+// B = 4 fp8 94.5 -> 91.2 us, B = 16 95.5 -> 94.3 us).  None spills.
 template <typename WT, bool LO, int TOK, int KC>
 constexpr int gu_min_blocks() {
   if (TOK == 64 && wbits<WT>() < 16) return 3;
   if (TOK == 32 && wbits<WT>() == 8 && LO) return 4;
+  if (TOK == 16 && wbits<WT>() == 8 && KC == kc_wide<WT>()) return 3;
   return 1;
 }
 
