@@ -306,20 +306,27 @@ __device__ __forceinline__ void route_small_publish(const SmallRoute& sr, int B,
 // K steps.  A step covers KC columns of the K dimension.  Weight rows are
 // staged in LDS as the bytes they are and decoded per MFMA fragment, so a
 // step's tile costs KC times the weight's bits, not 16 bits per weight.  With
-// 16-token tiles every weight type takes a step of 256 bytes of row (KC =
-// 128 fp16 / bf16, 256 fp8, 512 MXFP4): each wave then has 8 KB of weights
-// in flight per step and every load instruction reads 4 rows x 256 bytes
-// (with 128-column steps fp8 had half of that in flight, in 8 x 128-byte
-// pieces, and MXFP4 a quarter, in 16 x 64 bytes).  Larger token tiles, and K
-// dimensions that the wide step does not divide, take KC = 128.
+// 16-token tiles the 16-bit and fp8 weights take a step of 256 bytes of row
+// (KC = 128 fp16 / bf16, 256 fp8): each wave then has 8 KB of weights in
+// flight per step and every load instruction reads 4 rows x 256 bytes (with
+// 128-column steps fp8 had half of that in flight, in 8 x 128-byte pieces).
+// MXFP4 takes KC = 256, 8 rows x 128 bytes per instruction (KC = 128 was 16
+// x 64 bytes; KC = 512, 4 x 256 bytes, left room for fewer blocks per CU).
+// Larger token tiles, and K dimensions that the wide step does not divide,
+// take KC = 128.
 // ---------------------------------------------------------------------------
 template <typename WT>
 constexpr int wbits() {  // bits per stored weight
   return std::is_same<WT, fp4x2>::value ? 4 : (std::is_same<WT, fp8w>::value ? 8 : 16);
 }
+// The wide K step of 16-token tiles, in columns: 256 bytes of row for 16-bit
+// and fp8 weights; 256 columns (128 bytes) for MXFP4, whose 512-column step
+// took 73 KB of LDS and 224 VGPRs in gate/up (2 blocks per CU; 256 columns:
+// 40 KB, 144 VGPRs, 3 blocks) and 3 down blocks per CU instead of 5 (B = 16
+// 74.7 -> 72.2 us per call, B = 4 68.4 -> 67.8 us).
 template <typename WT>
-constexpr int kc_wide() {  // the 256-byte step, in columns
-  return 256 * 8 / wbits<WT>();
+constexpr int kc_wide() {
+  return std::is_same<WT, fp4x2>::value ? 256 : 256 * 8 / wbits<WT>();
 }
 
 // Token tiles in LDS: hi holds the hi terms, lo the lo terms; row n is token
@@ -1422,8 +1429,8 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
   // An expert has at most B tokens (a token selects it at most once), so
   // small batches take token tiles of 16 or 32.
   if (p.B <= WR_SMALL_TILE_MAX_B) {
-    // 16-token tiles: 256-byte K steps where the K dimension (h for gate/up,
-    // I for down) is a multiple of them.
+    // 16-token tiles: the wide K steps (kc_wide) where the K dimension (h for
+    // gate/up, I for down) is a multiple of them.
     constexpr int KW = kc_wide<WT>();
     if (p.h % KW == 0)
       hipLaunchKernelGGL((k_gu_mfma<WT, LO, 16, true, KW>), dim3(p.I / kBM, slots), dim3(kBlk), 0,
