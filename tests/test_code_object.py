@@ -265,8 +265,12 @@ def test_bounded_gateup_tiles_fit_their_blocks_per_cu(kernels):
     # term of x at 4 (128 VGPRs, 4 x LDS <= 160 KB), 16-token tiles of fp8
     # weights in 256-column steps at 3 (their weight tiles swizzled, not
     # padded, to fit the LDS).
-    want = {r"k_gu_mfmaINS_4fp8wELb[01]ELi64E": 3, r"k_gu_mfmaINS_5fp4x2ELb1ELi64E": 3,
-            r"k_gu_mfmaINS_4fp8wELb1ELi32E": 4, r"k_gu_mfmaINS_4fp8wELb[01]ELi16ELb1ELi256E": 3}
+    # (The template arguments end with the token and the weight K step; MXFP4's
+    # 64-token kernel with 256-column weight steps holds 2 blocks, unbounded.)
+    want = {r"k_gu_mfmaINS_4fp8wELb[01]ELi64ELb0ELi128ELi128E": 3,
+            r"k_gu_mfmaINS_5fp4x2ELb1ELi64ELb0ELi128ELi128E": 3,
+            r"k_gu_mfmaINS_4fp8wELb1ELi32ELb0ELi128ELi128E": 4,
+            r"k_gu_mfmaINS_4fp8wELb[01]ELi16ELb1ELi256ELi256E": 3}
     for pat, blocks in want.items():
         ks = {k: v for k, v in kernels.items() if re.search(pat, k)}
         assert ks, pat

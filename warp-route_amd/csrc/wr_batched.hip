@@ -68,6 +68,12 @@ namespace {
 #ifndef WR_MID_WIDE
 #define WR_MID_WIDE 1  // MXFP4 32-token tiles in the wide K step (kc_wide)
 #endif
+#ifndef WR_W2
+// MXFP4 64-token gate/up: weights in 256-column steps (8 rows x 128 bytes
+// per load instruction), two 128-column token steps each.  B = 48 / 64:
+// 167.0 / 198.8 -> 157.0 / 190.0 us per call (248 VGPRs, 2 blocks per CU).
+#define WR_W2 1
+#endif
 
 constexpr int kBlk = 256;       // 4 waves
 constexpr int kBK = 128;        // the base K step (columns); every step width is a multiple
@@ -629,15 +635,21 @@ struct GuScale {
   unsigned* s_amax;
 };
 
-template <typename WT, bool LO, int NT, int TOK, int KC>
-__device__ __forceinline__ void gu_pass(TokTile<TOK, KC>& xs, WTile<WT, 32, KC>& wt,
-                                        const WT* const (&wbase)[WRegs<WT, 32, KC>::N],
-                                        const uint8_t* const (&wsc)[WRegs<WT, 32, KC>::N],
+// WK: the weight K step, KC (the token step) or a multiple of it: each weight
+// tile then serves WK / KC token steps (MXFP4 64-token tiles: 8 rows x 128
+// bytes per weight load instruction, with the 128-column token tile).
+template <typename WT, bool LO, int NT, int TOK, int KC, int WK = KC>
+__device__ __forceinline__ void gu_pass(TokTile<TOK, KC>& xs, WTile<WT, 32, WK>& wt,
+                                        const WT* const (&wbase)[WRegs<WT, 32, WK>::N],
+                                        const uint8_t* const (&wsc)[WRegs<WT, 32, WK>::N],
                                         const f16* __restrict__ x_hi,
                                         const f16* __restrict__ x_lo, const BatchRoute& r,
                                         int p0, int mt, float* __restrict__ act, int row0,
                                         const float* __restrict__ sc, const GuScale& xsc,
                                         const Geom& g, int lane) {
+  static_assert(WK % KC == 0 && (WK == KC || std::is_same<WT, fp4x2>::value),
+                "a weight step of whole token steps (MXFP4 only)");
+  constexpr int R = WK / KC;  // token steps per weight step; h % WK == 0
   f32x4 ag[NT], au[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) ag[n] = au[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -655,41 +667,54 @@ __device__ __forceinline__ void gu_pass(TokTile<TOK, KC>& xs, WTile<WT, 32, KC>&
     xe[n] = (SC && tn < mt) ? xsc.x_exp[r.pair_tok[p0 + tn]] : 0;
   }
 
-  // Software pipeline, one K step deep: step s+1's weight and token loads are
+  // Software pipeline, one K step deep: step s+1's token loads, and with the
+  // first token step of a weight step the next weight step's loads, are
   // issued before step s's MFMAs.
-  WRegs<WT, 32, KC> wr;
+  WRegs<WT, 32, WK> wr;
   H8 th[TP], tl[TP];
-  w_load<WT, 32, KC>(wr, wbase, wsc, 0);
+  w_load<WT, 32, WK>(wr, wbase, wsc, 0);
   gu_tile_load(th, tl, x_hi, x_lo, off, 0, LO);
-  for (int s = 0; s < ns; ++s) {
-    __syncthreads();  // every wave is done reading the previous tiles
-    tile_store(xs, th, tl, LO);
-    w_store<WT, 32, KC>(wt, wr, lane);
-    __syncthreads();
-    if (s + 1 < ns) {
-      w_load<WT, 32, KC>(wr, wbase, wsc, (s + 1) * KC);
-      gu_tile_load(th, tl, x_hi, x_lo, off, (s + 1) * KC, LO);
-    }
-    // MXFP4: the next step's loads stay ahead of this step's MFMAs (the
-    // scheduler sank them below the MFMAs at 32 and 64 tokens, so each step's
-    // loads were awaited with no MFMA work in flight).
-    if constexpr (std::is_same<WT, fp4x2>::value) __builtin_amdgcn_sched_barrier(0);
+  for (int s0 = 0; s0 < ns; s0 += R) {
 #pragma unroll
-    for (int j = 0; j < KC / 32; ++j) {
-      const int c = 4 * j + (lane >> 4);
-      const H8 ga = a_frag(wt, lane & 15, j, lane >> 4);
-      const H8 ua = a_frag(wt, 16 + (lane & 15), j, lane >> 4);
+    for (int hs = 0; hs < R; ++hs) {
+      const int s = s0 + hs;
+      __syncthreads();  // every wave is done reading the previous tiles
+      tile_store(xs, th, tl, LO);
+      if (hs == 0) w_store<WT, 32, WK>(wt, wr, lane);
+      __syncthreads();
+      if constexpr (R == 1) {
+        if (s + 1 < ns) {
+          w_load<WT, 32, WK>(wr, wbase, wsc, (s + 1) * KC);
+          gu_tile_load(th, tl, x_hi, x_lo, off, (s + 1) * KC, LO);
+        }
+      } else {
+        // The next token step's loads first: the load counter is in order,
+        // so the store of that tile does not wait for the weights behind it.
+        if (s + 1 < ns) gu_tile_load(th, tl, x_hi, x_lo, off, (s + 1) * KC, LO);
+        if (hs == 0 && s0 + R < ns) w_load<WT, 32, WK>(wr, wbase, wsc, (s0 + R) * KC);
+      }
+      // MXFP4: the next step's loads stay ahead of this step's MFMAs (the
+      // scheduler sank them below the MFMAs at 32 and 64 tokens, so each
+      // step's loads were awaited with no MFMA work in flight).
+      if constexpr (std::is_same<WT, fp4x2>::value) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int n = 0; n < NT; ++n) {
-        const int tn = n * 16 + (lane & 15);
-        constexpr bool BF = bf16_ops<WT>();
-        const H8 bh = xs.hi[tn][tslot<TOK, KC>(tn, c)];
-        ag[n] = mfma<BF>(ga, bh, ag[n]);
-        au[n] = mfma<BF>(ua, bh, au[n]);
-        if (LO) {
-          const H8 bl = xs.lo[tn][tslot<TOK, KC>(tn, c)];
-          ag[n] = mfma<BF>(ga, bl, ag[n]);
-          au[n] = mfma<BF>(ua, bl, au[n]);
+      for (int j = 0; j < KC / 32; ++j) {
+        const int c = 4 * j + (lane >> 4);
+        const int jw = hs * (KC / 32) + j;  // MFMA j of the token step within the weight step
+        const H8 ga = a_frag(wt, lane & 15, jw, lane >> 4);
+        const H8 ua = a_frag(wt, 16 + (lane & 15), jw, lane >> 4);
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+          const int tn = n * 16 + (lane & 15);
+          constexpr bool BF = bf16_ops<WT>();
+          const H8 bh = xs.hi[tn][tslot<TOK, KC>(tn, c)];
+          ag[n] = mfma<BF>(ga, bh, ag[n]);
+          au[n] = mfma<BF>(ua, bh, au[n]);
+          if (LO) {
+            const H8 bl = xs.lo[tn][tslot<TOK, KC>(tn, c)];
+            ag[n] = mfma<BF>(ga, bl, ag[n]);
+            au[n] = mfma<BF>(ua, bl, au[n]);
+          }
         }
       }
     }
@@ -764,9 +789,9 @@ struct GuRouteLds<false> {};
 // unchanged); 16-token tiles of fp8 weights in 256-byte steps, with the
 // swizzled weight tiles (53 KB of LDS), 3 blocks instead of 2 (176 -> 168;
 // B = 4 fp8 94.5 -> 91.2 us, B = 16 95.5 -> 94.3 us).  None spills.
-template <typename WT, bool LO, int TOK, int KC>
+template <typename WT, bool LO, int TOK, int KC, int WK = KC>
 constexpr int gu_min_blocks() {
-  if (TOK == 64 && wbits<WT>() < 16) return 3;
+  if (TOK == 64 && wbits<WT>() < 16 && WK == KC) return 3;
   if (TOK == 32 && wbits<WT>() == 8 && LO) return 4;
   if (TOK == 16 && wbits<WT>() == 8 && KC == kc_wide<WT>()) return 3;
   return 1;
@@ -774,8 +799,8 @@ constexpr int gu_min_blocks() {
 
 // ROUTE: the block routes the batch itself (route_small) instead of reading
 // k_route's output; block (0, 0) publishes the routing for the later kernels.
-template <typename WT, bool LO, int TOK, bool ROUTE, int KC>
-__global__ __launch_bounds__(kBlk, (gu_min_blocks<WT, LO, TOK, KC>())) void k_gu_mfma(const WT* __restrict__ wbuf,
+template <typename WT, bool LO, int TOK, bool ROUTE, int KC, int WK = KC>
+__global__ __launch_bounds__(kBlk, (gu_min_blocks<WT, LO, TOK, KC, WK>())) void k_gu_mfma(const WT* __restrict__ wbuf,
                                                   const f16* __restrict__ x_hi,
                                                   const f16* __restrict__ x_lo,
                                                   const int32_t* __restrict__ x_exp,
@@ -785,7 +810,7 @@ __global__ __launch_bounds__(kBlk, (gu_min_blocks<WT, LO, TOK, KC>())) void k_gu
                                                   int32_t* __restrict__ ids_out,
                                                   float* __restrict__ w_out) {
   __shared__ TokTile<TOK, KC> xs;
-  __shared__ WTile<WT, 32, KC> wts[kBlk / kWave];
+  __shared__ WTile<WT, 32, WK> wts[kBlk / kWave];
   __shared__ GuRouteLds<ROUTE> rl;
   __shared__ unsigned s_amax[bf16_ops<WT>() ? 1 : TOK];
   if (!bf16_ops<WT>() && (int)threadIdx.x < TOK) s_amax[threadIdx.x] = 0u;
@@ -815,9 +840,9 @@ __global__ __launch_bounds__(kBlk, (gu_min_blocks<WT, LO, TOK, KC>())) void k_gu
   const int wave = threadIdx.x / kWave;
   const int row0 = blockIdx.x * kBM + wave * 16;
   const WT* blk = wbuf + (int64_t)e * g.stride;
-  const WT* G = w_lane_base<WT, KC>(blk, row0, g.h, lane);
+  const WT* G = w_lane_base<WT, WK>(blk, row0, g.h, lane);
   // Tile rows 0-15: gate rows row0 ..; rows 16-31: the same up rows.
-  constexpr int N = WRegs<WT, 32, KC>::N, RP = WGeo<WT, KC>::kRowsPer;
+  constexpr int N = WRegs<WT, 32, WK>::N, RP = WGeo<WT, WK>::kRowsPer;
   const WT* wbase[N];
   const uint8_t* wsc[N];
   // MXFP4 block scales: gate [I][h/32], then up [I][h/32]
@@ -825,29 +850,29 @@ __global__ __launch_bounds__(kBlk, (gu_min_blocks<WT, LO, TOK, KC>())) void k_gu
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     wbase[i] = G + (i < N / 2 ? 0 : g.off_up) + eoff<WT>((int64_t)(RP * (i % (N / 2))) * g.h);
-    wsc[i] = w_lane_scale<WT, KC>(mxs + (i < N / 2 ? 0 : (int64_t)g.I * g.h / 32), row0, g.h,
+    wsc[i] = w_lane_scale<WT, WK>(mxs + (i < N / 2 ? 0 : (int64_t)g.I * g.h / 32), row0, g.h,
                                   lane) +
              (int64_t)(RP * (i % (N / 2))) * (g.h / 32);
   }
   const float* sc = nullptr;
   if constexpr (std::is_same<WT, fp8w>::value) sc = wscales(blk, g.off_scale);
-  WTile<WT, 32, KC>& wt = wts[wave];
+  WTile<WT, 32, WK>& wt = wts[wave];
   for (int m0 = 0; m0 < M; m0 += TOK) {
     const int mt = min(TOK, M - m0);
     const int p0 = pbeg + m0;
     if constexpr (TOK == 16) {
-      gu_pass<WT, LO, 1, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
+      gu_pass<WT, LO, 1, TOK, KC, WK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
     } else if constexpr (TOK == 32) {
       if (mt <= 16)
-        gu_pass<WT, LO, 1, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
+        gu_pass<WT, LO, 1, TOK, KC, WK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
       else
-        gu_pass<WT, LO, 2, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
+        gu_pass<WT, LO, 2, TOK, KC, WK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane);
     } else {
       switch ((mt + 15) / 16) {
-        case 1: gu_pass<WT, LO, 1, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
-        case 2: gu_pass<WT, LO, 2, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
-        case 3: gu_pass<WT, LO, 3, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
-        default: gu_pass<WT, LO, 4, TOK, KC>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
+        case 1: gu_pass<WT, LO, 1, TOK, KC, WK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
+        case 2: gu_pass<WT, LO, 2, TOK, KC, WK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
+        case 3: gu_pass<WT, LO, 3, TOK, KC, WK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
+        default: gu_pass<WT, LO, 4, TOK, KC, WK>(xs, wt, wbase, wsc, x_hi, x_lo, r, p0, mt, act, row0, sc, xsc, g, lane); break;
       }
     }
   }
@@ -1472,10 +1497,20 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
       hipLaunchKernelGGL((k_gu_mfma<WT, LO, 32, false, kBK>), dim3(p.I / kBM, slots), dim3(kBlk),
                          0, s, wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, nullptr,
                          nullptr, nullptr);
-    else
-      hipLaunchKernelGGL((k_gu_mfma<WT, LO, kMaxTok, false, kBK>), dim3(p.I / kBM, slots),
-                         dim3(kBlk), 0, s, wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g,
-                         nullptr, nullptr, nullptr);
+    else {
+      bool wide = false;
+      if constexpr (WR_W2 && std::is_same<WT, fp4x2>::value) {
+        wide = p.h % kc_wide<WT>() == 0;
+        if (wide)
+          hipLaunchKernelGGL((k_gu_mfma<WT, LO, kMaxTok, false, kBK, kc_wide<WT>()>),
+                             dim3(p.I / kBM, slots), dim3(kBlk), 0, s, wb, w.x_hi, w.x_lo,
+                             w.x_exp, w.amax, w.route, w.act, g, nullptr, nullptr, nullptr);
+      }
+      if (!wide)
+        hipLaunchKernelGGL((k_gu_mfma<WT, LO, kMaxTok, false, kBK>), dim3(p.I / kBM, slots),
+                           dim3(kBlk), 0, s, wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act,
+                           g, nullptr, nullptr, nullptr);
+    }
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if (!mid || kPre32) {
       const int64_t pieces = (int64_t)P * (p.I / 8);
