@@ -74,6 +74,11 @@ namespace {
 // 167.0 / 198.8 -> 157.0 / 190.0 us per call (248 VGPRs, 2 blocks per CU).
 #define WR_W2 1
 #endif
+#ifndef WR_W2DN
+// The same for the MXFP4 64-token down kernel: B = 48 / 64 155.7 / 187.6 ->
+// 147.8 / 180.0 us per call (152 VGPRs, 3 blocks per CU instead of 4).
+#define WR_W2DN 1
+#endif
 
 constexpr int kBlk = 256;       // 4 waves
 constexpr int kBK = 128;        // the base K step (columns); every step width is a multiple
@@ -895,15 +900,20 @@ __device__ __forceinline__ int pair_exp(const unsigned* __restrict__ amax, int p
   }
 }
 
-template <typename WT, int NT, int TOK, int KC, bool PRE>
-__device__ __forceinline__ void dn_pass(TokTile<TOK, KC>& xs, WTile<WT, 16, KC>& wt,
-                                        const WT* const (&wbase)[WRegs<WT, 16, KC>::N],
-                                        const uint8_t* const (&wsc)[WRegs<WT, 16, KC>::N],
+// WK as in gu_pass: a weight step of WK / KC token steps (MXFP4 64-token
+// tiles, act split ahead); sb and se are then multiples of WK / KC.
+template <typename WT, int NT, int TOK, int KC, bool PRE, int WK = KC>
+__device__ __forceinline__ void dn_pass(TokTile<TOK, KC>& xs, WTile<WT, 16, WK>& wt,
+                                        const WT* const (&wbase)[WRegs<WT, 16, WK>::N],
+                                        const uint8_t* const (&wsc)[WRegs<WT, 16, WK>::N],
                                         const float* __restrict__ act,
                                         const unsigned* __restrict__ amax, int p0, int mt,
                                         int sb, int se, float* __restrict__ y, int row0,
                                         const float* __restrict__ sdown, const Geom& g,
                                         int lane) {
+  static_assert(WK % KC == 0 && (WK == KC || (std::is_same<WT, fp4x2>::value && PRE)),
+                "a weight step of whole token steps (MXFP4, act split ahead)");
+  constexpr int R = WK / KC;
   f32x4 acc[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -924,43 +934,54 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK, KC>& xs, WTile<WT, 16, KC>&
       const int n = ((int)threadIdx.x + kBlk * q) / (KC / 8);
       sx[q] = (!PRE && n < mt) ? pair_exp<WT>(amax, p0 + n) : 0;
     }
-    WRegs<WT, 16, KC> wr;
+    WRegs<WT, 16, WK> wr;
     ActRaw<PRE ? 1 : TP> ar;  // act split here: raw pieces
     H8 ph[TP], pl[TP];        // act split ahead: the two terms
-    w_load<WT, 16, KC>(wr, wbase, wsc, sb * KC);
+    w_load<WT, 16, WK>(wr, wbase, wsc, sb * KC);
     if constexpr (PRE)
       dn_tile_load_split(ph, pl, act, off, sb * KC);
     else
       dn_tile_load(ar, act, off, sb * KC);
-    for (int s = sb; s < se; ++s) {
-      __syncthreads();
-      if constexpr (PRE) {
-        tile_store(xs, ph, pl, true);
-      } else {
-        H8 th[TP], tl[TP];
-        dn_tile_split<bf16_ops<WT>()>(th, tl, ar, sx);
-        tile_store(xs, th, tl, true);
-      }
-      w_store<WT, 16, KC>(wt, wr, lane);
-      __syncthreads();
-      if (s + 1 < se) {
-        w_load<WT, 16, KC>(wr, wbase, wsc, (s + 1) * KC);
-        if constexpr (PRE)
-          dn_tile_load_split(ph, pl, act, off, (s + 1) * KC);
-        else
-          dn_tile_load(ar, act, off, (s + 1) * KC);
-      }
-      if constexpr (std::is_same<WT, fp4x2>::value)
-        __builtin_amdgcn_sched_barrier(0);  // loads ahead of the MFMAs, as in gu_pass
+    for (int s0 = sb; s0 < se; s0 += R) {
 #pragma unroll
-      for (int j = 0; j < KC / 32; ++j) {
-        const int c = 4 * j + (lane >> 4);
-        const H8 da = a_frag(wt, lane & 15, j, lane >> 4);
+      for (int hs = 0; hs < R; ++hs) {
+        const int s = s0 + hs;
+        __syncthreads();
+        if constexpr (PRE) {
+          tile_store(xs, ph, pl, true);
+        } else {
+          H8 th[TP], tl[TP];
+          dn_tile_split<bf16_ops<WT>()>(th, tl, ar, sx);
+          tile_store(xs, th, tl, true);
+        }
+        if (hs == 0) w_store<WT, 16, WK>(wt, wr, lane);
+        __syncthreads();
+        if constexpr (R == 1) {
+          if (s + 1 < se) {
+            w_load<WT, 16, WK>(wr, wbase, wsc, (s + 1) * KC);
+            if constexpr (PRE)
+              dn_tile_load_split(ph, pl, act, off, (s + 1) * KC);
+            else
+              dn_tile_load(ar, act, off, (s + 1) * KC);
+          }
+        } else {
+          // The next act tile's loads first (in-order load counter), as in
+          // gu_pass.
+          if (s + 1 < se) dn_tile_load_split(ph, pl, act, off, (s + 1) * KC);
+          if (hs == 0 && s0 + R < se) w_load<WT, 16, WK>(wr, wbase, wsc, (s0 + R) * KC);
+        }
+        if constexpr (std::is_same<WT, fp4x2>::value)
+          __builtin_amdgcn_sched_barrier(0);  // loads ahead of the MFMAs, as in gu_pass
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-          const int tn = n * 16 + (lane & 15);
-          acc[n] = mfma<bf16_ops<WT>()>(da, xs.hi[tn][tslot<TOK, KC>(tn, c)], acc[n]);
-          acc[n] = mfma<bf16_ops<WT>()>(da, xs.lo[tn][tslot<TOK, KC>(tn, c)], acc[n]);
+        for (int j = 0; j < KC / 32; ++j) {
+          const int c = 4 * j + (lane >> 4);
+          const H8 da = a_frag(wt, lane & 15, hs * (KC / 32) + j, lane >> 4);
+#pragma unroll
+          for (int n = 0; n < NT; ++n) {
+            const int tn = n * 16 + (lane & 15);
+            acc[n] = mfma<bf16_ops<WT>()>(da, xs.hi[tn][tslot<TOK, KC>(tn, c)], acc[n]);
+            acc[n] = mfma<bf16_ops<WT>()>(da, xs.lo[tn][tslot<TOK, KC>(tn, c)], acc[n]);
+          }
         }
       }
     }
@@ -988,14 +1009,15 @@ __device__ __forceinline__ void dn_pass(TokTile<TOK, KC>& xs, WTile<WT, 16, KC>&
   }
 }
 
-// PRE: act was split into its two terms by k_act_split.
-template <typename WT, int TOK, int KC, bool PRE = false>
+// PRE: act was split into its two terms by k_act_split.  WK: the weight K
+// step (dn_pass); the K slices are then whole weight steps.
+template <typename WT, int TOK, int KC, bool PRE = false, int WK = KC>
 __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, BatchRoute r,
                                                   const float* __restrict__ act,
                                                   const unsigned* __restrict__ amax,
                                                   float* __restrict__ ypart, Geom g, int P) {
   __shared__ TokTile<TOK, KC> xs;
-  __shared__ WTile<WT, 16, KC> wts[kBlk / kWave];
+  __shared__ WTile<WT, 16, WK> wts[kBlk / kWave];
   const int slot = blockIdx.z;
   if (slot >= *r.n_active) return;
   const int e = r.active[slot];
@@ -1004,14 +1026,15 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, B
   const int wave = threadIdx.x / kWave;
   const int row0 = blockIdx.x * kBM + wave * 16;
   const int ks = blockIdx.y;
-  const int nsteps = g.I / KC;
-  const int sb = nsteps * ks / BatchWs::kKSplit;
-  const int se = nsteps * (ks + 1) / BatchWs::kKSplit;
+  constexpr int R = WK / KC;  // token steps per weight step (I % WK == 0)
+  const int nsteps = g.I / WK;
+  const int sb = nsteps * ks / BatchWs::kKSplit * R;
+  const int se = nsteps * (ks + 1) / BatchWs::kKSplit * R;
   const WT* blk = wbuf + (int64_t)e * g.stride;
-  const WT* D = w_lane_base<WT, KC>(blk + g.off_down, row0, g.I, lane);
+  const WT* D = w_lane_base<WT, WK>(blk + g.off_down, row0, g.I, lane);
   const float* sdown = nullptr;  // fp8: s_down[h] follows the I gate and I up scales
   if constexpr (std::is_same<WT, fp8w>::value) sdown = wscales(blk, g.off_scale) + 2 * g.I;
-  constexpr int N = WRegs<WT, 16, KC>::N;
+  constexpr int N = WRegs<WT, 16, WK>::N;
   const WT* wbase[N];
   const uint8_t* wsc[N];
   // MXFP4 down block scales [h][I/32], after the gate and up scales
@@ -1019,27 +1042,27 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, B
       reinterpret_cast<const uint8_t*>(blk) + g.off_scale + 2 * ((int64_t)g.I * g.h / 32);
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    wbase[i] = D + eoff<WT>((int64_t)(WGeo<WT, KC>::kRowsPer * i) * g.I);
-    wsc[i] = w_lane_scale<WT, KC>(mxs, row0, g.I, lane) +
-             (int64_t)(WGeo<WT, KC>::kRowsPer * i) * (g.I / 32);
+    wbase[i] = D + eoff<WT>((int64_t)(WGeo<WT, WK>::kRowsPer * i) * g.I);
+    wsc[i] = w_lane_scale<WT, WK>(mxs, row0, g.I, lane) +
+             (int64_t)(WGeo<WT, WK>::kRowsPer * i) * (g.I / 32);
   }
   float* y = ypart + (int64_t)ks * P * g.h;
-  WTile<WT, 16, KC>& wt = wts[wave];
+  WTile<WT, 16, WK>& wt = wts[wave];
   for (int m0 = 0; m0 < M; m0 += TOK) {
     const int mt = min(TOK, M - m0);
     if constexpr (TOK == 16) {
-      dn_pass<WT, 1, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+      dn_pass<WT, 1, TOK, KC, PRE, WK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
     } else if constexpr (TOK == 32) {
       if (mt <= 16)
-        dn_pass<WT, 1, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+        dn_pass<WT, 1, TOK, KC, PRE, WK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
       else
-        dn_pass<WT, 2, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
+        dn_pass<WT, 2, TOK, KC, PRE, WK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane);
     } else {
       switch ((mt + 15) / 16) {
-        case 1: dn_pass<WT, 1, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-        case 2: dn_pass<WT, 2, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-        case 3: dn_pass<WT, 3, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
-        default: dn_pass<WT, 4, TOK, KC, PRE>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 1: dn_pass<WT, 1, TOK, KC, PRE, WK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 2: dn_pass<WT, 2, TOK, KC, PRE, WK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        case 3: dn_pass<WT, 3, TOK, KC, PRE, WK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
+        default: dn_pass<WT, 4, TOK, KC, PRE, WK>(xs, wt, wbase, wsc, act, amax, pbeg + m0, mt, sb, se, y, row0, sdown, g, lane); break;
       }
     }
   }
@@ -1525,10 +1548,20 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
     else if (mid)
       hipLaunchKernelGGL((k_dn_mfma<WT, 32, kBK, kPre32>), dim3(p.h / kBM, BatchWs::kKSplit, slots),
                          dim3(kBlk), 0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
-    else
-      hipLaunchKernelGGL((k_dn_mfma<WT, kMaxTok, kBK, true>),
-                         dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s, wb, w.route,
-                         w.act, w.amax, w.ypart, g, P);
+    else {
+      bool wide = false;
+      if constexpr (WR_W2DN && std::is_same<WT, fp4x2>::value) {
+        wide = p.I % kc_wide<WT>() == 0;
+        if (wide)
+          hipLaunchKernelGGL((k_dn_mfma<WT, kMaxTok, kBK, true, kc_wide<WT>()>),
+                             dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s, wb,
+                             w.route, w.act, w.amax, w.ypart, g, P);
+      }
+      if (!wide)
+        hipLaunchKernelGGL((k_dn_mfma<WT, kMaxTok, kBK, true>),
+                           dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s, wb,
+                           w.route, w.act, w.amax, w.ypart, g, P);
+    }
   }
   if ((err = hipGetLastError()) != hipSuccess) return err;
   static_assert(WR_MAX_TOPK == 6, "one combine instantiation per k");
