@@ -1024,8 +1024,21 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, B
   const int pbeg = r.off[e], M = r.off[e + 1] - pbeg;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int row0 = blockIdx.x * kBM + wave * 16;
-  const int ks = blockIdx.y;
+  // Workgroups go to the 8 XCDs round-robin by linear id, so with the grid's
+  // own (row tile, K slice) order every XCD ran all K slices and its L2
+  // fetched the whole act tensor.  Relabel: XCD pair q serves K slice q, and
+  // an XCD's L2 holds a quarter of act.  A bijection on (x, y) whenever
+  // gridDim.x is even; the z plane keeps its XCD offset (x*y blocks, a
+  // multiple of 8).
+  constexpr int kXcd = 8, kPer = kXcd / BatchWs::kKSplit;
+  static_assert(kXcd % BatchWs::kKSplit == 0, "K slices per XCD pair");
+  int bx = blockIdx.x, ks = blockIdx.y;
+  if (gridDim.x % kPer == 0) {
+    const int l = blockIdx.x + gridDim.x * blockIdx.y;
+    ks = (l % kXcd) / kPer;
+    bx = l % kPer + kPer * (l / kXcd);
+  }
+  const int row0 = bx * kBM + wave * 16;
   constexpr int R = WK / KC;  // token steps per weight step (I % WK == 0)
   const int nsteps = g.I / WK;
   const int sb = nsteps * ks / BatchWs::kKSplit * R;
