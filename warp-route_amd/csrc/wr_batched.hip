@@ -65,6 +65,18 @@ namespace {
 #ifndef WR_MID_TILE_MAX_B
 #define WR_MID_TILE_MAX_B 32    // and up to this size 32-token tiles
 #endif
+// Larger batches launch both the 32- and the 64-token tile kernels, and one
+// of them runs (tile_slot): the 32-token one when no expert has more than
+// this many pairs, else the 64-token one, for every expert.  Mixtral, B = 64,
+// per call, in 32-token tiles against 64-token tiles: random routing (26
+// pairs per expert at most) fp16 486 against 527 us, fp8 316 against 346,
+// MXFP4 241 against 290; clustered routing (64 pairs on the pair's experts)
+// fp16 346 against 264.  Splitting one call's experts between the two
+// launches by their own counts ran the launches one after the other, each on
+// part of the chip: clustered fp8 212 against 197 us.
+#ifndef WR_TILE_SPLIT_M
+#define WR_TILE_SPLIT_M 32
+#endif
 #ifndef WR_MID_WIDE
 #define WR_MID_WIDE 1  // MXFP4 32-token tiles in the wide K step (kc_wide)
 #endif
@@ -84,6 +96,24 @@ constexpr int kBlk = 256;       // 4 waves
 constexpr int kBK = 128;        // the base K step (columns); every step width is a multiple
 constexpr int kBM = 64;         // rows per block: 4 waves x 16
 constexpr int kMaxTok = 64;     // tokens per pass, at most: 4 MFMA N tiles
+
+// The expert slot that z (the grid's slot index) runs in a TOK-token tile
+// launch, or -1.  n_active[1] (k_route) counts the experts with more than
+// WR_TILE_SPLIT_M pairs: with none, the 32-token launch takes every slot,
+// else the 64-token launch does.  The other launch's blocks leave after one
+// load.  16-token tiles run alone and take every slot.
+template <int TOK>
+__device__ __forceinline__ int tile_slot(const BatchRoute& r, int z) {
+  static_assert(TOK == 16 || TOK == 32 || TOK == kMaxTok, "tile sizes");
+  static_assert(WR_MID_TILE_MAX_B <= WR_TILE_SPLIT_M, "32-token batches lead with no 64-token class");
+  if constexpr (TOK == 16) {
+    return z < r.n_active[0] ? z : -1;
+  } else {
+    const int n = r.n_active[0], nb = r.n_active[1];
+    const bool mine = TOK == kMaxTok ? nb > 0 : nb == 0;
+    return mine && z < n ? z : -1;
+  }
+}
 
 typedef f16x8 H8;  // eight 16-bit operands: fp16, or bf16 bit patterns
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -127,7 +157,8 @@ constexpr int kRouteLds = 4096;
 __device__ __forceinline__ void group_pairs(int P, int E, int k, const int* sel_id,
                                             const float* sel_w, int* cnt, int* off_s, int* off,
                                             int* active, int* na, int32_t* pair_tok,
-                                            float* pair_w, int32_t* tok_pair) {
+                                            float* pair_w, int32_t* tok_pair,
+                                            int* nbig = nullptr) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
@@ -145,12 +176,17 @@ __device__ __forceinline__ void group_pairs(int P, int E, int k, const int* sel_
     for (int e = 0; e < E; ++e) {
       off_s[e] = o;
       off[e] = o;
-      if (cnt[e] > 0) active[n++] = e;
       o += cnt[e];
     }
     off_s[E] = o;
     off[E] = o;
+    int nb = 0;
+    for (int e = 0; e < E; ++e) {
+      if (cnt[e] > 0) active[n++] = e;
+      nb += cnt[e] > WR_TILE_SPLIT_M;
+    }
     *na = n;
+    if (nbig != nullptr) *nbig = nb;  // experts for 64-token tiles (tile_slot)
   }
   __syncthreads();
   // Stable placement: expert e's pairs in token order.
@@ -231,7 +267,7 @@ __global__ __launch_bounds__(1024) void k_route(const float* __restrict__ logits
   }
   __syncthreads();
   group_pairs(P, E, k, sel_id, sel_w, s_cnt, s_off, r.off, r.active, r.n_active, r.pair_tok,
-              r.pair_w, r.tok_pair);
+              r.pair_w, r.tok_pair, r.n_active + 1);
 }
 
 // In-block routing for small batches (B <= WR_SMALL_TILE_MAX_B): every
@@ -836,8 +872,9 @@ __global__ __launch_bounds__(kBlk, (gu_min_blocks<WT, LO, TOK, KC, WK>())) void 
     (void)logits;
     (void)ids_out;
     (void)w_out;
-    if (slot >= *r.n_active) return;  // block-uniform
-    e = r.active[slot];
+    const int sl = tile_slot<TOK>(r, slot);
+    if (sl < 0) return;  // block-uniform
+    e = r.active[sl];
     pbeg = r.off[e];
     M = r.off[e + 1] - pbeg;
   }
@@ -1018,8 +1055,8 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, B
                                                   float* __restrict__ ypart, Geom g, int P) {
   __shared__ TokTile<TOK, KC> xs;
   __shared__ WTile<WT, 16, WK> wts[kBlk / kWave];
-  const int slot = blockIdx.z;
-  if (slot >= *r.n_active) return;
+  const int slot = tile_slot<TOK>(r, blockIdx.z);
+  if (slot < 0) return;
   const int e = r.active[slot];
   const int pbeg = r.off[e], M = r.off[e + 1] - pbeg;
   const int lane = threadIdx.x & (kWave - 1);
@@ -1525,15 +1562,18 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
     // B = 24 / 32: 115.1 / 119.6 -> 102.8 / 103.5 us per call (gate/up 176
     // VGPRs, 2 blocks per CU; a 3-block bound, 144 VGPRs, measured slower).
     constexpr int KM = (WR_MID_WIDE && std::is_same<WT, fp4x2>::value) ? kc_wide<WT>() : kBK;
-    if (mid && KM != kBK && p.h % KM == 0)
+    // Beyond WR_MID_TILE_MAX_B both tile launches are made and one of them
+    // runs (tile_slot); act is split for either down launch.
+    if (KM != kBK && p.h % KM == 0)
       hipLaunchKernelGGL((k_gu_mfma<WT, LO, 32, false, KM>), dim3(p.I / kBM, slots), dim3(kBlk),
                          0, s, wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, nullptr,
                          nullptr, nullptr);
-    else if (mid)
+    else
       hipLaunchKernelGGL((k_gu_mfma<WT, LO, 32, false, kBK>), dim3(p.I / kBM, slots), dim3(kBlk),
                          0, s, wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, nullptr,
                          nullptr, nullptr);
-    else {
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    if (!mid) {
       bool wide = false;
       if constexpr (WR_W2 && std::is_same<WT, fp4x2>::value) {
         wide = p.h % kc_wide<WT>() == 0;
@@ -1562,6 +1602,16 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
       hipLaunchKernelGGL((k_dn_mfma<WT, 32, kBK, kPre32>), dim3(p.h / kBM, BatchWs::kKSplit, slots),
                          dim3(kBlk), 0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
     else {
+      // act is split for every type here
+      if (KM != kBK && p.I % KM == 0)
+        hipLaunchKernelGGL((k_dn_mfma<WT, 32, KM, true>),
+                           dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s, wb,
+                           w.route, w.act, w.amax, w.ypart, g, P);
+      else
+        hipLaunchKernelGGL((k_dn_mfma<WT, 32, kBK, true>),
+                           dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s, wb,
+                           w.route, w.act, w.amax, w.ypart, g, P);
+      if ((err = hipGetLastError()) != hipSuccess) return err;
       bool wide = false;
       if constexpr (WR_W2DN && std::is_same<WT, fp4x2>::value) {
         wide = p.I % kc_wide<WT>() == 0;

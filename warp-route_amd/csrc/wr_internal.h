@@ -101,7 +101,7 @@ struct BatchRoute {
   int32_t* tok_pair;  // [P] by q: p
   int32_t* off;       // [E + 1]: expert e's pairs are [off[e], off[e + 1])
   int32_t* active;    // [E]: experts with pairs, ascending
-  int32_t* n_active;  // [1]
+  int32_t* n_active;  // [2]: experts with pairs; how many have more than 32 (k_route)
 };
 
 struct BatchWs {
@@ -154,7 +154,7 @@ struct BatchWs {
     w.route.tok_pair = reinterpret_cast<int32_t*>(take(P * 4));
     w.route.off = reinterpret_cast<int32_t*>(take((size_t)(E + 1) * 4));
     w.route.active = reinterpret_cast<int32_t*>(take((size_t)E * 4));
-    w.route.n_active = reinterpret_cast<int32_t*>(take(4));
+    w.route.n_active = reinterpret_cast<int32_t*>(take(8));
     w.act = reinterpret_cast<float*>(take(P * I * 4));
     w.ypart = reinterpret_cast<float*>(take((size_t)kKSplit * P * h * 4));
     if (total != nullptr) *total = off;
