@@ -82,6 +82,34 @@ def test_full_size_batched_clustered_every_row(cuda, mixtral_layer, B):
     check_rows(out, ids, ws, x, gw, buf, E, h, I, k, True, f"mixtral B={B}")
 
 
+@pytest.mark.parametrize("wd", [F16, FP8, MX4], ids=["f16", "fp8", "mxfp4"])
+@pytest.mark.parametrize("routing", ["random", "clustered"])
+def test_full_size_batched_tile_class_every_row(cuda, routing, wd):
+    """Beyond 32 tokens a call runs every expert in 32-token tiles when no
+    expert has more than 32 pairs, else in 64-token tiles (the device decides
+    from the pair counts). B = 48 at Mixtral shape: random tokens (at most
+    about 20 pairs per expert) take the 32-token launch, tokens clustered on
+    one pair (most of the batch on each of its experts) the 64-token one. Every row
+    against the oracle."""
+    cfg = CONFIGS["mixtral"].with_weights(wd)
+    E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+    B = 48
+    x, gw, buf = make_config_layer(cfg, seed=5, batch=B, device=cuda, gen_device=cuda)
+    if routing == "clustered":
+        x = clustered_batch(gw, B, pair=(2, 7), alpha=4.0, seed=5, device=cuda)
+    print(f"[gpu] full batched mixtral {WNAME[wd]} B={B} {routing}, every row", flush=True)
+    ids = torch.empty(B, k, dtype=torch.int32, device=cuda)
+    ws = torch.empty(B, k, dtype=torch.float32, device=cuda)
+    out = F.batched_fused_moe(x, gw, buf, E, h, I, k, cfg.renormalize, ids, ws)
+    torch.cuda.synchronize()
+    most = int(np.bincount(ids.cpu().numpy().reshape(-1), minlength=E).max())
+    assert (most <= 32) == (routing == "random"), f"{routing}: {most} pairs on one expert"
+    check_rows(out, ids, ws, x, gw, buf, E, h, I, k, cfg.renormalize,
+               f"mixtral {WNAME[wd]} B={B} {routing}")
+    del buf
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("B", [4, 24, 64])
 def test_full_size_batched_fp32_weights_every_row(cuda, B):
     """fp32 weights (the reference's only format) at Mixtral shape through the

@@ -286,7 +286,7 @@ GROUPED = [(8, 256, 512, 2, False), (16, 512, 1024, 2, True), (64, 256, 512, 6, 
 
 @pytest.mark.parametrize("wd", [F16, FP8, BF16, MX4, F32], ids=["f16", "fp8", "bf16", "mxfp4", "f32"])
 @pytest.mark.parametrize("x_dtype", [F32, F16], ids=["xf32", "xf16"])
-@pytest.mark.parametrize("B", [2, 5, 24, 33, 80])  # token tiles of 16, 16, 32, 64, 64
+@pytest.mark.parametrize("B", [2, 5, 24, 33, 80])  # tiles 16, 16, 32; then 32 or 64 by pairs per expert
 @pytest.mark.parametrize("cfg", GROUPED,
                          ids=lambda c: f"E{c[0]}-h{c[1]}-I{c[2]}-k{c[3]}" + ("-renorm" if c[4] else ""))
 def test_grouped_batched_parity(cuda, cfg, B, x_dtype, wd):
