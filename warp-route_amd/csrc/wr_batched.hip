@@ -1126,9 +1126,14 @@ __global__ __launch_bounds__(kBlk) void k_dn_mfma(const WT* __restrict__ wbuf, B
 // same values again (the down kernel's VALU work was about 2.3 times its
 // gate/up kernel's at B = 64).
 template <bool BF>
+//
+// only_big: when not null, the split runs only if *only_big > 0, i.e. when
+// the 64-token launch runs (tile_slot); 16-bit weights' 32-token down kernel
+// splits act while staging instead.
 __global__ __launch_bounds__(kBlk) void k_act_split(float* __restrict__ act,
                                                     const unsigned* __restrict__ amax, int P,
-                                                    int I) {
+                                                    int I, const int32_t* __restrict__ only_big) {
+  if (only_big != nullptr && *only_big == 0) return;  // grid-uniform
   const int pp = I / 8;  // pieces per pair
   const int64_t n = (int64_t)P * pp;
   for (int64_t i = (int64_t)blockIdx.x * kBlk + threadIdx.x; i < n;
@@ -1563,7 +1568,7 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
     // VGPRs, 2 blocks per CU; a 3-block bound, 144 VGPRs, measured slower).
     constexpr int KM = (WR_MID_WIDE && std::is_same<WT, fp4x2>::value) ? kc_wide<WT>() : kBK;
     // Beyond WR_MID_TILE_MAX_B both tile launches are made and one of them
-    // runs (tile_slot); act is split for either down launch.
+    // runs (tile_slot).
     if (KM != kBK && p.h % KM == 0)
       hipLaunchKernelGGL((k_gu_mfma<WT, LO, 32, false, KM>), dim3(p.I / kBM, slots), dim3(kBlk),
                          0, s, wb, w.x_hi, w.x_lo, w.x_exp, w.amax, w.route, w.act, g, nullptr,
@@ -1592,7 +1597,8 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
       const int64_t pieces = (int64_t)P * (p.I / 8);
       const int split_blocks = (int)std::min<int64_t>((pieces + kBlk - 1) / kBlk, 4096);
       hipLaunchKernelGGL((k_act_split<bf16_ops<WT>()>), dim3(split_blocks), dim3(kBlk), 0, s,
-                         w.act, w.amax, P, p.I);
+                         w.act, w.amax, P, p.I,
+                         kPre32 ? nullptr : static_cast<const int32_t*>(w.route.n_active + 1));
       if ((err = hipGetLastError()) != hipSuccess) return err;
     }
     if (mid && KM != kBK && p.I % KM == 0)
@@ -1602,13 +1608,14 @@ hipError_t grouped_t(const Problem& p, const BatchWs& w, hipStream_t s) {
       hipLaunchKernelGGL((k_dn_mfma<WT, 32, kBK, kPre32>), dim3(p.h / kBM, BatchWs::kKSplit, slots),
                          dim3(kBlk), 0, s, wb, w.route, w.act, w.amax, w.ypart, g, P);
     else {
-      // act is split for every type here
+      // act is split when the 64-token launch runs, and for 8- and 4-bit
+      // weights always
       if (KM != kBK && p.I % KM == 0)
-        hipLaunchKernelGGL((k_dn_mfma<WT, 32, KM, true>),
+        hipLaunchKernelGGL((k_dn_mfma<WT, 32, KM, kPre32>),
                            dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s, wb,
                            w.route, w.act, w.amax, w.ypart, g, P);
       else
-        hipLaunchKernelGGL((k_dn_mfma<WT, 32, kBK, true>),
+        hipLaunchKernelGGL((k_dn_mfma<WT, 32, kBK, kPre32>),
                            dim3(p.h / kBM, BatchWs::kKSplit, slots), dim3(kBlk), 0, s, wb,
                            w.route, w.act, w.amax, w.ypart, g, P);
       if ((err = hipGetLastError()) != hipSuccess) return err;
