@@ -19,6 +19,10 @@
 //   3. k_gu_mfma: block (row tile, expert slot): 4 waves x 16 gate rows and
 //      the same 16 up rows each, all of the expert's tokens (up to 64 per
 //      pass); the token tile is staged in LDS and shared by the 4 waves.
+//      Tiles of 16 tokens for B <= 16 and 32 for B <= 32; beyond that both
+//      the 32- and the 64-token kernels are launched and one of them runs,
+//      as k_route's count of experts with more than 32 pairs says
+//      (tile_slot).
 //      v_mfma_f32_16x16x32_f16 with A = weight rows (fp16, or fp8 E4M3 codes
 //      staged as they are and converted exactly to fp16 per fragment) and
 //      B = the hi and lo terms of x; products are exact and accumulate in
