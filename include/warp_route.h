@@ -19,10 +19,12 @@
  *               behaviour)
  *   out       = sum_kk w[kk] * Wd_e (silu(Wg_e x) * (Wu_e x)),  e = ids[kk]
  *                                                        (src/fused_moe.cu:167-224)
- * Gating and accumulation are fp32.  Expert weights are fp32, fp16, bf16 or
- * fp8 (e4m3) in the packed expert layout (src/expert_layout.cuh:5-18): per
- * expert [gate I x h][up I x h][down h x I], row-major, expert stride rounded
- * up to 128 bytes.  fp8 blocks also hold fp32 scales (wr_layout_dtype).
+ * Gating and accumulation are fp32.  Expert weights are fp32, fp16, bf16, fp8
+ * (e4m3) or MXFP4 (e2m1 codes, two per byte, with an e8m0 scale per 32
+ * elements of a row) in the packed expert layout (src/expert_layout.cuh:5-18):
+ * per expert [gate I x h][up I x h][down h x I], row-major, expert stride
+ * rounded up to 128 bytes.  fp8 blocks also hold fp32 row scales, MXFP4
+ * blocks their scale bytes after the codes (wr_layout_dtype).
  *
  * Streams: work is enqueued asynchronously on `stream` (a hipStream_t passed
  * as void*, NULL = the null stream).  The reference launched on the legacy
@@ -57,7 +59,7 @@ extern "C" {
 #define WR_EXPERT_ALIGN 128
 /* Bytes of device scratch wr_fused_moe_noalloc holds per GPU (1 MiB): enough
  * for wr_workspace_bytes(WR_KIND_FUSED, ...) up to k * roundup(I, 16) =
- * 253,440 (Mixtral needs 28,672, DBRX 43,008, DeepSeek 8,448). */
+ * 252,992 (Mixtral needs 28,672, DBRX 43,008, DeepSeek 8,448). */
 #define WR_NOALLOC_SCRATCH_BYTES (1u << 20)
 
 typedef enum wr_status {
@@ -216,7 +218,10 @@ WR_API size_t wr_workspace_bytes(int kind, int num_experts, int hidden_dim,
  * (src/gate.cu:103-116, declared at src/gate.cuh:21-27). */
 WR_API int wr_gate_topk(const wr_moe_args *args, void *stream);
 
-/* Single-token fused MoE (batch_size must be 1).  Replaces fused_moe_forward
+/* Single-token fused MoE (batch_size must be 1): a router launch, then one
+ * kernel for the selection and the whole expert FFN.  The workspace needs no
+ * initialisation (each call resets the control words it uses) and may be
+ * reused by later calls on the same stream.  Replaces fused_moe_forward
  * (src/fused_moe.cu:233-263, declared at src/fused_moe.cuh:29-32). */
 WR_API int wr_fused_moe(const wr_moe_args *args, void *stream);
 
@@ -233,7 +238,7 @@ WR_API int wr_fused_moe_opts(const wr_moe_args *args, const wr_fused_opts *opts,
  * WR_ETIMEOUT if a hand-off wait expired (the output then holds NaN rows).
  * Reads the timeout word with a copy on `stream` and synchronises `stream`;
  * call it after the op and before the next single-token call on the same
- * workspace, whose router launch clears the word.  Has no counterpart in the
+ * workspace, which clears the word.  Has no counterpart in the
  * reference, whose fused kernel exits the process on error
  * (src/fused_moe.cu:9-15). */
 WR_API int wr_fused_moe_status(const void *workspace, size_t workspace_bytes, void *stream);
@@ -241,7 +246,7 @@ WR_API int wr_fused_moe_status(const void *workspace, size_t workspace_bytes, vo
 /* The two launches of wr_fused_moe, for callers that issue them separately
  * (to overlap the router with other work on the stream's timeline, or to time
  * the expert FFN alone).  wr_fused_moe_route computes the router logits into
- * the workspace and resets its control block; wr_fused_moe_ffn selects the
+ * the workspace and resets its control words; wr_fused_moe_ffn selects the
  * experts from those logits and runs the FFN.  Both take the arguments of
  * wr_fused_moe and validate them the same way.  Call them in this order, on
  * one stream, with one workspace and nothing else using that workspace in
@@ -261,11 +266,14 @@ WR_API int wr_fused_moe_ffn(const wr_moe_args *args, void *stream);
  * that GPU's array address once.  Returns WR_EINVAL_SCRATCH (before any HIP
  * call) when wr_workspace_bytes(WR_KIND_FUSED, E, h, I, k, 1) exceeds
  * WR_NOALLOC_SCRATCH_BYTES.  Every call on one GPU shares its array, and the
- * array keeps the last call's contents (each call's router launch clears the
- * control words it needs), so calls that overlap on one GPU -- on different
- * streams, or from different threads -- race and must be serialised by the
- * caller.  Otherwise identical to wr_fused_moe, with the same kernels and
- * results. */
+ * array keeps the last call's contents (each call clears the control words
+ * it needs), so calls that overlap on one GPU -- on different streams, or
+ * from different threads -- race and must be serialised by the caller.  The
+ * call may be recorded into a HIP graph once a first call on the GPU has
+ * looked up the array.  A hand-off expiry shows only as
+ * NaN output rows: the timeout word lives in the library's array, which
+ * wr_fused_moe_status cannot be given.  Otherwise identical to wr_fused_moe,
+ * with the same kernels and results. */
 WR_API int wr_fused_moe_noalloc(const wr_moe_args *args, void *stream);
 
 /* B-token fused MoE (batch_size >= 0; 0 is a no-op as in

@@ -82,22 +82,30 @@ def test_full_size_batched_clustered_every_row(cuda, mixtral_layer, B):
     check_rows(out, ids, ws, x, gw, buf, E, h, I, k, True, f"mixtral B={B}")
 
 
-@pytest.mark.parametrize("wd", [F16, FP8, MX4], ids=["f16", "fp8", "mxfp4"])
-@pytest.mark.parametrize("routing", ["random", "clustered"])
-def test_full_size_batched_tile_class_every_row(cuda, routing, wd):
+TILE_CLASS = [("random", F16, F32), ("clustered", F16, F32), ("random", FP8, F32),
+              ("clustered", FP8, F32), ("random", MX4, F32), ("clustered", MX4, F32),
+              ("random", BF16, F32), ("clustered", BF16, F32), ("random", F16, F16)]
+
+
+@pytest.mark.parametrize("routing,wd,x_dtype", TILE_CLASS,
+                         ids=[f"{r}-{WNAME[w]}-x{WNAME[x]}" for r, w, x in TILE_CLASS])
+def test_full_size_batched_tile_class_every_row(cuda, routing, wd, x_dtype):
     """Beyond 32 tokens a call runs every expert in 32-token tiles when no
     expert has more than 32 pairs, else in 64-token tiles (the device decides
     from the pair counts). B = 48 at Mixtral shape: random tokens (at most
     about 20 pairs per expert) take the 32-token launch, tokens clustered on
     one pair (most of the batch on each of its experts) the 64-token one. Every row
-    against the oracle."""
+    against the oracle; fp16, fp8, MXFP4 and bf16 weights with fp32 x, and fp16
+    x through the 32-token class."""
     cfg = CONFIGS["mixtral"].with_weights(wd)
     E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
     B = 48
     x, gw, buf = make_config_layer(cfg, seed=5, batch=B, device=cuda, gen_device=cuda)
     if routing == "clustered":
         x = clustered_batch(gw, B, pair=(2, 7), alpha=4.0, seed=5, device=cuda)
-    print(f"[gpu] full batched mixtral {WNAME[wd]} B={B} {routing}, every row", flush=True)
+    x = x.to(x_dtype)
+    print(f"[gpu] full batched mixtral {WNAME[wd]} B={B} {routing} x {WNAME[x_dtype]}, "
+          f"every row", flush=True)
     ids = torch.empty(B, k, dtype=torch.int32, device=cuda)
     ws = torch.empty(B, k, dtype=torch.float32, device=cuda)
     out = F.batched_fused_moe(x, gw, buf, E, h, I, k, cfg.renormalize, ids, ws)
@@ -105,7 +113,8 @@ def test_full_size_batched_tile_class_every_row(cuda, routing, wd):
     most = int(np.bincount(ids.cpu().numpy().reshape(-1), minlength=E).max())
     assert (most <= 32) == (routing == "random"), f"{routing}: {most} pairs on one expert"
     check_rows(out, ids, ws, x, gw, buf, E, h, I, k, cfg.renormalize,
-               f"mixtral {WNAME[wd]} B={B} {routing}")
+               f"mixtral {WNAME[wd]} B={B} {routing} x {WNAME[x_dtype]}",
+               rel_tol=2e-3 if x_dtype == F16 else 1e-4)
     del buf
     torch.cuda.empty_cache()
 
@@ -222,10 +231,17 @@ RANGE = [("x1e5", 1e5, 1e-5, 0.05, F32), ("x1e-6", 1e-6, 1e6, 0.05, F32),
          ("std2e-4", 1.0, 1.0, 2e-4, F32), ("xf16-4096", 4096.0, 1.0 / 4096.0, 2e-4, F16)]
 
 
+# (B, routing): 16-token tiles at B = 5, 32-token tiles at B = 24; at B = 40
+# clustered tokens put more than 32 pairs on one expert (64-token tiles, act
+# split ahead of the down kernel) and random tokens at most 32 on every
+# expert (32-token tiles, whose down kernel splits act while staging it).
+RANGE_BATCHES = [(5, "clustered"), (24, "clustered"), (40, "clustered"), (40, "random")]
+
+
 @pytest.mark.parametrize("wd", [F16, FP8, BF16, MX4, F32], ids=["f16", "fp8", "bf16", "mxfp4", "f32"])
-@pytest.mark.parametrize("B", [5, 40])
+@pytest.mark.parametrize("B,routing", RANGE_BATCHES, ids=[f"B{b}-{r}" for b, r in RANGE_BATCHES])
 @pytest.mark.parametrize("case", RANGE, ids=[c[0] for c in RANGE])
-def test_grouped_batched_range(cuda, case, B, wd):
+def test_grouped_batched_range(cuda, case, B, routing, wd):
     """The grouped path stays within the parity bar when x and act leave
     fp16's range: every row equals the single-token op (fp32 throughout) up
     to summation order, and every robust row the oracle."""
@@ -233,16 +249,23 @@ def test_grouped_batched_range(cuda, case, B, wd):
     E, h, I, k, rn = 8, 512, 1024, 2, True
     _, gw, buf = make_layer(E, h, I, wd, router_std=h ** -0.5, expert_std=es, seed=3,
                             device=cuda)
-    x = (clustered_batch(gw, B, pair=(1, E - 1), alpha=4.0, seed=B, device=cuda) * xs)
+    if routing == "clustered":
+        x = clustered_batch(gw, B, pair=(1, E - 1), alpha=4.0, seed=B, device=cuda) * xs
+    else:
+        gen = torch.Generator(device="cpu").manual_seed(B)
+        x = torch.randn(B, h, generator=gen).to(cuda) * xs
     x = x.to(x_dtype)
     gw = (gw * rs).contiguous()
     assert torch.isfinite(x).all()
-    print(f"[gpu] grouped range {name} B={B} {WNAME[wd]}", flush=True)
+    print(f"[gpu] grouped range {name} B={B} {routing} {WNAME[wd]}", flush=True)
     ids = torch.empty(B, k, dtype=torch.int32, device=cuda)
     ws = torch.empty(B, k, dtype=torch.float32, device=cuda)
     out = F.batched_fused_moe(x, gw, buf, E, h, I, k, rn, ids, ws)
     torch.cuda.synchronize()
     assert torch.isfinite(out).all(), f"{name}: non-finite output"
+    most = int(np.bincount(ids.cpu().numpy().reshape(-1), minlength=E).max())
+    if B > 32:
+        assert (most <= 32) == (routing == "random"), f"{routing}: {most} pairs on one expert"
     rows = oracle_rows(x, gw, buf, E, h, I, k, rn)
     checked = 0
     for b in range(B):

@@ -284,12 +284,21 @@ GROUPED = [(8, 256, 512, 2, False), (16, 512, 1024, 2, True), (64, 256, 512, 6, 
            (8, 384, 640, 1, True)]
 
 
+# (B, routing): tiles of 16 tokens for B <= 16 and of 32 for B <= 32; beyond
+# that 32-token tiles when no expert has more than 32 (token, expert) pairs,
+# else 64-token tiles.  Clustered batches of 33 and 80 put more than 32 pairs
+# on one expert (E = 16 at B = 33 exactly 32: the 32-token class), random
+# batches of 33 and 48 at most 18.
+BATCHES = [(2, "clustered"), (5, "clustered"), (24, "clustered"), (33, "clustered"),
+           (80, "clustered"), (33, "random"), (48, "random")]
+
+
 @pytest.mark.parametrize("wd", [F16, FP8, BF16, MX4, F32], ids=["f16", "fp8", "bf16", "mxfp4", "f32"])
 @pytest.mark.parametrize("x_dtype", [F32, F16], ids=["xf32", "xf16"])
-@pytest.mark.parametrize("B", [2, 5, 24, 33, 80])  # tiles 16, 16, 32; then 32 or 64 by pairs per expert
+@pytest.mark.parametrize("B,routing", BATCHES, ids=[f"B{b}-{r}" for b, r in BATCHES])
 @pytest.mark.parametrize("cfg", GROUPED,
                          ids=lambda c: f"E{c[0]}-h{c[1]}-I{c[2]}-k{c[3]}" + ("-renorm" if c[4] else ""))
-def test_grouped_batched_parity(cuda, cfg, B, x_dtype, wd):
+def test_grouped_batched_parity(cuda, cfg, B, routing, x_dtype, wd):
     """The grouped MFMA batched path (fp16, fp8, bf16 or MXFP4 weights, h and
     I multiples of 128; fp32 weights with exact fp32 MFMA products; fp8 and
     MXFP4 codes are staged raw and decoded per MFMA fragment, fp8 to fp16
@@ -301,7 +310,9 @@ def test_grouped_batched_parity(cuda, cfg, B, x_dtype, wd):
     them, so their rows are compared with the single-token op at 5e-5 of
     max|out| instead of 1e-5).
     Tokens cluster on one expert pair, so experts get anywhere from 1 to B
-    tokens (B = 80 puts more than 64 on one expert: two token passes).  Every
+    tokens (B = 80 puts more than 64 on one expert: two token passes), or
+    route at random (x ~ N(0, 1)), which keeps every expert at 32 pairs or
+    fewer and so pins the 32-token class beyond 32 tokens.  Every
     row's ids and weights are bit-identical to the single-token op and its
     output equals that op's up to summation order; a subset is checked against
     the oracle; two calls are bit-identical."""
@@ -309,8 +320,12 @@ def test_grouped_batched_parity(cuda, cfg, B, x_dtype, wd):
     _, gw, buf = make_layer(E, h, I, wd, router_std=h ** -0.5, expert_std=0.05, seed=3,
                             device=cuda)
     pair = (1, 1) if k == 1 else (1, E - 1)  # k = 1: every token on one expert
-    x = clustered_batch(gw, B, pair=pair, alpha=4.0, seed=B, device=cuda).to(x_dtype)
-    print(f"[gpu] grouped E{E}-h{h}-I{I}-k{k} B={B} {x_dtype} {WNAME[wd]}", flush=True)
+    if routing == "clustered":
+        x = clustered_batch(gw, B, pair=pair, alpha=4.0, seed=B, device=cuda).to(x_dtype)
+    else:
+        gen = torch.Generator(device="cpu").manual_seed(B)
+        x = torch.randn(B, h, generator=gen).to(device=cuda, dtype=x_dtype)
+    print(f"[gpu] grouped E{E}-h{h}-I{I}-k{k} B={B} {routing} {x_dtype} {WNAME[wd]}", flush=True)
     ids = torch.empty(B, k, dtype=torch.int32, device=cuda)
     ws = torch.empty(B, k, dtype=torch.float32, device=cuda)
     out = F.batched_fused_moe(x, gw, buf, E, h, I, k, rn, ids, ws)
@@ -321,6 +336,10 @@ def test_grouped_batched_parity(cuda, cfg, B, x_dtype, wd):
     assert counts.sum() == B * k
     if B == 80:
         assert counts.max() > 64, counts
+    if routing == "random":
+        assert counts.max() <= 32, counts  # 32-token tiles for B > 32
+    elif B == 33:
+        assert (counts.max() > 32) == (E != 16), counts  # 64-token tiles except at E = 16
     checked = 0
     for b in range(B):
         s_ids = torch.empty(k, dtype=torch.int32, device=cuda)

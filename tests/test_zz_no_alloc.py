@@ -85,3 +85,51 @@ def test_noalloc_rejects_problems_over_its_scratch(cuda):
     a.weight_bytes = 1 << 40  # pass the size check; the scratch check comes first anyway
     st = capi.lib().wr_fused_moe_noalloc(ctypes.byref(a), None)
     assert st == capi.WR_EINVAL_SCRATCH, capi.status_str(st)
+
+
+def test_noalloc_call_captured_in_a_graph(cuda):
+    """wr_fused_moe_noalloc recorded into a HIP graph (torch.cuda.graph on its
+    capture stream) after a first eager call on the GPU (which looks up the
+    scratch array's address; the captured call then makes no HIP call but the
+    launch).  Each replay, with new x values copied into the captured input
+    and eager calls of the same entry point between replays, equals
+    wr_fused_moe on a caller workspace bit for bit."""
+    E, h, I, k, wd = 64, 2048, 1408, 6, torch.float16
+    x, gw, buf = make_layer(E, h, I, wd, router_std=h ** -0.5, seed=40, device=cuda,
+                            gen_device=cuda)
+    out = torch.empty_like(x)
+    ids = torch.empty(k, dtype=torch.int32, device=cuda)
+    ws = torch.empty(k, dtype=torch.float32, device=cuda)
+    a = _args(x, gw, buf, E, h, I, k, out, ids, ws)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert capi.lib().wr_fused_moe_noalloc(ctypes.byref(a), stream) == capi.WR_OK
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        cs = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        st = capi.lib().wr_fused_moe_noalloc(ctypes.byref(a), cs)
+    assert st == capi.WR_OK, capi.status_str(st)
+    nws = capi.lib().wr_workspace_bytes(capi.WR_KIND_FUSED, E, h, I, k, 1)
+    work = torch.empty(nws, dtype=torch.uint8, device=cuda)
+    gen = torch.Generator(device="cpu").manual_seed(41)
+    for rep in range(4):
+        print(f"[gpu] noalloc graph replay {rep}", flush=True)
+        x.copy_(torch.randn(h, generator=gen).to(cuda))
+        g.replay()
+        torch.cuda.synchronize()
+        got = (out.clone(), ids.clone(), ws.clone())
+        want = (torch.empty_like(x), torch.empty_like(ids), torch.empty_like(ws))
+        st = capi.lib().wr_fused_moe(
+            ctypes.byref(_args(x, gw, buf, E, h, I, k, *want, work=work)), stream)
+        assert st == capi.WR_OK, capi.status_str(st)
+        # an eager call of the entry point between replays (other outputs)
+        other = (torch.empty_like(x), torch.empty_like(ids), torch.empty_like(ws))
+        xo = -x
+        st = capi.lib().wr_fused_moe_noalloc(
+            ctypes.byref(_args(xo, gw, buf, E, h, I, k, *other)), stream)
+        assert st == capi.WR_OK, capi.status_str(st)
+        torch.cuda.synchronize()
+        for gv, wv, what in zip(got, want, ("out", "ids", "weights")):
+            assert torch.equal(gv, wv), f"replay {rep}: {what} differs from wr_fused_moe"
+    del g, buf
+    torch.cuda.empty_cache()

@@ -11,11 +11,17 @@
 
 Both land in warp_route/ so that the package directory is self-contained and
 travels with the source tree.  Run ``python warp-route_amd/build.py``.
+
+WR_HIPCC_FLAGS in the environment adds hipcc options to every HIP compile:
+the kernels' tuning macros (#ifndef WR_... in csrc/) are set that way, e.g.
+``WR_HIPCC_FLAGS=-DWR_ROUTER_IN_FFN=1 python warp-route_amd/build.py`` builds
+the single-token kernel with its router inside.  Tests assume the defaults.
 """
 from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import shlex
 import shutil
 import subprocess
 import sys
@@ -38,6 +44,7 @@ HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
+    *shlex.split(os.environ.get("WR_HIPCC_FLAGS", "")),
 ]
 HIP_SOURCES = ["wr_api.hip", "wr_kernels.hip", "wr_batched.hip", "wr_naive.hip"]
 PROBE_SOURCE = "wr_probe.hip"

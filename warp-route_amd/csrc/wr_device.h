@@ -330,6 +330,24 @@ __device__ __forceinline__ unsigned xcc_id() {
   return v & 15u;
 }
 
+// The dispatch id of the running kernel: the index of its dispatch packet in
+// its hardware queue (64-bit, one per launch, increasing along the queue; a
+// replayed graph's kernels get new ones), the same for every workgroup.
+extern "C" __device__ uint64_t wr_llvm_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+
+// A 64-bit tag of this kernel launch, the same in every workgroup of it: a
+// hash of the launch's (hardware queue address, dispatch id), bijective in
+// the dispatch id for a fixed queue, so no two launches on one queue share a
+// tag, and launches on different queues share one with probability 2^-64.
+__device__ __forceinline__ void launch_tag(uint32_t& lo, uint32_t& hi) {
+  const uint64_t d = wr_llvm_dispatch_id();
+  const uint64_t q = (uint64_t)(uintptr_t)__builtin_amdgcn_queue_ptr();
+  uint64_t t = (d + 1u) * 0x9E3779B97F4A7C15ull;
+  t ^= (q >> 4) * 0xC2B2AE3D27D4EB4Full;
+  lo = __builtin_amdgcn_readfirstlane((uint32_t)t);
+  hi = __builtin_amdgcn_readfirstlane((uint32_t)(t >> 32));
+}
+
 // Invalidate this CU's vector L1 and wait for it.  The CU's later loads then
 // fetch from L2.
 __device__ __forceinline__ void invalidate_l1() {

@@ -9,6 +9,17 @@
 
 #include "warp_route.h"
 
+// 1: the single-token kernel computes the router rows itself and publishes
+// them to its other blocks (wr_kernels.hip, route_and_select): one launch per
+// layer.  0 (the default): a router launch ahead of it, whose first block
+// also zeroes the hand-off's control words.  Measured on one box (layer us,
+// fp16 unless noted): DeepSeek 26.5 -> 27.3, DeepSeek MXFP4 19.1 -> 21.2, a
+// Mixtral tp8 shard 29.9 -> 30.9, Mixtral 115.7 -> 115.6: the in-kernel
+// publish and poll cost about what the kernel boundary does.
+#ifndef WR_ROUTER_IN_FFN
+#define WR_ROUTER_IN_FFN 0
+#endif
+
 namespace wr {
 
 struct Problem {
@@ -48,8 +59,9 @@ struct FusedWs {
   // counters, the wait-timeout flag, an unused word, kCounters XCD-rotation
   // masks (gate/up block b ORs bit (its XCD - b) mod 8 into mask
   // b mod kCounters), then kClasses claim counters of the gate/up chunks
-  // beyond the launched blocks (class b mod 8).  The router kernel of each
-  // single-token call zeroes them.
+  // beyond the launched blocks (class b mod 8).  The router launch of each
+  // single-token call zeroes them (with WR_ROUTER_IN_FFN, block 0 of the
+  // call's kernel, before it publishes its router slot).
   static constexpr int kCounters = 64;
   static constexpr int kClasses = 8;
   static constexpr int kCounterStride = 64;  // words (256 bytes)
@@ -57,7 +69,19 @@ struct FusedWs {
   static constexpr int kRotWord = kTimeoutWord + 2 * kCounterStride;
   static constexpr int kClaimWord = kRotWord + kCounters * kCounterStride;
   static constexpr int kCtrlWords = 2 * kCounters + 2 + kClasses;  // zeroed words, kCounterStride apart
-  static constexpr size_t kCtrlBytes = (size_t)kCtrlWords * kCounterStride * 4;
+  // WR_ROUTER_IN_FFN: router slots after the zeroed words, 16 bytes per
+  // expert: two 64-bit words {logit bits, tag half} carrying the tag of the
+  // call that wrote them (never zeroed: a slot counts only when it carries
+  // the reader's own call tag).  kSlotReplicas copies, kReplicaBytes apart (9
+  // cache lines, so that the copies start on different L2 channels); block b
+  // polls copy b mod kSlotReplicas, which spreads the polls of a whole grid.
+  static constexpr int kSlotWord = kCtrlWords * kCounterStride;
+  static constexpr int kSlotBytes = 16;
+  static constexpr int kSlotReplicas = 16;
+  static constexpr int kReplicaBytes = 1152;
+  static_assert(WR_MAX_EXPERTS * kSlotBytes <= kReplicaBytes, "a copy holds every slot");
+  static constexpr size_t kCtrlBytes =
+      (size_t)kSlotWord * 4 + (WR_ROUTER_IN_FFN ? (size_t)kSlotReplicas * kReplicaBytes : 0);
   // Single-token act rows: I rounded up to whole chunks of `cols` columns, the
   // columns one gate/up block computes (4 waves x rows per wave: 8 or 16).
   static constexpr int kMaxActCols = 16;

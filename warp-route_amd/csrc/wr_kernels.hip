@@ -4,7 +4,9 @@
 // token) computes the router dot product (src/fused_moe.cu:100-112); each
 // wave covers a quarter of the row, so one memory round trip covers it.
 // Every consumer then derives the top-K selection from the logits itself
-// (wave_select_topk: DPP max/sum and a 64-bit ballot).
+// (wave_select_topk: DPP max/sum and a 64-bit ballot).  Built with
+// WR_ROUTER_IN_FFN=1, the single-token kernel computes the router rows itself
+// instead (route_and_select), one launch per layer as in the reference.
 //
 // Single token (the decode hot path): k_fused_ffn, ONE launch whose first
 // blocks stream the selected experts' gate/up rows and write
@@ -205,9 +207,10 @@ struct XSplit {
 
 // grid (E, B), block 256.  Token b's logits go to logits[b * 64 + e] (padded
 // so that consumers can read all 64 with scalar loads).  Block (0, 0) also
-// zeroes the words zero[i * zstride], i < nzero <= kBlock (the fused kernel's
-// arrival counters, timeout flag and rotation masks), which the next kernel on
-// the stream reads.  With xs.hi != NULL, block (e, b) also writes its 1/E
+// zeroes the words zero[i * zstride], i < nzero <= kBlock (the single-token
+// kernel's arrival counters, timeout flag, rotation masks and claim
+// counters), which the next kernel on the stream reads.  With xs.hi != NULL,
+// block (e, b) also writes its 1/E
 // share of token b's split x (XSplit); every block of the token derives the
 // same exponent from the whole row.
 template <typename XT, int VEC>
@@ -589,6 +592,12 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 // keeps act dense, so the readers' loads stay fully coalesced.
 // ---------------------------------------------------------------------------
 struct Handoff {
+  unsigned* ctrl;       // the control block: FusedWs::kCtrlWords words zeroed at the start of
+                        // each call, FusedWs::kCounterStride words apart
+  uint64_t* slot;       // WR_ROUTER_IN_FFN: router slots, 2 words per expert (FusedWs::kSlotWord)
+  const float* gate_w;  // router matrix [E][h]; nullptr: the logits are read from `logits`
+  int nb;               // blocks in the grid
+  int rvec;             // router rows and x in 128-bit loads (else scalar)
   unsigned* cnt;        // FusedWs::kCounters counters, FusedWs::kCounterStride words apart
   unsigned* timeout;    // set to 1 if a wait expired (that block's rows are then NaN)
   unsigned* rot;        // FusedWs::kCounters rotation masks, FusedWs::kCounterStride words apart
@@ -600,6 +609,102 @@ struct Handoff {
   unsigned spin_limit;  // polls before a wait gives up
   unsigned wait_extra;  // added to every arrival target: 0, or (tests) a wait that cannot complete
 };
+
+// The router inside k_fused_ffn, so that a layer is one launch as in the
+// reference (src/fused_moe.cu:100-150 computes the logits inside its kernel).
+//
+// Block b computes router rows e = b, b + nb, ... < E with the router
+// kernel's arithmetic (router_partial, router_combine: the same bits), or
+// with gate_w == nullptr reads them from `logits` (written by an earlier
+// router launch), and publishes row e as slot e: the 64-bit words
+// {logit, tag lo} and {logit, tag hi}, where the tag is this launch's
+// (launch_tag), in each of FusedWs::kSlotReplicas copies.  Block 0 first
+// zeroes the control words of the hand-off (arrival counters, timeout word,
+// rotation masks, claim counters) and waits for those stores to complete.
+// Wave 0 of every block then polls the E slots of its copy until each
+// carries this launch's tag in both words, and every wave selects from the
+// logits read (wave_select_topk_reg).
+//
+// Why nothing needs resetting between calls: a slot written by an earlier
+// launch carries that launch's tag, never this one's, and any other bytes
+// match both 32-bit halves with probability 2^-64.  Why the control words are
+// zero when used: every block reads or updates them only after it has seen
+// slot 0, which block 0 publishes after its zero stores completed.  Why this
+// cannot deadlock: the blocks that compute rows are the lowest ids of the
+// grid (at most 64 of them), dispatched before any other, and they wait for
+// nothing before they publish.  The poll is bounded like the hand-off wait;
+// on expiry the block sets the timeout word and returns false (no
+// selection).  Every thread of the block must call it.
+template <typename XT>
+__device__ __forceinline__ bool route_and_select(const XT* __restrict__ x,
+                                                 const float* __restrict__ logits, const Geom& g,
+                                                 const Handoff& hs, TopK& t) {
+  __shared__ float s_part[kWavesPerBlock];
+  __shared__ float s_logit[kWave];
+  __shared__ int s_routed;
+  static_assert(FusedWs::kCtrlWords <= kBlock, "one thread zeroes each control word");
+  constexpr int kRepWords = FusedWs::kReplicaBytes / 8;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int q = (int)threadIdx.x / kWave;
+  uint32_t tlo, thi;
+  launch_tag(tlo, thi);
+  // Block 0's zero stores go out before its router loads, so that the wait
+  // for the loads covers them too.
+  if (blockIdx.x == 0 && (int)threadIdx.x < FusedWs::kCtrlWords)
+    __hip_atomic_store(hs.ctrl + threadIdx.x * FusedWs::kCounterStride, 0u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  for (int e = blockIdx.x; e < g.E; e += hs.nb) {  // block-uniform
+    if (hs.gate_w != nullptr) {
+      float unused;
+      const float* row = hs.gate_w + (int64_t)e * g.h;
+      const float p = hs.rvec ? router_partial<XT, 4>(row, x, g.h, q, false, unused)
+                              : router_partial<XT, 1>(row, x, g.h, q, false, unused);
+      if (lane == 0) s_part[q] = p;
+    }
+    if (e == 0) __builtin_amdgcn_s_waitcnt(0);  // this thread's zero store has completed
+    __syncthreads();
+    if (q == 0 && lane < FusedWs::kSlotReplicas) {  // lane r writes copy r
+      const float l = hs.gate_w != nullptr ? router_combine(s_part) : logits[e];
+      const uint64_t bits = __float_as_uint(l);
+      uint64_t* sp = hs.slot + lane * kRepWords + 2 * e;
+      __hip_atomic_store(sp, bits | ((uint64_t)tlo << 32), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(sp + 1, bits | ((uint64_t)thi << 32), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();  // s_part is reused by the next row
+  }
+  if (q == 0) {
+    const uint64_t* rep = hs.slot + (blockIdx.x % FusedWs::kSlotReplicas) * kRepWords;
+    float l = 0.0f;
+    unsigned spins = 0;
+    int ok_all = 1;
+    for (;;) {
+      bool ok = true;
+      if (lane < g.E) {
+        const uint64_t a = __hip_atomic_load(rep + 2 * lane, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t b = __hip_atomic_load(rep + 2 * lane + 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        ok = (uint32_t)(a >> 32) == tlo && (uint32_t)(b >> 32) == thi && (uint32_t)a == (uint32_t)b;
+        l = __uint_as_float((uint32_t)a);
+      }
+      if (__ballot(!ok) == 0) break;
+      if (++spins > hs.spin_limit) {
+        ok_all = 0;
+        if (lane == 0)
+          __hip_atomic_store(hs.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    s_logit[lane] = l;
+    if (lane == 0) s_routed = ok_all;
+  }
+  __syncthreads();
+  wave_select_topk_reg(s_logit[lane], g.E, g.k, g.renorm, t);
+  return s_routed != 0;
+}
 
 // The chunk gate/up block b computes: a permutation of each aligned group of
 // 8 LB blocks (LB = chunks per 128-byte act line).
@@ -1002,7 +1107,12 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   const int64_t act_row = FusedWs::act_row(g.I, COLS);
 
   TopK t;
+#if WR_ROUTER_IN_FFN
+  const bool routed = route_and_select<XT>(x, logits, g, hs, t);
+#else
   block_select_topk(logits, g.E, g.k, g.renorm, t);
+  constexpr bool routed = true;
+#endif
   // The x-in-LDS variant's buffer: the gate/up role's x copy (and, with
   // STG, its waves' scale bytes); the down role's scale copy with STG.
   static_assert(!STG || XL, "scale staging lives in the x-in-LDS variant's buffer");
@@ -1010,6 +1120,7 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
 
   if ((int)blockIdx.x < hs.n1b) {
     // ---- gate/up block ----
+    if (!routed) return;  // the slot wait expired (timeout word set); no arrival
     if (blockIdx.x == 0 && wave == 0) {
 #pragma unroll
       for (int kk = 0; kk < WR_MAX_TOPK; ++kk) {
@@ -1082,6 +1193,10 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   const int nrows = min(RPD, g.h - r0);
   const int nch = (g.I + kWave * VEC - 1) / (kWave * VEC);
   const int C = g.k * nch;
+  if (!routed) {  // the slot wait expired (timeout word set): NaN rows, no loads
+    if (wave == 0 && lane < nrows) out[r0 + lane] = to_out<XT>(__builtin_nanf(""));
+    return;
+  }
 
   // STG: every selected expert's block-scale bytes of rows r0 .. r0 + nrows,
   // [kk][j][I / 32], into lds_raw before the wait (they do not depend on act);
@@ -1383,10 +1498,16 @@ int gu_launch_blocks(const Problem& p, int n1, const void* kernel) {
   return n1;
 }
 
+// fold: the kernel computes the router rows (one launch per layer); else it
+// reads the logits an earlier router launch left in the workspace.
 template <typename WT, typename XT, int VEC, int RPW, int U1>
-hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
+hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
   const Geom g = make_geom(p);
   Handoff hs;
+  hs.ctrl = w.ctrl;
+  hs.slot = reinterpret_cast<uint64_t*>(w.ctrl + FusedWs::kSlotWord);
+  hs.gate_w = fold ? p.gate_w : nullptr;
+  hs.rvec = router_vec4(p) ? 1 : 0;
   hs.cnt = w.ctrl;
   hs.timeout = w.ctrl + FusedWs::kTimeoutWord;
   hs.rot = w.ctrl + FusedWs::kRotWord;
@@ -1420,6 +1541,7 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
         constexpr size_t kRaw = fused_raw_bytes<WT, XT, VEC, RPW, true, true>();
         if (p.h % 128 == 0 && p.I % 128 == 0 && p.I >= WR_F4_STG_MIN_I &&
             (size_t)p.k * RPD * (p.I / 32) <= kRaw) {
+          hs.nb = hs.n1 + n2;
           hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, true>),
                              dim3(hs.n1 + n2), dim3(kBlock), 0, s,
                              static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x),
@@ -1428,6 +1550,7 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
           return hipGetLastError();
         }
       }
+      hs.nb = hs.n1 + n2;
       hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, false>),
                          dim3(hs.n1 + n2), dim3(kBlock), 0, s,
                          static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x), w.logits,
@@ -1444,12 +1567,14 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, hipStream_t s) {
     const int n1b = gu_launch_blocks(p, hs.n1, reinterpret_cast<const void*>(kc));
     if (n1b < hs.n1) {
       hs.n1b = n1b;
+      hs.nb = hs.n1b + n2;
       hipLaunchKernelGGL(kc, dim3(hs.n1b + n2), dim3(kBlock), 0, s,
                          static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x), w.logits,
                          w.act, static_cast<XT*>(p.out), p.topk_ids, p.topk_w, g, hs);
       return hipGetLastError();
     }
   }
+  hs.nb = hs.n1 + n2;
   hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, false, false>),
                      dim3(hs.n1 + n2), dim3(kBlock), 0, s, static_cast<const WT*>(p.wbuf),
                      static_cast<const XT*>(p.x), w.logits, w.act, static_cast<XT*>(p.out),
@@ -1467,20 +1592,20 @@ constexpr int fused_u1() {
 }
 
 template <typename WT, typename XT, int VEC>
-hipError_t fused_t(const Problem& p, const FusedWs& w, hipStream_t s) {
-  if (fused_rpw(p) == 4) return fused_rpw_t<WT, XT, VEC, 4, fused_u1<WT, 4>()>(p, w, s);
-  return fused_rpw_t<WT, XT, VEC, 2, fused_u1<WT, 2>()>(p, w, s);
+hipError_t fused_t(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
+  if (fused_rpw(p) == 4) return fused_rpw_t<WT, XT, VEC, 4, fused_u1<WT, 4>()>(p, w, fold, s);
+  return fused_rpw_t<WT, XT, VEC, 2, fused_u1<WT, 2>()>(p, w, fold, s);
 }
 
 template <typename WT, typename XT, int VEC>
-hipError_t ffn_t(const Problem& p, const FusedWs& w, hipStream_t s) {
+hipError_t ffn_t(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
   constexpr int RPW = WR_GU_RPW, RPD = WR_DN_RPD;
   // fp8: half the chunks in flight (16 fp32 x values per chunk and lane);
   // MXFP4: one chunk (32 values), and one chunk per down tile.
   constexpr bool kFp4 = std::is_same<WT, fp4x2>::value;
   constexpr int U1 = kFp4 ? 1 : (std::is_same<WT, fp8w>::value ? WR_GU_U / 2 : WR_GU_U);
   constexpr int UD = kFp4 ? 1 : WR_DN_U;
-  if (p.B == 1) return fused_t<WT, XT, VEC>(p, w, s);
+  if (p.B == 1) return fused_t<WT, XT, VEC>(p, w, fold, s);
   const Geom g = make_geom(p);
   const WT* wb = static_cast<const WT*>(p.wbuf);
   const int nw1 = waves_for(p.k * ((p.I + RPW - 1) / RPW), p.B);
@@ -1497,19 +1622,19 @@ hipError_t ffn_t(const Problem& p, const FusedWs& w, hipStream_t s) {
 }
 
 template <typename WT, typename XT>
-hipError_t ffn_w(const Problem& p, const FusedWs& w, hipStream_t s) {
+hipError_t ffn_w(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
   constexpr int V = wvec_width<WT>(), V1 = wvec_scalar<WT>();
-  return p.vec == V ? ffn_t<WT, XT, V>(p, w, s) : ffn_t<WT, XT, V1>(p, w, s);
+  return p.vec == V ? ffn_t<WT, XT, V>(p, w, fold, s) : ffn_t<WT, XT, V1>(p, w, fold, s);
 }
 
 template <typename XT>
-hipError_t ffn_x(const Problem& p, const FusedWs& w, hipStream_t s) {
+hipError_t ffn_x(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
   switch (p.wdt) {
-    case WR_F16: return ffn_w<f16, XT>(p, w, s);
-    case WR_BF16: return ffn_w<bf16w, XT>(p, w, s);
-    case WR_FP8_E4M3: return ffn_w<fp8w, XT>(p, w, s);
-    case WR_MXFP4: return ffn_w<fp4x2, XT>(p, w, s);
-    default: return ffn_w<float, XT>(p, w, s);
+    case WR_F16: return ffn_w<f16, XT>(p, w, fold, s);
+    case WR_BF16: return ffn_w<bf16w, XT>(p, w, fold, s);
+    case WR_FP8_E4M3: return ffn_w<fp8w, XT>(p, w, fold, s);
+    case WR_MXFP4: return ffn_w<fp4x2, XT>(p, w, fold, s);
+    default: return ffn_w<float, XT>(p, w, fold, s);
   }
 }
 
@@ -1524,16 +1649,20 @@ hipError_t run_route(const Problem& p, hipStream_t s) {
                          : logits_t<float>(p, w.logits, zero, nz, zs, s);
 }
 
-// The expert FFN from the logits run_route left in the workspace.
-hipError_t run_ffn_only(const Problem& p, hipStream_t s) {
+// The expert FFN from the logits run_route left in the workspace (fold =
+// false), or for one token with the router inside the FFN kernel.
+hipError_t run_ffn_only(const Problem& p, bool fold, hipStream_t s) {
   const FusedWs w = FusedWs::carve(p.ws, p.E, p.I, p.k, p.B);
-  return p.adt == WR_F16 ? ffn_x<f16>(p, w, s) : ffn_x<float>(p, w, s);
+  return p.adt == WR_F16 ? ffn_x<f16>(p, w, fold, s) : ffn_x<float>(p, w, fold, s);
 }
 
+// With WR_ROUTER_IN_FFN, one token takes one launch.  Otherwise the router
+// launch, then the FFN kernel(s).
 hipError_t run_ffn(const Problem& p, hipStream_t s) {
+  if (WR_ROUTER_IN_FFN && p.B == 1) return run_ffn_only(p, true, s);
   const hipError_t err = run_route(p, s);
   if (err != hipSuccess) return err;
-  return run_ffn_only(p, s);
+  return run_ffn_only(p, false, s);
 }
 
 template <typename XT>
@@ -1563,7 +1692,7 @@ hipError_t launch_fused(const Problem& p, hipStream_t s) { return run_ffn(p, s);
 
 hipError_t launch_fused_route(const Problem& p, hipStream_t s) { return run_route(p, s); }
 
-hipError_t launch_fused_ffn(const Problem& p, hipStream_t s) { return run_ffn_only(p, s); }
+hipError_t launch_fused_ffn(const Problem& p, hipStream_t s) { return run_ffn_only(p, false, s); }
 
 hipError_t launch_logits_split(const Problem& p, float* logits, f16* x_hi, f16* x_lo,
                                int32_t* x_exp, unsigned* amax, int split_bf16, hipStream_t s) {
