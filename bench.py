@@ -22,6 +22,8 @@ bounded sample of the same layer.
   python bench.py --op naive       # the naive multi-kernel path, with fused beside it
   python bench.py --read-probe     # read-only streaming ceiling over the same bytes
   python bench.py --throughput     # batched vs a loop of single-token calls (Mixtral, DBRX)
+  python bench.py --timeline 20    # per-phase timeline of the single-token kernel; needs
+                                   # WR_HIPCC_FLAGS=-DWR_TIMELINE=1 python warp-route_amd/build.py
 
 The headline line also carries roofline.read_ceiling: the best rate of a
 plain read-only streaming kernel (libwr_probe.so) over exactly the selected
@@ -173,6 +175,64 @@ def ffn_kernel_us(layers, cfg, steps: int, warmup: int) -> float:
         e1.record()
     torch.cuda.synchronize()
     return statistics.fmean(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3
+
+
+TL_EVENTS = 8
+
+
+def timeline_summary(step, n_calls: int) -> dict:
+    """Per-phase timeline of the single-token kernel from its per-workgroup
+    records (include/wr_timeline.h; the library must be built with
+    WR_HIPCC_FLAGS=-DWR_TIMELINE=1).  Each of n_calls calls (layers rotating
+    as in the timed region, each after the previous call's stream drained)
+    gives one record set; every figure is in microseconds from the first
+    workgroup's start, as the median over the calls of that call's statistic."""
+    import ctypes
+    import numpy as np
+    import torch
+    from warp_route import capi
+    lib = capi.lib()
+    khz = lib.wr_timeline_clock_khz()
+    buf = (ctypes.c_uint64 * (65536 * TL_EVENTS))()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rows = []
+    for i in range(n_calls):
+        step(i)
+        n = lib.wr_timeline_read(buf, 65536, stream)
+        if n == -1:
+            raise RuntimeError("the library was built without WR_TIMELINE: rebuild with "
+                               "WR_HIPCC_FLAGS=-DWR_TIMELINE=1 python warp-route_amd/build.py")
+        if n < 0 or khz <= 0:
+            raise RuntimeError(f"wr_timeline_read: {n}, clock {khz} kHz")
+        rec = np.frombuffer(buf, dtype=np.uint64, count=n * TL_EVENTS).reshape(n, TL_EVENTS)
+        t = rec[:, :5].astype(np.int64)
+        t = (t - t[:, 0].min()) / (khz / 1e3)  # microseconds
+        gu = rec[:, 6] == 0
+        dn = ~gu
+
+        def q(v, p):
+            return float(np.percentile(v, p)) if len(v) else float("nan")
+        rows.append({
+            "gateup_blocks": int(gu.sum()), "down_blocks": int(dn.sum()),
+            "gu_start_p50": q(t[gu, 0], 50), "gu_start_max": q(t[gu, 0], 100),
+            "gu_selection_p50": q(t[gu, 1] - t[gu, 0], 50),
+            "gu_life_p50": q(t[gu, 3] - t[gu, 0], 50),
+            "gu_end_p50": q(t[gu, 3], 50),
+            "gu_last_arrival": q(t[gu, 3], 100),
+            "dn_start_min": q(t[dn, 0], 0), "dn_start_p50": q(t[dn, 0], 50),
+            "dn_start_max": q(t[dn, 0], 100),
+            "dn_selection_p50": q(t[dn, 1] - t[dn, 0], 50),
+            "dn_release_min": q(t[dn, 3], 0), "dn_release_p50": q(t[dn, 3], 50),
+            "dn_release_max": q(t[dn, 3], 100),
+            "dn_after_release_p50": q(t[dn, 4] - t[dn, 3], 50),
+            "dn_after_release_max": q(t[dn, 4] - t[dn, 3], 100),
+            "kernel_end": float(max(t[gu, 3].max() if gu.any() else 0.0,
+                                    t[dn, 4].max() if dn.any() else 0.0)),
+        })
+    out = {k: round(float(np.median([r[k] for r in rows])), 2) for k in rows[0]}
+    out["calls"] = n_calls
+    out["clock_khz"] = int(khz)
+    return out
 
 
 def _timed(step, steps: int, warmup: int) -> float:
@@ -529,6 +589,9 @@ def main() -> int:
                     help="time one token through this many layers instead")
     ap.add_argument("--graph", action="store_true",
                     help="with --stack: also replay the step from a captured HIP graph")
+    ap.add_argument("--timeline", type=int, default=0, metavar="N",
+                    help="per-phase timeline of the single-token kernel over N calls instead "
+                         "(needs the library built with WR_HIPCC_FLAGS=-DWR_TIMELINE=1)")
     ap.add_argument("--tp-shard", type=int, default=1, metavar="G",
                     help="time one GPU's share of a G-way tensor-parallel split over the "
                          "intermediate dimension (I/G rows of gate/up, I/G columns of down)")
@@ -595,6 +658,15 @@ def main() -> int:
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+
+    if args.timeline:
+        print(json.dumps({
+            "metric": "single-token kernel phase timeline (us from the first workgroup's start)",
+            "config": {"workload": f"{cfg.name} MoE layer, decode batch 1"
+                       + (f", one of {G} tensor-parallel shards over I" if G > 1 else ""),
+                       "weight_dtype": args.weights, "layers_rotated": args.layers},
+            "timeline": timeline_summary(step, args.timeline)}), flush=True)
+        return 0
 
     # Whole timed region: K back-to-back calls between two events on the
     # stream the kernels run on (the current HIP stream).

@@ -323,3 +323,17 @@ def test_gate_topk_requires_outputs():
     a.topk_weights = None
     assert capi.call("wr_gate_topk", a) == capi.WR_EINVAL_NULL
     assert capi.lib().wr_fused_moe(None, None) == capi.WR_EINVAL_NULL
+
+
+def test_timeline_hook_is_exported_and_off_by_default():
+    """include/wr_timeline.h: both functions are exported; a default build
+    (no WR_TIMELINE) records nothing and says so before any HIP call."""
+    import re as _re
+    text = open(os.path.join(ROOT, "include", "wr_timeline.h")).read()
+    names = _re.findall(r"WR_TL_API\s+[\w\s\*]+?\b(wr_\w+)\s*\(", text)
+    assert sorted(names) == ["wr_timeline_clock_khz", "wr_timeline_read"]
+    lib = capi.lib()
+    for name in names:
+        assert hasattr(lib, name), name
+    buf = (ctypes.c_uint64 * 8)()
+    assert lib.wr_timeline_read(buf, 1, None) == -1

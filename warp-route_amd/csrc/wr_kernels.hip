@@ -34,6 +34,7 @@
 
 #include "wr_device.h"
 #include "wr_internal.h"
+#include "wr_timeline.h"
 
 // Single-token gate/up chunk slots beyond one round of resident blocks, up to
 // this percentage of the round, are claimed by the launched blocks instead of
@@ -608,7 +609,32 @@ struct Handoff {
   int chunks;           // k * bpk
   unsigned spin_limit;  // polls before a wait gives up
   unsigned wait_extra;  // added to every arrival target: 0, or (tests) a wait that cannot complete
+#if WR_TIMELINE
+  uint64_t* tl;         // per-block records (include/wr_timeline.h)
+#endif
 };
+
+// WR_TIMELINE builds: thread 0 stores the wall clock as record `ev` of its
+// workgroup (include/wr_timeline.h), a plain store that nothing waits for.
+#if WR_TIMELINE
+#define WR_TL_MARK(hs, ev)                                                              \
+  do {                                                                                  \
+    if (threadIdx.x == 0 && blockIdx.x < WR_TIMELINE_MAX_BLOCKS)                        \
+      (hs).tl[(size_t)blockIdx.x * WR_TIMELINE_EVENTS + (ev)] = (uint64_t)wall_clock64(); \
+  } while (0)
+#define WR_TL_SET(hs, ev, v)                                                     \
+  do {                                                                           \
+    if (threadIdx.x == 0 && blockIdx.x < WR_TIMELINE_MAX_BLOCKS)                 \
+      (hs).tl[(size_t)blockIdx.x * WR_TIMELINE_EVENTS + (ev)] = (uint64_t)(v);   \
+  } while (0)
+#else
+#define WR_TL_MARK(hs, ev) \
+  do {                     \
+  } while (0)
+#define WR_TL_SET(hs, ev, v) \
+  do {                       \
+  } while (0)
+#endif
 
 // The router inside k_fused_ffn, so that a layer is one launch as in the
 // reference (src/fused_moe.cu:100-150 computes the logits inside its kernel).
@@ -1089,9 +1115,17 @@ constexpr size_t fused_raw_bytes() {
   }
 }
 
+// WR_TIMELINE builds hold the claiming variant to 4 blocks per CU, the
+// occupancy its default build has, so that the timeline shows the launch
+// configuration the default build runs.
+#if WR_TIMELINE
+#define WR_FUSED_BOUNDS __launch_bounds__(kBlock, CLAIM ? 4 : 1)
+#else
+#define WR_FUSED_BOUNDS __launch_bounds__(kBlock)
+#endif
 template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2, bool XL,
           bool STG, bool CLAIM = false>
-__global__ __launch_bounds__(kBlock) void k_fused_ffn(
+__global__ WR_FUSED_BOUNDS void k_fused_ffn(
     const WT* __restrict__ wbuf, const XT* __restrict__ x, const float* __restrict__ logits,
     float* act, XT* __restrict__ out, int32_t* __restrict__ ids_out, float* __restrict__ w_out,
     Geom g, Handoff hs) {
@@ -1106,12 +1140,22 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
                       : (int)threadIdx.x / kWave;
   const int64_t act_row = FusedWs::act_row(g.I, COLS);
 
+  WR_TL_MARK(hs, 0);
   TopK t;
 #if WR_ROUTER_IN_FFN
   const bool routed = route_and_select<XT>(x, logits, g, hs, t);
 #else
   block_select_topk(logits, g.E, g.k, g.renorm, t);
   constexpr bool routed = true;
+#endif
+  WR_TL_MARK(hs, 1);
+#if WR_TIMELINE
+  {
+    unsigned hwid;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));
+    WR_TL_SET(hs, 5, (uint64_t)xcc_id() | ((uint64_t)hwid << 32));
+    WR_TL_SET(hs, 6, (int)blockIdx.x < hs.n1b ? 0u : 1u);
+  }
 #endif
   // The x-in-LDS variant's buffer: the gate/up role's x copy (and, with
   // STG, its waves' scale bytes); the down role's scale copy with STG.
@@ -1181,6 +1225,7 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
         if (v >= hs.n1) break;
       }
     }
+    WR_TL_MARK(hs, 3);
     return;
   }
 
@@ -1268,6 +1313,7 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
       }
     }
   }
+  WR_TL_MARK(hs, 2);
   if constexpr (kFp8) {
     // Published to the block by the __syncthreads after the wait below.
     const int i = threadIdx.x, kk = i / RPD, j = i % RPD;
@@ -1312,6 +1358,7 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
   }
   if constexpr (STG) __builtin_amdgcn_s_waitcnt(0);  // this wave's scale copies have landed
   __syncthreads();
+  WR_TL_MARK(hs, 3);
 
   float acc[RPD];
 #pragma unroll
@@ -1371,6 +1418,7 @@ __global__ __launch_bounds__(kBlock) void k_fused_ffn(
     out[r0 + lane] = to_out<XT>(expired ? __builtin_nanf("")
                                         : (part[0][lane] + part[1][lane]) +
                                               (part[2][lane] + part[3][lane]));
+  WR_TL_MARK(hs, 4);
 }
 
 // ---------------------------------------------------------------------------
@@ -1498,12 +1546,37 @@ int gu_launch_blocks(const Problem& p, int n1, const void* kernel) {
   return n1;
 }
 
+#if WR_TIMELINE
+#define WR_TL_GRID(n) g_tl_blocks.store((n), std::memory_order_relaxed)
+#else
+#define WR_TL_GRID(n) \
+  do {                \
+  } while (0)
+#endif
+
+#if WR_TIMELINE
+// The timeline records of the last single-token launch on each device, and
+// that launch's workgroup count.
+static __device__ uint64_t tl_buf[(size_t)WR_TIMELINE_MAX_BLOCKS * WR_TIMELINE_EVENTS];
+std::atomic<int64_t> g_tl_blocks{0};
+
+uint64_t* tl_ptr() {
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(tl_buf)) != hipSuccess) return nullptr;
+  return static_cast<uint64_t*>(p);
+}
+#endif
+
 // fold: the kernel computes the router rows (one launch per layer); else it
 // reads the logits an earlier router launch left in the workspace.
 template <typename WT, typename XT, int VEC, int RPW, int U1>
 hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
   const Geom g = make_geom(p);
   Handoff hs;
+#if WR_TIMELINE
+  hs.tl = tl_ptr();
+  if (hs.tl == nullptr) return hipErrorInvalidSymbol;
+#endif
   hs.ctrl = w.ctrl;
   hs.slot = reinterpret_cast<uint64_t*>(w.ctrl + FusedWs::kSlotWord);
   hs.gate_w = fold ? p.gate_w : nullptr;
@@ -1542,6 +1615,7 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
         if (p.h % 128 == 0 && p.I % 128 == 0 && p.I >= WR_F4_STG_MIN_I &&
             (size_t)p.k * RPD * (p.I / 32) <= kRaw) {
           hs.nb = hs.n1 + n2;
+          WR_TL_GRID(hs.nb);
           hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, true>),
                              dim3(hs.n1 + n2), dim3(kBlock), 0, s,
                              static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x),
@@ -1551,6 +1625,7 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
         }
       }
       hs.nb = hs.n1 + n2;
+      WR_TL_GRID(hs.nb);
       hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, false>),
                          dim3(hs.n1 + n2), dim3(kBlock), 0, s,
                          static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x), w.logits,
@@ -1568,6 +1643,7 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
     if (n1b < hs.n1) {
       hs.n1b = n1b;
       hs.nb = hs.n1b + n2;
+      WR_TL_GRID(hs.nb);
       hipLaunchKernelGGL(kc, dim3(hs.n1b + n2), dim3(kBlock), 0, s,
                          static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x), w.logits,
                          w.act, static_cast<XT*>(p.out), p.topk_ids, p.topk_w, g, hs);
@@ -1575,6 +1651,7 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
     }
   }
   hs.nb = hs.n1 + n2;
+  WR_TL_GRID(hs.nb);
   hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, false, false>),
                      dim3(hs.n1 + n2), dim3(kBlock), 0, s, static_cast<const WT*>(p.wbuf),
                      static_cast<const XT*>(p.x), w.logits, w.act, static_cast<XT*>(p.out),
@@ -1707,3 +1784,32 @@ hipError_t launch_batched(const Problem& p, hipStream_t s) {
 }
 
 }  // namespace wr
+
+extern "C" WR_TL_API int64_t wr_timeline_clock_khz(void) {
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+    return -2;
+  return khz;
+}
+
+extern "C" WR_TL_API int64_t wr_timeline_read(uint64_t* rec, int64_t max_blocks, void* stream) {
+#if WR_TIMELINE
+  if (rec == nullptr || max_blocks < 0) return -2;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t n = std::min<int64_t>(
+      std::min<int64_t>(wr::g_tl_blocks.load(std::memory_order_relaxed), WR_TIMELINE_MAX_BLOCKS),
+      max_blocks);
+  uint64_t* src = wr::tl_ptr();
+  if (src == nullptr || hipStreamSynchronize(s) != hipSuccess) return -2;
+  if (n > 0 && hipMemcpy(rec, src, (size_t)n * WR_TIMELINE_EVENTS * sizeof(uint64_t),
+                         hipMemcpyDeviceToHost) != hipSuccess)
+    return -2;
+  return n;
+#else
+  (void)rec;
+  (void)max_blocks;
+  (void)stream;
+  return -1;
+#endif
+}
