@@ -137,17 +137,12 @@ def test_workspace_bytes():
     # word, 64 XCD-rotation masks and 8 gate/up claim counters, one 256-byte
     # line each) + 64 fp32 logits per token (E padded to 64) + act: single
     # token k rows of I rounded up to 16 columns, B > 1 B*k*I; fp32, rounded up
-    # to 256 bytes; single token also x as 4 fp8 terms with a scale byte per
-    # term and 32 elements, rounded up to 256 bytes.
+    # to 256 bytes.
     ctrl = 138 * 256
-
-    def xq(h):
-        return (4 * h + 4 * ((h + 31) // 32) + 255) // 256 * 256
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 4096, 14336, 2, 1) == (
-        ctrl + 256 + 2 * 14336 * 4 + xq(4096))
-    assert xq(4096) == 16896
+        ctrl + 256 + 2 * 14336 * 4)
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 64, 100, 3, 1) == (
-        ctrl + 256 + 1536 + 512)  # 3 * 112 * 4 = 1344 -> 1536; 4 * 64 + 4 * 2 -> 512
+        ctrl + 256 + 1536)  # 3 * 112 * 4 = 1344 -> 1536
     # batched, B > 1: the larger of the per-token layout above and the
     # grouped MFMA layout: logits, x as two fp16 terms and its per-token
     # exponents, one act-maximum word per pair on its own 256-byte line, five

@@ -215,10 +215,8 @@ def test_single_token_kernels_keep_four_waves_per_simd(kernels):
         r"k_fused_ffnI(DF16_|NS_5bf16wE)(DF16_|f)Li8E|k_fused_ffnINS_5fp4x2E(DF16_|f)Li32E", k)}
     # 3 weight types x 2 x types x 2 RPW x 2 x paths, plus the MXFP4 kernels
     # with staged block scales (x in LDS, 4 rows per wave) for the 2 x types,
-    # plus the claiming register-path variants of f16 and bf16 (2 x 2 x 2),
-    # plus the MXFP4 kernels whose gate/up blocks run on the MFMA (2 x types,
-    # with and without staged scales)
-    assert len(fused) == 38, sorted(fused)
+    # plus the claiming register-path variants of f16 and bf16 (2 x 2 x 2)
+    assert len(fused) == 34, sorted(fused)
     assert all(n > 0 for n in fused.values()), "kernel descriptors not found"
     over = {k: n for k, n in fused.items() if n > 128}
     assert not over, f"single-token kernels allocating more than 128 VGPRs: {over}"
@@ -238,7 +236,7 @@ def test_register_path_kernels_hold_no_per_thread_arrays_in_lds(kernels):
         return 1024 + (32768 if pre else 0)
 
     reg = {k: v.get("group_segment_fixed_size", 0) for k, v in kernels.items()
-           if ("k_fused_ffn" in k and re.search(r"ELb0ELb0ELb[01]ELb0EEEv", k)) or "k_gateup" in k
+           if ("k_fused_ffn" in k and re.search(r"ELb0ELb0ELb[01]EEEv", k)) or "k_gateup" in k
            or "k_down" in k}
     assert len(reg) >= 16, sorted(reg)
     big = {k: n for k, n in reg.items() if n > limit(k)}
@@ -246,18 +244,17 @@ def test_register_path_kernels_hold_no_per_thread_arrays_in_lds(kernels):
 
 
 def test_x_in_lds_kernels_fit_four_blocks_per_cu(kernels):
-    # The x-in-LDS single-token kernels (k_fused_ffn<..., true, STG, false, MF>,
-    # MF: gate/up blocks on the MFMA with the x terms in the buffer) size their
+    # The x-in-LDS single-token kernels (k_fused_ffn<..., true, STG>) size their
     # buffer for 4 blocks of 4 waves per CU: at most 40 KB of the CU's 160 KB
     # each.  The MXFP4 staged-scale kernels fill that budget (their down
     # blocks stage one more weight chunk per wave in the x copy's bytes).
     xl = {k: v.get("group_segment_fixed_size", 0) for k, v in kernels.items()
-          if "k_fused_ffn" in k and re.search(r"ELb1ELb[01]ELb0ELb[01]EEEv", k)}
+          if "k_fused_ffn" in k and re.search(r"ELb1ELb[01]ELb0EEEv", k)}
     assert len(xl) >= 8, sorted(xl)
     assert all(n > 0 for n in xl.values()), xl
     big = {k: n for k, n in xl.items() if n > 40 * 1024}
     assert not big, f"x-in-LDS kernels over 40 KB of LDS: {big}"
-    stg = [n for k, n in xl.items() if re.search(r"ELb1ELb1ELb0ELb[01]EEEv", k)]
+    stg = [n for k, n in xl.items() if re.search(r"ELb1ELb1ELb0EEEv", k)]
     assert stg and min(stg) > 36 * 1024, f"staged-scale kernels without their chunk buffer: {stg}"
 
 

@@ -105,7 +105,7 @@ LOWP = [
     (8, 6144, 512, 2, MX4, False),    # 3 KB code rows: x staged in LDS up to h = 6144
     (4, 6176, 256, 2, MX4, True),     # h just above the MXFP4 LDS copy: x from registers
     (5, 96, 64, 2, MX4, False),       # three and two blocks per row, k == 2 of 5
-    # MXFP4 with h a multiple of 2048 (at most 4096): gate/up blocks on the MFMA
+    # MXFP4 at h = 2048 and 4096 (x staged in LDS with the block scales)
     (8, 2048, 256, 2, MX4, False),
     (64, 2048, 128, 6, MX4, True),
     (16, 4096, 512, 4, MX4, False),
@@ -281,13 +281,12 @@ def test_batched_parity(cuda, cfg, B):
                                            (1.0, F16), (16.0, F16)],
                          ids=["x1", "x1e5", "x1e-6", "x3e-30", "xf16", "xf16-16"])
 @pytest.mark.parametrize("h", [2048, 4096])
-def test_mxfp4_mfma_gateup_x_range(cuda, h, scale, x_dtype):
-    """MXFP4 gate/up blocks on the MFMA take x as 4 fp8 terms with a
-    power-of-two scale per term and 32 elements: the split follows x's own
-    magnitude, so the layer matches the oracle at the usual bar for x scaled
-    far outside fp8's range (and near fp32's bottom), and for fp16 x (scaled
-    by 16 at most: the fp16 output grows with the square of x).  The router is
-    scaled inversely so that the routing stays the same."""
+def test_mxfp4_single_token_x_range(cuda, h, scale, x_dtype):
+    """MXFP4 single-token layers at h = 2048 and 4096 match the oracle at the
+    usual bar for x scaled far from 1 (up to 1e5, down to near fp32's bottom)
+    and for fp16 x (scaled by 16 at most: the fp16 output grows with the
+    square of x).  The router is scaled inversely so that the routing stays
+    the same."""
     E, I, k, rn = 8, 512, 2, True
     x, gw, buf = make_layer(E, h, I, MX4, router_std=h ** -0.5, expert_std=0.05, seed=7,
                             device=cuda)
@@ -295,7 +294,7 @@ def test_mxfp4_mfma_gateup_x_range(cuda, h, scale, x_dtype):
     gw = (gw / scale).contiguous()
     assert torch.isfinite(x).all() and bool((x != 0).any())
     ref = oracle_token(x, gw, buf, E, h, I, k, rn)
-    print(f"[gpu] mxfp4 mfma gate/up h={h} x*{scale} {x_dtype} robust={ref['robust']}", flush=True)
+    print(f"[gpu] mxfp4 single token h={h} x*{scale} {x_dtype} robust={ref['robust']}", flush=True)
     ids = torch.empty(k, dtype=torch.int32, device=cuda)
     ws = torch.empty(k, dtype=torch.float32, device=cuda)
     out = F.fused_moe(x, gw, buf, E, h, I, k, rn, ids, ws)

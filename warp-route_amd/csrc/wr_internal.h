@@ -86,15 +86,10 @@ struct FusedWs {
   // columns one gate/up block computes (4 waves x rows per wave: 8 or 16).
   static constexpr int kMaxActCols = 16;
 
-  // Single token: x as kXTerms fp8 terms with block scales for the MXFP4
-  // gate/up MFMAs ([kXTerms][h] codes, then [kXTerms][h / 32] scale bytes).
-  static constexpr int kXTerms = 4;
-
   unsigned* ctrl;  // kCtrlBytes
   float* logits;   // [B][WR_MAX_EXPERTS]: token b's E logits, padded to 64
   float* act;      // B == 1: [k][act_row(I, cols)]; B > 1: [B][k][I].
                    // Values are already scaled by the gate weight.
-  uint8_t* xq;     // B == 1: the x terms (xq_bytes(h)); B > 1: NULL
 
   __host__ __device__ static int64_t act_row(int I, int cols) {
     return (int64_t)((I + cols - 1) / cols) * cols;
@@ -102,25 +97,19 @@ struct FusedWs {
   static size_t act_floats(int I, int k, int B) {
     return B == 1 ? (size_t)k * act_row(I, kMaxActCols) : (size_t)B * k * I;
   }
-  static size_t xq_bytes(int h) {
-    return align_up((size_t)kXTerms * h + (size_t)kXTerms * ((h + 31) / 32), kWsAlign);
-  }
-  static size_t bytes(int E, int h, int I, int k, int B) {
+  static size_t bytes(int E, int I, int k, int B) {
     (void)E;
     return kCtrlBytes + (size_t)B * WR_MAX_EXPERTS * 4 +
-           align_up(act_floats(I, k, B) * 4, kWsAlign) + (B == 1 ? xq_bytes(h) : 0);
+           align_up(act_floats(I, k, B) * 4, kWsAlign);
   }
-  static FusedWs carve(char* ws, int E, int h, int I, int k, int B) {
+  static FusedWs carve(char* ws, int E, int I, int k, int B) {
     FusedWs w;
     w.ctrl = reinterpret_cast<unsigned*>(ws);
     w.logits = reinterpret_cast<float*>(ws + kCtrlBytes);
-    const size_t act_off = kCtrlBytes + (size_t)B * WR_MAX_EXPERTS * 4;
-    w.act = reinterpret_cast<float*>(ws + act_off);
-    w.xq = B == 1 ? reinterpret_cast<uint8_t*>(ws + act_off +
-                                               align_up(act_floats(I, k, B) * 4, kWsAlign))
-                  : nullptr;
+    w.act = reinterpret_cast<float*>(ws + kCtrlBytes + (size_t)B * WR_MAX_EXPERTS * 4);
     (void)E;
-    (void)h;
+    (void)I;
+    (void)k;
     return w;
   }
 };

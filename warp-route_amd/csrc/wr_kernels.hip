@@ -123,11 +123,6 @@
 #ifndef WR_F4_U2
 #define WR_F4_U2 1   // column chunks per down tile
 #endif
-// MXFP4 single-token gate/up blocks on the block-scaled MFMA (gateup_item_mf)
-// where h allows it (a multiple of 2048, at most 4096); 0: the VALU decode.
-#ifndef WR_F4_MFMA
-#define WR_F4_MFMA 1
-#endif
 // MXFP4 block scales staged in LDS (x-in-LDS variant) from this intermediate
 // size up; smaller layers keep the per-load scale bytes.
 #ifndef WR_F4_STG_MIN_I
@@ -144,7 +139,6 @@
 namespace wr {
 
 constexpr int kBlock = 256;  // 4 waves
-constexpr int kXTerms = FusedWs::kXTerms;
 constexpr int kWavesPerBlock = kBlock / kWave;
 
 // ---------------------------------------------------------------------------
@@ -212,53 +206,6 @@ struct XSplit {
   int bf16;
 };
 
-// x of one token as kXTerms fp8 E4M3 terms with one E8M0 scale per term and
-// 32-element block, for the MXFP4 gate/up MFMAs: q[t][h] codes, s[t][h / 32]
-// scale bytes.  q == NULL: no terms.
-struct XTerms {
-  uint8_t* q;
-  uint8_t* s;
-};
-
-// Block e of the router writes the terms of MX blocks [e cs, (e + 1) cs) of
-// token 0's x, cs = ceil(h / 32 / E): half-wave j of the block takes one
-// 32-element block, lane i its element i.  Term t of a block is
-// q_t = e4m3(r_t 2^-e_t) with 2^e_t = the power of two that brings the
-// block's max |r_t| into [128, 256) (scale byte e_t + 127, at least 1), and
-// r_(t+1) = r_t - q_t 2^e_t, r_0 = x; q_t 2^e_t and the subtraction are exact,
-// whatever the conversion's rounding, so after T terms x = sum_t q_t 2^e_t +
-// r_T exactly, and |r_T| <= max |x of the block| 2^(-4T) or so (4 terms:
-// 1.8e-6 of the block's largest element at most, 3.5e-7 relative in l2 over
-// N(0, 1) values).  A block scale is the 32-element max of its term, as the
-// MFMA's block scales take it.
-template <typename XT>
-__device__ __forceinline__ void x_terms(const XT* __restrict__ x, int h, int E, int e,
-                                        const XTerms& xt) {
-  const int nblk = h / 32;
-  const int cs = (nblk + E - 1) / E;
-  const int b0 = e * cs, b1 = min(nblk, b0 + cs);
-  const int j = threadIdx.x & 31;
-  for (int base = b0; base < b1; base += kBlock / 32) {  // block-uniform
-    const int blk = base + (int)threadIdx.x / 32;
-    const bool mine = blk < b1;                          // half-wave-uniform
-    float r = mine ? (float)x[blk * 32 + j] : 0.0f;
-#pragma unroll
-    for (int t = 0; t < kXTerms; ++t) {
-      float m = row_max(fabsf(r));        // over the 16-lane row
-      m = fmaxf(m, __shfl_xor(m, 16));    // over the 32-lane half-wave
-      int pe = 0;
-      if (m > 0.0f) (void)frexpf(m, &pe);  // m in [2^(pe - 1), 2^pe)
-      const int ex = m > 0.0f ? max(pe - 8, -126) : -126;
-      const int q = __builtin_amdgcn_cvt_pk_fp8_f32(r * ldexpf(1.0f, -ex), 0.0f, 0, false) & 0xff;
-      r -= __builtin_amdgcn_cvt_pk_f32_fp8(q, false)[0] * ldexpf(1.0f, ex);
-      if (mine) {
-        xt.q[(int64_t)t * h + blk * 32 + j] = (uint8_t)q;
-        if (j == 0) xt.s[t * nblk + blk] = (uint8_t)(ex + 127);
-      }
-    }
-  }
-}
-
 // grid (E, B), block 256.  Token b's logits go to logits[b * 64 + e] (padded
 // so that consumers can read all 64 with scalar loads).  Block (0, 0) also
 // zeroes the words zero[i * zstride], i < nzero <= kBlock (the single-token
@@ -272,8 +219,7 @@ __global__ __launch_bounds__(kBlock) void k_router_logits(const float* __restric
                                                           const XT* __restrict__ x,
                                                           float* __restrict__ logits, int E,
                                                           int h, unsigned* __restrict__ zero,
-                                                          int nzero, int zstride, XSplit xs,
-                                                          XTerms xt) {
+                                                          int nzero, int zstride, XSplit xs) {
   __shared__ float part[4];
   __shared__ float pmax[4];
   const int q = threadIdx.x / kWave;
@@ -290,7 +236,6 @@ __global__ __launch_bounds__(kBlock) void k_router_logits(const float* __restric
     zero[(int64_t)threadIdx.x * zstride] = 0u;
   __syncthreads();
   if (threadIdx.x == 0) logits[(int64_t)b * WR_MAX_EXPERTS + e] = router_combine(part);
-  if (xt.q != nullptr && b == 0) x_terms<XT>(x, h, E, e, xt);
   if (xs.hi != nullptr) {
     const XT* xb = x + (int64_t)b * h;
     const int ex = scaled ? split_exp(fmaxf(fmaxf(pmax[0], pmax[1]), fmaxf(pmax[2], pmax[3])),
@@ -664,7 +609,6 @@ struct Handoff {
   int chunks;           // k * bpk
   unsigned spin_limit;  // polls before a wait gives up
   unsigned wait_extra;  // added to every arrival target: 0, or (tests) a wait that cannot complete
-  const uint8_t* xq;    // x as fp8 terms for the MFMA gate/up blocks (FusedWs::xq), or nullptr
 #if WR_TIMELINE
   uint64_t* tl;         // per-block records (include/wr_timeline.h)
 #endif
@@ -942,119 +886,6 @@ __device__ __forceinline__ void stage_bytes_lds(const uint8_t* src, unsigned cha
   }
 }
 
-// MXFP4 gate/up block on the block-scaled MFMA, v_mfma_scale_f32_16x16x128_f8f6f4
-// with A = E2M1 weight codes and B = x as kXTerms fp8 E4M3 terms (x_terms):
-// the matrix core decodes the codes and applies both block scales, so no
-// VALU decode or FMA is left.  Block = 16 rows r0 .. r0 + 16 of expert eid's
-// gate and up matrices (the 16 act columns of one chunk); wave w takes the
-// quarter [w h / 4, (w + 1) h / 4) of each row, nst = h / 512 K steps of 128,
-// all loaded in one round.  Operands (checked on gfx950 against a CPU
-// product, every (lane, byte) position mapped):
-//   A, fp4: lane l holds row l mod 16, elements 32 (l / 16) + 0 .. 31 of the
-//     step, i.e. 16 bytes of the row, element 2i in the low nibble of byte i:
-//     one 16-byte load, one MX block;
-//   B, fp8: lane l holds column n = l mod 16 (term n; columns >= kXTerms are
-//     zero), elements 16 (l / 16) + 0 .. 15 in bytes 0-15 and 64 + 16 (l / 16)
-//     + 0 .. 15 in bytes 16-31;
-//   scales: lane l gives the E8M0 byte of (row / column l mod 16, 32-element
-//     block l / 16 of the step) for A and B alike;
-//   D: lane l holds rows 4 (l / 16) + i, i < 4, of column l mod 16.
-// So a row's gate dot product is the sum of its kXTerms columns over the 4
-// waves.  The terms are copied from the workspace into the LDS buffer (rows
-// h + 16 bytes apart, then the scale bytes), issued before the weight loads
-// so that one wait covers both.  Every wave of the block calls it (two
-// barriers); rows past nrows load nothing and store nothing.  h a multiple
-// of 2048 and at most 4096 (nst 4 or 8).
-constexpr int kMfMaxSteps = 8;
-__device__ __forceinline__ void gateup_item_mf(const fp4x2* __restrict__ wbuf, float* a,
-                                               const Geom& g, int eid, float wk, int r0,
-                                               int nrows, int lane, int wave, unsigned char* lds,
-                                               const uint8_t* __restrict__ xq) {
-  typedef int v8i __attribute__((ext_vector_type(8)));
-  typedef float v4f __attribute__((ext_vector_type(4)));
-  const int h = g.h, nblk = h / 32, ts = h + 16, nst = h / 512;
-  unsigned char* lq = lds;                                // [kXTerms][ts] codes
-  unsigned char* ls = lds + (size_t)kXTerms * ts;         // [kXTerms][nblk] scale bytes
-  float* mpart = reinterpret_cast<float*>(ls + kXTerms * nblk);  // [4 waves][2][16]
-  for (int t = 0; t < kXTerms; ++t)
-    for (int off = wave * kWave * 16; off < h; off += kBlock * 16)  // 1 KB runs, h % 1024 == 0
-      __builtin_amdgcn_global_load_lds(
-          static_cast<const void*>(xq + (int64_t)t * h + off + 16 * lane),
-          (__attribute__((address_space(3))) void*)(lq + (size_t)t * ts + off), 16, 0, 0);
-  if (wave == 0) stage_bytes_lds(xq + (int64_t)kXTerms * h, ls, kXTerms * nblk, lane);
-
-  const int rr = lane & 15, grp = lane >> 4;
-  const bool rok = rr < nrows;
-  const int kb0 = wave * (h / 4);
-  const fp4x2* blk = wbuf + (int64_t)eid * g.stride;
-  const fp4x2* G = blk + eoff<fp4x2>((int64_t)(r0 + (rok ? rr : 0)) * h);
-  const fp4x2* Up = G + g.off_up;
-  u32x4 ag[kMfMaxSteps], au[kMfMaxSteps];
-#pragma unroll
-  for (int s = 0; s < kMfMaxSteps; ++s) {
-    const int off = (kb0 + 128 * s) / 2 + 16 * grp;  // bytes into the row
-    const bool ld = rok && s < nst;
-    ag[s] = ld ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(G + off))
-               : u32x4{0u, 0u, 0u, 0u};
-    au[s] = ld ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Up + off))
-               : u32x4{0u, 0u, 0u, 0u};
-  }
-  // The row's block-scale bytes of this wave's range: 4 nst of them (16 or
-  // 32 bytes, 16-byte aligned).  Rows that load nothing take scale 1.
-  u32x4 sg[2], su[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const bool ld = rok && 4 * i < nst;
-    const uint8_t* pg = mx_row(blk, g, 0, r0 + (rok ? rr : 0)) + kb0 / 32 + 16 * i;
-    const uint8_t* pu = mx_row(blk, g, 1, r0 + (rok ? rr : 0)) + kb0 / 32 + 16 * i;
-    sg[i] = ld ? *reinterpret_cast<const u32x4*>(pg) : u32x4{0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu};
-    su[i] = ld ? *reinterpret_cast<const u32x4*>(pu) : u32x4{0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu};
-  }
-  __builtin_amdgcn_s_waitcnt(0);  // the term copies (and the weights) have landed
-  __syncthreads();
-
-  const int n = lane & 15;  // this lane's B column: term n
-  v4f dg = {0.0f, 0.0f, 0.0f, 0.0f}, du = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int s = 0; s < kMfMaxSteps; ++s) {
-    if (s < nst) {  // wave-uniform
-      v8i bv = {0, 0, 0, 0, 0, 0, 0, 0};
-      int sb = 127;
-      if (n < kXTerms) {
-        const unsigned char* tq = lq + (size_t)n * ts + kb0 + 128 * s + 16 * grp;
-        const u32x4 lo = *reinterpret_cast<const u32x4*>(tq);
-        const u32x4 hi = *reinterpret_cast<const u32x4*>(tq + 64);
-        bv = v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
-                 (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-        sb = ls[n * nblk + kb0 / 32 + 4 * s + grp];
-      }
-      const int sag = (int)((sg[s >> 2][s & 3] >> (8 * grp)) & 0xffu);
-      const int sau = (int)((su[s >> 2][s & 3] >> (8 * grp)) & 0xffu);
-      const v8i av = {(int)ag[s][0], (int)ag[s][1], (int)ag[s][2], (int)ag[s][3], 0, 0, 0, 0};
-      const v8i uv = {(int)au[s][0], (int)au[s][1], (int)au[s][2], (int)au[s][3], 0, 0, 0, 0};
-      dg = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, dg, 4, 0, 0, sag, 0, sb);
-      du = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(uv, bv, du, 4, 0, 0, sau, 0, sb);
-    }
-  }
-  // Sum each row's columns (the 16 lanes of its group), then the 4 waves.
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float gs = row_sum(dg[i]), us = row_sum(du[i]);
-    if (n == 0) {
-      mpart[(wave * 2 + 0) * 16 + 4 * grp + i] = gs;
-      mpart[(wave * 2 + 1) * 16 + 4 * grp + i] = us;
-    }
-  }
-  __syncthreads();
-  if (wave == 0 && lane < nrows) {
-    const float gs = (mpart[0 * 32 + lane] + mpart[1 * 32 + lane]) +
-                     (mpart[2 * 32 + lane] + mpart[3 * 32 + lane]);
-    const float us = (mpart[0 * 32 + 16 + lane] + mpart[1 * 32 + 16 + lane]) +
-                     (mpart[2 * 32 + 16 + lane] + mpart[3 * 32 + 16 + lane]);
-    __hip_atomic_store(a + lane, wk * (silu(gs) * us), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
 // gateup_item with x read from the block's LDS copy (XlLayout).  Every wave
 // of the block calls it, because the copy ends in a block barrier; a wave
 // without an item passes nrows = 0.  The copy is made with direct
@@ -1272,15 +1103,10 @@ template <typename WT, int RPW, bool STG>
 constexpr size_t stg_gu_bytes() {
   return STG ? (size_t)kWavesPerBlock * 2 * RPW * (xl_max_h<WT>() / 32) : 0;
 }
-// LDS bytes of gateup_item_mf at h = 4096: term codes, scale bytes, wave sums.
-constexpr size_t kMfLdsBytes = (size_t)kXTerms * (4096 + 16) + (size_t)kXTerms * 128 + 512;
 // Bytes of the kernel-wide LDS buffer of k_fused_ffn.
-template <typename WT, typename XT, int VEC, int RPW, bool XL, bool STG, bool MF = false>
+template <typename WT, typename XT, int VEC, int RPW, bool XL, bool STG>
 constexpr size_t fused_raw_bytes() {
-  if constexpr (MF && !STG) {
-    constexpr size_t xl = fused_raw_bytes<WT, XT, VEC, RPW, XL, false, false>();
-    return xl > kMfLdsBytes ? xl : kMfLdsBytes;
-  } else if constexpr (XL) {
+  if constexpr (XL) {
     constexpr size_t gu = XlLayout<XT, VEC>::bytes(xl_max_h<WT>()) + stg_gu_bytes<WT, RPW, STG>();
     static_assert(!STG || gu <= WR_F4_STG_RAW, "the staged-scale buffer holds the gate/up copy");
     return STG ? (size_t)WR_F4_STG_RAW : gu;
@@ -1298,7 +1124,7 @@ constexpr size_t fused_raw_bytes() {
 #define WR_FUSED_BOUNDS __launch_bounds__(kBlock)
 #endif
 template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2, bool XL,
-          bool STG, bool CLAIM = false, bool MF = false>
+          bool STG, bool CLAIM = false>
 __global__ WR_FUSED_BOUNDS void k_fused_ffn(
     const WT* __restrict__ wbuf, const XT* __restrict__ x, const float* __restrict__ logits,
     float* act, XT* __restrict__ out, int32_t* __restrict__ ids_out, float* __restrict__ w_out,
@@ -1334,10 +1160,7 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
   // The x-in-LDS variant's buffer: the gate/up role's x copy (and, with
   // STG, its waves' scale bytes); the down role's scale copy with STG.
   static_assert(!STG || XL, "scale staging lives in the x-in-LDS variant's buffer");
-  static_assert(!MF || (XL && RPW == 4 && std::is_same<WT, fp4x2>::value),
-                "MFMA gate/up blocks are MXFP4 blocks of 16 rows with the LDS buffer");
-  static_assert(!STG || kMfLdsBytes <= WR_F4_STG_RAW, "the staged-scale buffer holds the terms");
-  __shared__ __align__(16) unsigned char lds_raw[fused_raw_bytes<WT, XT, VEC, RPW, XL, STG, MF>()];
+  __shared__ __align__(16) unsigned char lds_raw[fused_raw_bytes<WT, XT, VEC, RPW, XL, STG>()];
 
   if ((int)blockIdx.x < hs.n1b) {
     // ---- gate/up block ----
@@ -1363,13 +1186,7 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
     const int cls = (int)blockIdx.x % FusedWs::kClasses;
     for (int v = blockIdx.x;;) {
       const int G = chunk_of_block<LB>(v);
-      if constexpr (MF) {
-        const int kk = __builtin_amdgcn_readfirstlane(G < hs.chunks ? G / bpk : 0);
-        const int rb = (G - kk * bpk) * COLS;
-        const int nr = G < hs.chunks ? max(0, min(COLS, g.I - rb)) : 0;
-        gateup_item_mf(wbuf, act + kk * act_row + rb, g, topk_id(t, kk), topk_w(t, kk),
-                       nr > 0 ? rb : 0, nr, lane, wave, lds_raw, hs.xq);
-      } else if constexpr (XL) {
+      if constexpr (XL) {
         // Wave-uniform by construction; readfirstlane keeps them in SGPRs (the
         // TopK reads below take a scalar slot index).
         const int kk = __builtin_amdgcn_readfirstlane(G < hs.chunks ? G / bpk : 0);
@@ -1662,16 +1479,15 @@ bool router_vec4(const Problem& p) {
 
 template <typename XT>
 hipError_t logits_t(const Problem& p, float* logits, unsigned* zero, int nzero, int zstride,
-                    hipStream_t s, XSplit xs = XSplit{nullptr, nullptr, nullptr, nullptr, 0, 0},
-                    XTerms xt = XTerms{nullptr, nullptr}) {
+                    hipStream_t s, XSplit xs = XSplit{nullptr, nullptr, nullptr, nullptr, 0, 0}) {
   const dim3 grid(p.E, p.B);
   const XT* x = static_cast<const XT*>(p.x);
   if (router_vec4(p))
     hipLaunchKernelGGL((k_router_logits<XT, 4>), grid, dim3(kBlock), 0, s, p.gate_w, x, logits,
-                       p.E, p.h, zero, nzero, zstride, xs, xt);
+                       p.E, p.h, zero, nzero, zstride, xs);
   else
     hipLaunchKernelGGL((k_router_logits<XT, 1>), grid, dim3(kBlock), 0, s, p.gate_w, x, logits,
-                       p.E, p.h, zero, nzero, zstride, xs, xt);
+                       p.E, p.h, zero, nzero, zstride, xs);
   return hipGetLastError();
 }
 
@@ -1687,15 +1503,6 @@ int fused_rpw(const Problem& p) {
   if (p.wdt == WR_FP8_E4M3) return p.vec > 1 ? WR_F8_RPW : 2;
   if (p.wdt == WR_MXFP4) return p.vec == 32 ? 4 : 2;
   return (p.vec > 1 && row_bytes <= 2048) ? 4 : 2;
-}
-
-// Whether a single-token call runs its MXFP4 gate/up blocks on the MFMA
-// (gateup_item_mf): 16-byte aligned MXFP4 rows (4 rows per gate/up wave), h
-// a multiple of 2048 and at most 4096 (the x-in-LDS path's shapes).  The
-// router launch then also writes x's fp8 terms (x_terms).
-bool mf_gateup(const Problem& p) {
-  return WR_F4_MFMA && p.B == 1 && p.wdt == WR_MXFP4 && p.vec == 32 && fused_rpw(p) == 4 &&
-         p.h % 2048 == 0 && p.h <= 4096 && p.h <= WR_XL_FP4_MAXH;
 }
 
 // act chunks of the single-token fused kernel, and its gate/up blocks (the
@@ -1771,7 +1578,6 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
   if (hs.tl == nullptr) return hipErrorInvalidSymbol;
 #endif
   hs.ctrl = w.ctrl;
-  hs.xq = w.xq;
   hs.slot = reinterpret_cast<uint64_t*>(w.ctrl + FusedWs::kSlotWord);
   hs.gate_w = fold ? p.gate_w : nullptr;
   hs.rvec = router_vec4(p) ? 1 : 0;
@@ -1806,29 +1612,11 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
       // DBRX 105.0 -> 102.0 us; DeepSeek (I = 1408) 18.7 -> 19.0 us.
       if constexpr (kFp4 && RPW == 4) {
         constexpr size_t kRaw = fused_raw_bytes<WT, XT, VEC, RPW, true, true>();
-        const bool mf = mf_gateup(p) && w.xq != nullptr;
         if (p.h % 128 == 0 && p.I % 128 == 0 && p.I >= WR_F4_STG_MIN_I &&
             (size_t)p.k * RPD * (p.I / 32) <= kRaw) {
           hs.nb = hs.n1 + n2;
           WR_TL_GRID(hs.nb);
-          if (mf)
-            hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, true, false, true>),
-                               dim3(hs.n1 + n2), dim3(kBlock), 0, s,
-                               static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x),
-                               w.logits, w.act, static_cast<XT*>(p.out), p.topk_ids, p.topk_w, g,
-                               hs);
-          else
-            hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, true>),
-                               dim3(hs.n1 + n2), dim3(kBlock), 0, s,
-                               static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x),
-                               w.logits, w.act, static_cast<XT*>(p.out), p.topk_ids, p.topk_w, g,
-                               hs);
-          return hipGetLastError();
-        }
-        if (mf) {
-          hs.nb = hs.n1 + n2;
-          WR_TL_GRID(hs.nb);
-          hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, false, false, true>),
+          hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, true>),
                              dim3(hs.n1 + n2), dim3(kBlock), 0, s,
                              static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x),
                              w.logits, w.act, static_cast<XT*>(p.out), p.topk_ids, p.topk_w, g,
@@ -1930,21 +1718,18 @@ hipError_t ffn_x(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
 // Router logits into the workspace; for one token also the reset of the
 // single-token kernel's control words, which start each call at zero.
 hipError_t run_route(const Problem& p, hipStream_t s) {
-  const FusedWs w = FusedWs::carve(p.ws, p.E, p.h, p.I, p.k, p.B);
+  const FusedWs w = FusedWs::carve(p.ws, p.E, p.I, p.k, p.B);
   static_assert(FusedWs::kCtrlWords <= kBlock, "one router thread zeroes each control word");
   unsigned* zero = p.B == 1 ? w.ctrl : nullptr;
   const int nz = FusedWs::kCtrlWords, zs = FusedWs::kCounterStride;
-  const XSplit none{nullptr, nullptr, nullptr, nullptr, 0, 0};
-  const XTerms xt = mf_gateup(p) ? XTerms{w.xq, w.xq + (size_t)kXTerms * p.h}
-                                 : XTerms{nullptr, nullptr};
-  return p.adt == WR_F16 ? logits_t<f16>(p, w.logits, zero, nz, zs, s, none, xt)
-                         : logits_t<float>(p, w.logits, zero, nz, zs, s, none, xt);
+  return p.adt == WR_F16 ? logits_t<f16>(p, w.logits, zero, nz, zs, s)
+                         : logits_t<float>(p, w.logits, zero, nz, zs, s);
 }
 
 // The expert FFN from the logits run_route left in the workspace (fold =
 // false), or for one token with the router inside the FFN kernel.
 hipError_t run_ffn_only(const Problem& p, bool fold, hipStream_t s) {
-  const FusedWs w = FusedWs::carve(p.ws, p.E, p.h, p.I, p.k, p.B);
+  const FusedWs w = FusedWs::carve(p.ws, p.E, p.I, p.k, p.B);
   return p.adt == WR_F16 ? ffn_x<f16>(p, w, fold, s) : ffn_x<float>(p, w, fold, s);
 }
 
