@@ -59,7 +59,7 @@ extern "C" {
 #define WR_EXPERT_ALIGN 128
 /* Bytes of device scratch wr_fused_moe_noalloc holds per GPU (1 MiB): enough
  * for wr_workspace_bytes(WR_KIND_FUSED, ...) up to k * roundup(I, 16) =
- * 252,992 (Mixtral needs 28,672, DBRX 43,008, DeepSeek 8,448). */
+ * 253,248 (Mixtral needs 28,672, DBRX 43,008, DeepSeek 8,448). */
 #define WR_NOALLOC_SCRATCH_BYTES (1u << 20)
 
 typedef enum wr_status {
