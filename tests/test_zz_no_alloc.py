@@ -3,8 +3,9 @@ kernels use the library's fixed per-GPU scratch array instead of a caller
 workspace.  Checked through the C-ABI against wr_fused_moe (same kernels,
 caller workspace): bit-identical outputs, ids and weights, on two calls in a
 row, the second with a smaller layer (the array keeps the first call's
-contents), then once more with the first layer; and the size limit is
-rejected before any HIP call."""
+contents), then once more with the first layer; the size limit is
+rejected before any HIP call; and a call recorded into a HIP graph (after a
+first eager call on the device) replays equal to the eager entry point."""
 import ctypes
 
 import numpy as np
