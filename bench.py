@@ -208,8 +208,7 @@ def timeline_summary(step, n_calls: int) -> dict:
         t = rec[:, :5].astype(np.int64)
         t = (t - t[:, 0].min()) / (khz / 1e3)  # microseconds
         gu = rec[:, 6] == 0
-        dn = rec[:, 6] == 1
-        res = rec[:, 6] == 2  # resident schedule: gate/up slots, then own rows
+        dn = ~gu
 
         def q(v, p):
             return float(np.percentile(v, p)) if len(v) else float("nan")
@@ -227,20 +226,10 @@ def timeline_summary(step, n_calls: int) -> dict:
             "dn_release_max": q(t[dn, 3], 100),
             "dn_after_release_p50": q(t[dn, 4] - t[dn, 3], 50),
             "dn_after_release_max": q(t[dn, 4] - t[dn, 3], 100),
-            "res_blocks": int(res.sum()),
-            "res_start_max": q(t[res, 0], 100),
-            "res_selection_p50": q(t[res, 1] - t[res, 0], 50),
-            "res_gateup_done_p50": q(t[res, 2], 50), "res_gateup_done_max": q(t[res, 2], 100),
-            "res_release_min": q(t[res, 3], 0), "res_release_p50": q(t[res, 3], 50),
-            "res_release_max": q(t[res, 3], 100),
-            "res_after_release_p50": q(t[res, 4] - t[res, 3], 50),
-            "res_after_release_max": q(t[res, 4] - t[res, 3], 100),
             "kernel_end": float(max(t[gu, 3].max() if gu.any() else 0.0,
-                                    t[dn, 4].max() if dn.any() else 0.0,
-                                    t[res, 4].max() if res.any() else 0.0)),
+                                    t[dn, 4].max() if dn.any() else 0.0)),
         })
-    out = {k: round(float(np.nanmedian([r[k] for r in rows])), 2) for k in rows[0]}
-    out = {k: v for k, v in out.items() if v == v}  # phases this schedule does not have
+    out = {k: round(float(np.median([r[k] for r in rows])), 2) for k in rows[0]}
     out["calls"] = n_calls
     out["clock_khz"] = int(khz)
     return out

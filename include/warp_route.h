@@ -178,17 +178,6 @@ typedef struct wr_fused_opts {
                            blocks that finish first).  Fewer blocks than the
                            layer's chunks exercise that path at small shapes
                            (tests)                                            */
-  uint32_t schedule;    /* 0 = chosen by shape; 1 = separate gate/up and down
-                           blocks; 2 = every block does gate/up chunks, then
-                           its own output rows, wherever that grid is resident
-                           at once (16-bit weights; else as 0)                */
-  uint32_t steal_after; /* schedule 2: polls of a block's wait before it takes
-                           gate/up chunks left in other XCDs' queues; 0 = the
-                           default (4,096)                                    */
-  uint32_t claim_queues;/* schedule 2: blocks on XCDs 0 .. claim_queues - 1
-                           claim gate/up chunks from their XCD's queue at
-                           first, the others only take what is left after
-                           steal_after polls; 0 = all 8 (tests use fewer)     */
 } wr_fused_opts;
 
 /* Human-readable name of a status code (never NULL). */
@@ -243,16 +232,6 @@ WR_API int wr_fused_moe(const wr_moe_args *args, void *stream);
  * kernel is one warp (src/fused_moe.cu:76-227) and its error paths call
  * exit(1) (src/fused_moe.cu:9-15). */
 WR_API int wr_fused_moe_opts(const wr_moe_args *args, const wr_fused_opts *opts, void *stream);
-
-/* The schedule wr_fused_moe_opts(args, opts, ...) would run on the current
- * device: 1 = separate gate/up and down blocks (the down blocks take the
- * slots the gate/up blocks leave), 2 = every block does gate/up chunks, then
- * its own output rows, all blocks resident at once (16-bit weights, layers of
- * about one round of resident blocks: DeepSeek's shape, tensor-parallel
- * shards).  Negative: -(a wr_status) for invalid arguments or a HIP error.
- * Launches nothing.  No counterpart in the reference (its fused kernel has
- * one schedule, src/fused_moe.cu:257). */
-WR_API int wr_fused_moe_schedule(const wr_moe_args *args, const wr_fused_opts *opts);
 
 /* Status of the last single-token fused call that used `workspace` (size
  * workspace_bytes, at least wr_workspace_bytes(WR_KIND_FUSED, ...)): WR_OK, or

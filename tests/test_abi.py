@@ -25,8 +25,7 @@ def test_header_declares_the_expected_entry_points():
         "wr_status_str", "wr_layout", "wr_total_weight_bytes", "wr_layout_dtype",
         "wr_weight_bytes", "wr_workspace_bytes", "wr_gate_topk", "wr_fused_moe",
         "wr_fused_moe_route", "wr_fused_moe_ffn", "wr_batched_fused_moe", "wr_naive_moe",
-        "wr_fused_moe_opts", "wr_fused_moe_schedule", "wr_fused_moe_status",
-        "wr_fused_moe_noalloc"])
+        "wr_fused_moe_opts", "wr_fused_moe_status", "wr_fused_moe_noalloc"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -57,10 +56,9 @@ def test_struct_layout_matches_header_order():
     assert capi.WrMoeArgs.x.offset == 56
     assert ctypes.sizeof(capi.WrOffsets) == 32
     assert ctypes.sizeof(capi.WrLayoutInfo) == 48
-    # spin_limit, wait_extra, gu_blocks, schedule, steal_after, claim_queues
-    assert ctypes.sizeof(capi.WrFusedOpts) == 24
+    # spin_limit, wait_extra, gu_blocks
+    assert ctypes.sizeof(capi.WrFusedOpts) == 12
     assert capi.WrFusedOpts.gu_blocks.offset == 8
-    assert capi.WrFusedOpts.claim_queues.offset == 20
 
 
 FMT = {capi.WR_F32: "f32", capi.WR_F16: "f16", capi.WR_BF16: "bf16", capi.WR_FP8_E4M3: "fp8",

@@ -162,10 +162,6 @@ int validate(const wr_moe_args* a, int kind, Problem* p) {
   p->spin_limit = wr::kDefaultSpinLimit;
   p->wait_extra = 0;
   p->gu_blocks = 0;
-  p->schedule = 0;
-  p->steal_after = 0;
-  p->classes = 8;
-  p->plan = nullptr;
   return WR_OK;
 }
 
@@ -295,23 +291,8 @@ WR_API int wr_fused_moe_opts(const wr_moe_args* args, const wr_fused_opts* opts,
     if (opts->spin_limit != 0) p.spin_limit = opts->spin_limit;
     p.wait_extra = opts->wait_extra;
     p.gu_blocks = (int)(opts->gu_blocks & 0x7fffffe0u);  // a multiple of 32, or 0
-    p.schedule = opts->schedule <= 2 ? (int)opts->schedule : 0;
-    p.steal_after = opts->steal_after;
-    if (opts->claim_queues >= 1 && opts->claim_queues <= 8) p.classes = (int)opts->claim_queues;
   }
   return hip_status(wr::launch_fused(p, static_cast<hipStream_t>(stream)));
-}
-
-WR_API int wr_fused_moe_schedule(const wr_moe_args* args, const wr_fused_opts* opts) {
-  Problem p{};
-  const int st = validate(args, WR_KIND_FUSED, &p);
-  if (st != WR_OK) return -st;
-  if (opts != nullptr) {
-    p.schedule = opts->schedule <= 2 ? (int)opts->schedule : 0;
-    if (opts->claim_queues >= 1 && opts->claim_queues <= 8) p.classes = (int)opts->claim_queues;
-  }
-  const int sched = wr::fused_schedule(p);
-  return sched > 0 ? sched : -WR_EHIP;
 }
 
 WR_API int wr_fused_moe_noalloc(const wr_moe_args* args, void* stream) {

@@ -45,25 +45,10 @@ struct Problem {
   // (the rest of the gate/up chunks are claimed by the blocks that finish
   // first), else this many (tests).
   int gu_blocks;
-  // Single-token schedule: 0 = chosen by shape, 1 = split gate/up and down
-  // blocks (k_fused_ffn), 2 = resident (k_fused_res) wherever its grid fits.
-  int schedule;
-  // Resident schedule: polls before a waiting block takes unclaimed gate/up
-  // chunks from any XCD's queue (0 = kDefaultStealAfter), and the XCD queues
-  // that blocks claim from at first (8; fewer only in tests, to exercise the
-  // taking).
-  unsigned steal_after;
-  int classes;
-  // Not NULL: the single-token launcher stores the schedule it would use (1
-  // split, 2 resident) here and launches nothing.
-  int* plan;
 };
 
 // Polls of the single-token hand-off wait before it expires (about 0.2 s).
 constexpr unsigned kDefaultSpinLimit = 1u << 20;
-// Polls of the resident schedule's wait before a block looks for unclaimed
-// gate/up chunks (about a millisecond; a layer's hand-off takes microseconds).
-constexpr unsigned kDefaultStealAfter = 4096;
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 constexpr size_t kWsAlign = 256;
@@ -73,10 +58,8 @@ struct FusedWs {
   // Single-token hand-off, one 256-byte line per word: kCounters arrival
   // counters, the wait-timeout flag, an unused word, kCounters XCD-rotation
   // masks (gate/up block b ORs bit (its XCD - b) mod 8 into mask
-  // b mod kCounters; in the resident schedule the first mask is set when a
-  // block computes a chunk of another XCD's queue), then kClasses claim
-  // counters: of the gate/up chunks beyond the launched blocks (class b mod
-  // 8), or of the resident schedule's per-XCD queues.  The router launch of each
+  // b mod kCounters), then kClasses claim counters of the gate/up chunks
+  // beyond the launched blocks (class b mod 8).  The router launch of each
   // single-token call zeroes them (with WR_ROUTER_IN_FFN, block 0 of the
   // call's kernel, before it publishes its router slot).
   static constexpr int kCounters = 64;
@@ -244,9 +227,6 @@ hipError_t launch_fused(const Problem& p, hipStream_t s);
 // The two launches of launch_fused, for callers that issue them separately.
 hipError_t launch_fused_route(const Problem& p, hipStream_t s);
 hipError_t launch_fused_ffn(const Problem& p, hipStream_t s);
-// The single-token schedule launch_fused would use for p (1 split gate/up and
-// down blocks, 2 resident), or 0 on a HIP error.
-int fused_schedule(const Problem& p);
 hipError_t launch_batched(const Problem& p, hipStream_t s);
 hipError_t run_naive(const Problem& p, hipStream_t s);
 

@@ -135,29 +135,6 @@
 #ifndef WR_F4_STG_RAW
 #define WR_F4_STG_RAW 39936
 #endif
-// Resident schedule of the single-token kernel (k_fused_res): 1 to use it by
-// default for the layers it fits (16-bit weights, every block resident at
-// once); 0: only when a caller asks for it (wr_fused_opts.schedule = 2).
-// Measured slower than the split schedule (layer us, fp16, one box, 4 layers
-// rotated): DeepSeek 26.4 -> 34.0 (down weights loaded before the gate/up
-// chunks) / 30.8 (after), Mixtral tp8 shard 29.9 -> 34.6 / 33.6, tp4 shard
-// 45.6 -> 50.4 (before).
-#ifndef WR_RES
-#define WR_RES 0
-#endif
-// Its LDS buffer of down weights, in 1 KB row-chunks per block: 36 KB keeps 4
-// blocks per CU.
-#ifndef WR_RES_LDS_ROWCHUNKS
-#define WR_RES_LDS_ROWCHUNKS 36
-#endif
-// 1: it loads the down weights into LDS before its gate/up chunks; 0: after.
-#ifndef WR_RES_EARLY
-#define WR_RES_EARLY 1
-#endif
-// Minimum blocks per CU in its launch bound (0: none).
-#ifndef WR_RES_MINBLOCKS
-#define WR_RES_MINBLOCKS 0
-#endif
 
 namespace wr {
 
@@ -632,10 +609,6 @@ struct Handoff {
   int chunks;           // k * bpk
   unsigned spin_limit;  // polls before a wait gives up
   unsigned wait_extra;  // added to every arrival target: 0, or (tests) a wait that cannot complete
-  // Resident schedule (k_fused_res) only:
-  unsigned steal_after;   // polls without the release before a block takes unclaimed gate/up
-                          // chunks from any XCD's queue
-  int classes;            // XCD queues that blocks claim from at first: 8, or fewer (tests)
 #if WR_TIMELINE
   uint64_t* tl;         // per-block records (include/wr_timeline.h)
 #endif
@@ -1449,274 +1422,6 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
 }
 
 // ---------------------------------------------------------------------------
-// Single-token fused FFN, resident schedule (layers whose gate/up work is
-// about one round of resident blocks: DeepSeek's shape, tensor-parallel
-// shards).  The grid has one block per RPD output rows, all resident at once,
-// and every block does both parts of the layer:
-//
-// 1. Its down weights (the selected experts' columns of its RPD rows, up to
-//    WR_RES_LDS_ROWCHUNKS 1 KB row-chunks) go into LDS with direct
-//    global-to-LDS loads, which hold no registers and do not depend on act:
-//    before its gate/up work (WR_RES_EARLY), so that they stream with it, or
-//    after it.
-// 2. Gate/up chunk slot v (computed as k_fused_ffn's gate/up blocks compute
-//    slot v, then counted on arrival counter v mod 64) belongs to queue
-//    v mod 8.  A block running on XCD x takes slots x, x + 8, x + 16, ... from
-//    queue x, one atomic each (the first in flight during the expert
-//    selection), until the queue is empty.
-// 3. Wave 0 waits for all n1 arrivals; the block then computes its rows from
-//    LDS (chunks beyond the buffer from registers) and writes each row once.
-//
-// Act lines: chunk_of_block maps the LB slots of each 128-byte act line to one
-// queue, and a queue's slots are computed on its own XCD, so the argument at
-// k_fused_ffn holds with the hardware XCD id in place of the dispatch
-// rotation, and readers invalidate only their L1.  A block that computes a
-// slot of another XCD's queue (below) sets the first rotation word first, and
-// readers then make a full agent-scope acquire instead.
-//
-// Progress does not depend on dispatch order or on which XCDs run blocks:
-// every slot is taken from a queue by a running block, and a block whose wait
-// has lasted steal_after polls takes any slot left in any queue.  If fewer
-// than all blocks are resident (other kernels hold CUs), the resident ones do
-// every slot, the release comes and they exit, making room for the rest.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ int queue_slot(int cls, unsigned ticket, int n1) {
-  const int64_t v = cls + 8 * (int64_t)ticket;
-  return v < n1 ? (int)v : -1;
-}
-
-// A slot left in any queue, or -1 (one thread).
-__device__ __forceinline__ int steal_slot(const Handoff& hs) {
-  for (int c = 0; c < FusedWs::kClasses; ++c) {
-    unsigned* q = hs.claim + c * FusedWs::kCounterStride;
-    const unsigned n = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (queue_slot(c, n, hs.n1) < 0) continue;  // empty: no atomic
-    const int v = queue_slot(
-        c, __hip_atomic_fetch_add(q, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), hs.n1);
-    if (v >= 0) return v;
-  }
-  return -1;
-}
-
-template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2>
-#if WR_RES_MINBLOCKS
-#define WR_RES_BOUNDS __launch_bounds__(kBlock, WR_RES_MINBLOCKS)
-#else
-#define WR_RES_BOUNDS __launch_bounds__(kBlock)
-#endif
-__global__ WR_RES_BOUNDS void k_fused_res(
-    const WT* __restrict__ wbuf, const XT* __restrict__ x, const float* __restrict__ logits,
-    float* act, XT* __restrict__ out, int32_t* __restrict__ ids_out, float* __restrict__ w_out,
-    Geom g, Handoff hs) {
-  typedef typename WVec<WT, VEC>::type V;
-  static_assert(sizeof(V) == 16, "16-byte weight vectors");
-  constexpr int COLS = kWavesPerBlock * RPW;  // act columns per gate/up slot
-  constexpr int LB = 32 / COLS;               // slots per 128-byte act line
-  static_assert(COLS * LB == 32 && COLS <= FusedWs::kMaxActCols, "unsupported rows per wave");
-  constexpr int kLdsChunks = WR_RES_LDS_ROWCHUNKS / RPD;  // down chunks held in LDS
-  constexpr int kPerWave = (kLdsChunks + kWavesPerBlock - 1) / kWavesPerBlock;
-  // Row j of LDS chunk q: lane l's 16 bytes at ((q RPD + j) 64 + l) 16.
-  __shared__ __align__(16) unsigned char dl[kLdsChunks * RPD * kWave * 16];
-  __shared__ float part[kWavesPerBlock][RPD];
-  __shared__ int s_v, s_state;
-  const int lane = threadIdx.x & (kWave - 1);
-  // The wave index in an SGPR, and the item indices derived from it.
-  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
-  const int wu = wave;
-  const int64_t act_row = FusedWs::act_row(g.I, COLS);
-  unsigned* const ctrl = hs.ctrl;  // the words at their FusedWs offsets
-  const int xcd = (int)xcc_id();
-  const int cls = (xcd < FusedWs::kClasses && xcd < hs.classes) ? xcd : -1;  // -1: no queue
-
-  WR_TL_MARK(hs, 0);
-  // The first claim is made by wave 1, whose memory operations do not wait for
-  // the logits (wave 0 reads them for E > 16).
-  unsigned first = 0;
-  if (threadIdx.x == kWave && cls >= 0)
-    first = __hip_atomic_fetch_add(ctrl + FusedWs::kClaimWord + cls * FusedWs::kCounterStride, 1u,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  TopK t;
-  block_select_topk(logits, g.E, g.k, g.renorm, t);
-  WR_TL_MARK(hs, 1);
-#if WR_TIMELINE
-  {
-    unsigned hwid;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));
-    WR_TL_SET(hs, 5, (uint64_t)(unsigned)xcd | ((uint64_t)hwid << 32));
-    WR_TL_SET(hs, 6, 2u);
-  }
-#endif
-  if (threadIdx.x == kWave) s_v = cls >= 0 ? queue_slot(cls, first, hs.n1) : -1;
-  if (blockIdx.x == 0 && wave == 0) {
-#pragma unroll
-    for (int kk = 0; kk < WR_MAX_TOPK; ++kk) {
-      if (kk < g.k && lane == kk) {
-        if (ids_out != nullptr) ids_out[kk] = t.id[kk];
-        if (w_out != nullptr) w_out[kk] = t.w[kk];
-      }
-    }
-  }
-
-  const int r0 = (int)blockIdx.x * RPD;
-  const int nrows = min(RPD, g.h - r0);
-  const int nch = (g.I + kWave * VEC - 1) / (kWave * VEC);
-  const int C = g.k * nch;              // down chunks of this block
-  const int CL = min(C, kLdsChunks);    // of them in LDS; wave q mod 4 loads and reads chunk q
-  auto load_lds = [&]() {
-#pragma unroll
-    for (int v = 0; v < kPerWave; ++v) {
-      const int q = wu + kWavesPerBlock * v;
-      if (q < CL) {  // wave-uniform
-        const int kk = q / nch;
-        const int c = (q - kk * nch) * kWave * VEC + lane * VEC;
-        const WT* D = wbuf + (int64_t)topk_id(t, kk) * g.stride + g.off_down +
-                      eoff<WT>((int64_t)r0 * g.I + c);
-#pragma unroll
-        for (int j = 0; j < RPD; ++j) {
-          if (j < nrows && c < g.I)
-            __builtin_amdgcn_global_load_lds(
-                static_cast<const void*>(D + eoff<WT>((int64_t)j * g.I)),
-                (__attribute__((address_space(3))) void*)(dl + (size_t)(q * RPD + j) * kWave * 16),
-                16, 0, 0);
-        }
-      }
-    }
-  };
-  if constexpr (WR_RES_EARLY) load_lds();
-
-  // Gate/up slot v, then its arrival.  A slot of another XCD's queue sets the
-  // first rotation word before the arrival (the wait for this wave's memory
-  // operations below orders the two).
-  const int items = (g.I + RPW - 1) / RPW;
-  const int bpk = (items + kWavesPerBlock - 1) / kWavesPerBlock;  // slots per expert
-  auto gateup_slot = [&](int v) {
-    const int G = chunk_of_block<LB>(v);
-    if (G < hs.chunks) {
-      const int kk = G / bpk;
-      const int it = (G - kk * bpk) * kWavesPerBlock + wave;
-      if (it < items)
-        gateup_item<WT, XT, VEC, RPW, U1>(wbuf, x, act + kk * act_row + it * RPW, g, t, kk,
-                                          it * RPW, lane);
-    }
-    if (threadIdx.x == 0 && (v & (FusedWs::kClasses - 1)) != xcd)
-      __hip_atomic_fetch_or(ctrl + FusedWs::kRotWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's act stores have completed
-    __syncthreads();
-    if (threadIdx.x == 0)
-      __hip_atomic_fetch_add(ctrl + (v % FusedWs::kCounters) * FusedWs::kCounterStride, 1u,
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
-  // Slots from this XCD's queue until it is empty.
-  __syncthreads();
-  for (int v = __builtin_amdgcn_readfirstlane(s_v); v >= 0;) {
-    gateup_slot(v);
-    WR_TL_MARK(hs, 7);
-    if (threadIdx.x == 0)
-      s_v = queue_slot(cls,
-                       __hip_atomic_fetch_add(ctrl + FusedWs::kClaimWord +
-                                                  cls * FusedWs::kCounterStride,
-                                              1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                       hs.n1);
-    __syncthreads();
-    v = __builtin_amdgcn_readfirstlane(s_v);
-  }
-  if constexpr (!WR_RES_EARLY) load_lds();
-  WR_TL_MARK(hs, 2);
-  // The wait for every slot's arrival (wave 0, lane c: counter c), taking
-  // slots left in any queue after each steal_after polls.
-  unsigned spins = 0;
-  for (;;) {
-    if (wave == 0) {
-      const int c = lane;
-      const unsigned target =
-          (c < hs.n1 ? (unsigned)((hs.n1 - c + FusedWs::kCounters - 1) / FusedWs::kCounters)
-                     : 0u) + hs.wait_extra;
-      const unsigned* ctr = ctrl + c * FusedWs::kCounterStride;
-      int st = 0;
-      for (unsigned polls = 1;; ++polls) {
-        if (__ballot(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-                     target) == 0) {
-          st = 1;
-          break;
-        }
-        if (++spins > hs.spin_limit) {
-          st = 2;
-          if (lane == 0)
-            __hip_atomic_store(ctrl + FusedWs::kTimeoutWord, 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-          break;
-        }
-        if (polls >= hs.steal_after) break;
-        __builtin_amdgcn_s_sleep(8);
-      }
-      if (lane == 0) s_state = st;
-    }
-    __syncthreads();
-    if (s_state != 0) break;
-    if (threadIdx.x == 0) s_v = steal_slot(hs);
-    __syncthreads();
-    const int v = __builtin_amdgcn_readfirstlane(s_v);
-    if (v >= 0) gateup_slot(v);
-  }
-  const bool expired = s_state == 2;
-  if (wave == 0 && !expired) {
-    if (__hip_atomic_load(ctrl + FusedWs::kRotWord, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    else
-      invalidate_l1();
-  }
-  __syncthreads();
-  WR_TL_MARK(hs, 3);
-
-  float acc[RPD];
-#pragma unroll
-  for (int j = 0; j < RPD; ++j) acc[j] = 0.0f;
-  if (!expired) {
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's global-to-LDS loads have landed
-    asm volatile("" ::: "memory");
-    // Fresh copies of the lane index and the selection, so that the compiler
-    // recomputes the chunk offsets here instead of holding the ones of the
-    // LDS loads in registers across the gate/up work.
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
-    TopK td = t;
-    asm volatile("" : "+v"(td.lid));
-#pragma unroll
-    for (int v = 0; v < kPerWave; ++v) {
-      const int q = wu + kWavesPerBlock * v;
-      if (q < CL) {
-        const int kk = q / nch;
-        const int c = (q - kk * nch) * kWave * VEC + ln * VEC;
-        V lw[1][RPD];
-#pragma unroll
-        for (int j = 0; j < RPD; ++j)
-          lw[0][j] = (j < nrows && c < g.I)
-                         ? *reinterpret_cast<const V*>(dl + ((size_t)(q * RPD + j) * kWave + ln) *
-                                                               16)
-                         : vzero<V>();
-        down_tile_fma<WT, V, VEC, RPD, 1>(acc, lw, act, g, act_row, q, nch, ln, nullptr);
-      }
-    }
-    for (int q0 = CL + wave; q0 < C; q0 += kWavesPerBlock * U2) {
-      V wv[U2][RPD];
-      down_tile_load<WT, VEC, RPD, U2>(wv, wbuf, g, td, r0, nrows, q0, nch, ln);
-      down_tile_fma<WT, V, VEC, RPD, U2>(acc, wv, act, g, act_row, q0, nch, ln, nullptr);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < RPD; ++j) {
-    const float s = wave_sum(acc[j]);
-    if (lane == 0) part[wave][j] = s;
-  }
-  __syncthreads();
-  if (wave == 0 && lane < nrows)
-    out[r0 + lane] = to_out<XT>(expired ? __builtin_nanf("")
-                                        : (part[0][lane] + part[1][lane]) +
-                                              (part[2][lane] + part[3][lane]));
-  WR_TL_MARK(hs, 4);
-}
-
-// ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
 namespace {
@@ -1862,45 +1567,6 @@ uint64_t* tl_ptr() {
 }
 #endif
 
-template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD>
-hipError_t res_launch(const Problem& p, const FusedWs& w, Handoff hs, const Geom& g,
-                      hipStream_t s) {
-  hs.nb = (p.h + RPD - 1) / RPD;
-  WR_TL_GRID(hs.nb);
-  hipLaunchKernelGGL((k_fused_res<WT, XT, VEC, RPW, U1, RPD, WR_FU_U>), dim3(hs.nb), dim3(kBlock),
-                     0, s, static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x), w.logits,
-                     w.act, static_cast<XT*>(p.out), p.topk_ids, p.topk_w, g, hs);
-  return hipGetLastError();
-}
-
-// Output rows per block of the resident schedule (k_fused_res) for this
-// layer, or 0 when it does not suit it: one block per RPD = 2 or 4 rows, all of
-// them resident at once, and gate/up work of at most (100 + WR_GU_CLAIM_PCT)%
-// of one round of resident blocks (any amount when the caller asks for this
-// schedule).
-template <typename WT, typename XT, int VEC, int RPW, int U1>
-int res_rows(const Problem& p, int n1) {
-  if (p.schedule == 1 || (!WR_RES && p.schedule != 2)) return 0;
-  const int cus = cu_count();
-  const int s2 =
-      blocks_per_cu(reinterpret_cast<const void*>(k_fused_res<WT, XT, VEC, RPW, U1, 2, WR_FU_U>)) *
-      cus;
-  const int s4 =
-      blocks_per_cu(reinterpret_cast<const void*>(k_fused_res<WT, XT, VEC, RPW, U1, 4, WR_FU_U>)) *
-      cus;
-  int rpd = 0, slots = 0;
-  if (p.h <= 2 * s2) {
-    rpd = 2;
-    slots = s2;
-  } else if (p.h <= 4 * s4) {
-    rpd = 4;
-    slots = s4;
-  }
-  if (rpd == 0) return 0;
-  if ((int64_t)n1 * 100 > (int64_t)slots * (100 + WR_GU_CLAIM_PCT) && p.schedule != 2) return 0;
-  return rpd;
-}
-
 // fold: the kernel computes the router rows (one launch per layer); else it
 // reads the logits an earlier router launch left in the workspace.
 template <typename WT, typename XT, int VEC, int RPW, int U1>
@@ -1924,27 +1590,6 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
   hs.chunks = fused_chunks(p.I, p.k, RPW);
   hs.spin_limit = p.spin_limit;
   hs.wait_extra = p.wait_extra;
-  hs.steal_after = 0;
-  hs.classes = FusedWs::kClasses;
-  // The resident schedule for 16-bit weights in 16-byte vectors, unless the
-  // router runs in the kernel.  p.plan: report the schedule, launch nothing.
-  if constexpr (sizeof(WT) == 2 && VEC == 8) {
-    const int rpd = fold ? 0 : res_rows<WT, XT, VEC, RPW, U1>(p, hs.n1);
-    if (rpd > 0) {
-      if (p.plan != nullptr) {
-        *p.plan = 2;
-        return hipSuccess;
-      }
-      hs.steal_after = p.steal_after != 0 ? p.steal_after : kDefaultStealAfter;
-      hs.classes = p.classes;
-      return rpd == 2 ? res_launch<WT, XT, VEC, RPW, U1, 2>(p, w, hs, g, s)
-                      : res_launch<WT, XT, VEC, RPW, U1, 4>(p, w, hs, g, s);
-    }
-  }
-  if (p.plan != nullptr) {
-    *p.plan = 1;
-    return hipSuccess;
-  }
   // fp8 down blocks take twice the rows and half the chunks in flight: the
   // same weight bytes per tile as fp16, and half the act reads per weight byte.
   // MXFP4 (32 act values per lane and chunk): 8 rows, one chunk in flight.
@@ -2125,14 +1770,6 @@ hipError_t launch_fused(const Problem& p, hipStream_t s) { return run_ffn(p, s);
 hipError_t launch_fused_route(const Problem& p, hipStream_t s) { return run_route(p, s); }
 
 hipError_t launch_fused_ffn(const Problem& p, hipStream_t s) { return run_ffn_only(p, false, s); }
-
-int fused_schedule(const Problem& p) {
-  int plan = 0;
-  Problem q = p;
-  q.plan = &plan;
-  if (run_ffn_only(q, WR_ROUTER_IN_FFN != 0 && p.B == 1, nullptr) != hipSuccess) return 0;
-  return plan;
-}
 
 hipError_t launch_logits_split(const Problem& p, float* logits, f16* x_hi, f16* x_lo,
                                int32_t* x_exp, unsigned* amax, int split_bf16, hipStream_t s) {

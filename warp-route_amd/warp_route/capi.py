@@ -58,8 +58,7 @@ class WrLayoutInfo(ctypes.Structure):
 
 class WrFusedOpts(ctypes.Structure):
     _fields_ = [("spin_limit", ctypes.c_uint32), ("wait_extra", ctypes.c_uint32),
-                ("gu_blocks", ctypes.c_uint32), ("schedule", ctypes.c_uint32),
-                ("steal_after", ctypes.c_uint32), ("claim_queues", ctypes.c_uint32)]
+                ("gu_blocks", ctypes.c_uint32)]
 
 
 class WrMoeArgs(ctypes.Structure):
@@ -112,9 +111,6 @@ def lib() -> ctypes.CDLL:
         l.wr_fused_moe_opts.argtypes = [ctypes.POINTER(WrMoeArgs), ctypes.POINTER(WrFusedOpts),
                                         ctypes.c_void_p]
         l.wr_fused_moe_opts.restype = ctypes.c_int
-        l.wr_fused_moe_schedule.argtypes = [ctypes.POINTER(WrMoeArgs),
-                                            ctypes.POINTER(WrFusedOpts)]
-        l.wr_fused_moe_schedule.restype = ctypes.c_int
         l.wr_fused_moe_status.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         l.wr_fused_moe_status.restype = ctypes.c_int
         # include/wr_timeline.h (measurement hook)
