@@ -217,6 +217,11 @@ def timeline_summary(step, n_calls: int) -> dict:
             "gu_start_p50": q(t[gu, 0], 50), "gu_start_max": q(t[gu, 0], 100),
             "gu_selection_p50": q(t[gu, 1] - t[gu, 0], 50),
             "gu_life_p50": q(t[gu, 3] - t[gu, 0], 50),
+            # x staged in LDS: the copy and the first weight round landed
+            "gu_first_round_p50": q((rec[gu, 2].astype(np.int64) - rec[gu, 0].astype(np.int64))
+                                    [rec[gu, 2] > 0] / (khz / 1e3), 50),
+            "gu_computed_p50": q((rec[gu, 7].astype(np.int64) - rec[gu, 0].astype(np.int64))
+                                 [rec[gu, 7] > 0] / (khz / 1e3), 50),
             "gu_end_p50": q(t[gu, 3], 50),
             "gu_last_arrival": q(t[gu, 3], 100),
             "dn_start_min": q(t[dn, 0], 0), "dn_start_p50": q(t[dn, 0], 50),
@@ -229,7 +234,8 @@ def timeline_summary(step, n_calls: int) -> dict:
             "kernel_end": float(max(t[gu, 3].max() if gu.any() else 0.0,
                                     t[dn, 4].max() if dn.any() else 0.0)),
         })
-    out = {k: round(float(np.median([r[k] for r in rows])), 2) for k in rows[0]}
+    out = {k: round(float(np.nanmedian([r[k] for r in rows])), 2) for k in rows[0]}
+    out = {k: v for k, v in out.items() if v == v}  # phases this kernel variant does not mark
     out["calls"] = n_calls
     out["clock_khz"] = int(khz)
     return out

@@ -31,14 +31,15 @@ extern "C" {
  * GPU's constant-rate wall clock (hipDeviceAttributeWallClockRate, kHz):
  *   0  workgroup start
  *   1  expert selection done
- *   2  down: first weight tile's loads issued (gate/up: 0)
+ *   2  down: first weight tile's loads issued; gate/up with x staged in LDS:
+ *      the x copy and the first round of weight loads landed (else 0)
  *   3  gate/up: last arrival counted, the workgroup's end; down: hand-off
  *      release seen by the workgroup
  *   4  down: workgroup end (gate/up: 0)
  * and
  *   5  hardware ids: XCD id in bits 0-3, the HW_ID register in bits 32-63
  *   6  role: 0 gate/up, 1 down
- *   7  unused (0)
+ *   7  gate/up: the last chunk's rows computed, before their stores (down: 0)
  */
 
 /* Copies the records of the last k_fused_ffn launch on the current device

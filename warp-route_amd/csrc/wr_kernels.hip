@@ -744,7 +744,8 @@ __host__ __device__ __forceinline__ int chunk_of_block(int b) {
 template <typename WT, typename XT, int VEC, int RPW, int U>
 __device__ __forceinline__ void gateup_item(const WT* __restrict__ wbuf, const XT* __restrict__ xb,
                                             float* a, const Geom& g, const TopK& t, int kk,
-                                            int r0, int lane) {
+                                            int r0, int lane, const Handoff* hsp = nullptr) {
+  (void)hsp;  // WR_TIMELINE builds of k_fused_ffn record a mark
   typedef typename WVec<WT, VEC>::type V;
   constexpr int CH = kWave * VEC;
   const WT* blk = wbuf + (int64_t)topk_id(t, kk) * g.stride;
@@ -790,6 +791,9 @@ __device__ __forceinline__ void gateup_item(const WT* __restrict__ wbuf, const X
           au[j] = fmaf(wdec<WT>(wu[u][j], i), xv[u][i], au[j]);
         }
   }
+#if WR_TIMELINE
+  if (hsp != nullptr) WR_TL_MARK(*hsp, 7);
+#endif
   const float wk = topk_w(t, kk);
 #pragma unroll
   for (int j = 0; j < RPW; ++j) {
@@ -896,7 +900,9 @@ template <typename WT, typename XT, int VEC, int RPW, int U, bool STG>
 __device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
                                                const XT* __restrict__ xb, float* a,
                                                const Geom& g, int eid, float wk, int r0,
-                                               int nrows, int lane, unsigned char* xs_raw) {
+                                               int nrows, int lane, unsigned char* xs_raw,
+                                               const Handoff& hs) {
+  (void)hs;  // WR_TIMELINE builds record two marks
   typedef typename WVec<WT, VEC>::type V;
   typedef XlLayout<XT, VEC> L;
   constexpr int CH = kWave * VEC;
@@ -941,6 +947,7 @@ __device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
   load_row_scales<WT, RPW>(rs, blk, g, r0, nrows);
   __builtin_amdgcn_s_waitcnt(0);  // the copy's loads (and the weights) have landed
   __syncthreads();
+  WR_TL_MARK(hs, 2);
 
   float ag[RPW], au[RPW];
 #pragma unroll
@@ -992,6 +999,7 @@ __device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
         }
     }
   }
+  WR_TL_MARK(hs, 7);
 #pragma unroll
   for (int j = 0; j < RPW; ++j) {
     const float gs = wave_sum(ag[j]);
@@ -1194,13 +1202,14 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
         const int nrows = (G < hs.chunks && it < items) ? min(RPW, g.I - it * RPW) : 0;
         gateup_item_xl<WT, XT, VEC, RPW, U1, STG>(wbuf, x, act + kk * act_row + it * RPW, g,
                                                   topk_id(t, kk), topk_w(t, kk),
-                                                  nrows > 0 ? it * RPW : 0, nrows, lane, lds_raw);
+                                                  nrows > 0 ? it * RPW : 0, nrows, lane, lds_raw,
+                                                  hs);
       } else if (G < hs.chunks) {
         const int kk = G / bpk;
         const int it = (G - kk * bpk) * kWavesPerBlock + wave;
         if (it < items)
           gateup_item<WT, XT, VEC, RPW, U1>(wbuf, x, act + kk * act_row + it * RPW, g, t, kk,
-                                            it * RPW, lane);
+                                            it * RPW, lane, &hs);
       }
       if (threadIdx.x == 0 && v == (int)blockIdx.x)
         __hip_atomic_fetch_or(hs.rot + (blockIdx.x % FusedWs::kCounters) * FusedWs::kCounterStride,
