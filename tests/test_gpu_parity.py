@@ -591,6 +591,38 @@ def test_fused_workspace_reused_across_layers(cuda):
         assert torch.equal(o, want[i % 2]), f"call {i}"
 
 
+@pytest.mark.parametrize("wd", [F16, MX4], ids=["f16", "mxfp4"])
+def test_fused_calls_on_two_streams(cuda, wd):
+    """Single-token calls of two full-size Mixtral layers issued on two
+    streams at once, 20 each, alternately, so that the two streams' kernels
+    share the GPU and two hand-offs run at the same time, each on its own
+    workspace.  Gate/up blocks never wait, and each kernel's gate/up blocks
+    are dispatched before its down blocks, so neither kernel can hold slots
+    the other one needs to finish.  Every output must equal its layer's
+    output on one stream bit for bit (an expired wait would leave NaN
+    rows)."""
+    E, h, I, k = 8, 4096, 14336, 2
+    layers = [make_layer(E, h, I, wd, router_std=h ** -0.5, seed=s, device=cuda,
+                         gen_device=cuda) for s in (21, 22)]
+    want = [F.fused_moe(x, gw, buf, E, h, I, k) for x, gw, buf in layers]
+    torch.cuda.synchronize()
+    assert not torch.equal(want[0], want[1])
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[], []]
+    print(f"[gpu] fused calls on two streams, {WNAME[wd]}", flush=True)
+    for _ in range(20):
+        for i, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                x, gw, buf = layers[i]
+                outs[i].append(F.fused_moe(x, gw, buf, E, h, I, k))
+    torch.cuda.synchronize()
+    for i in range(2):
+        for n, o in enumerate(outs[i]):
+            assert torch.equal(o, want[i]), f"stream {i} call {n}"
+    del layers
+    torch.cuda.empty_cache()
+
+
 def test_golden_toy_fixture(cuda):
     """The toy config (seed 0) against the committed fixture."""
     import json
