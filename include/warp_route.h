@@ -243,6 +243,20 @@ WR_API int wr_fused_moe_opts(const wr_moe_args *args, const wr_fused_opts *opts,
  * (src/fused_moe.cu:9-15). */
 WR_API int wr_fused_moe_status(const void *workspace, size_t workspace_bytes, void *stream);
 
+/* Whether a single-token call's hand-off wait has expired since the last
+ * call with clear != 0: 1 or 0.  A down block whose wait expires also stores
+ * 1 to a host-visible word of the library (4 bytes of pinned host memory,
+ * allocated by the first wr_fused_moe, wr_fused_moe_opts or wr_fused_moe_ffn
+ * call made outside stream capture, held until the process ends;
+ * wr_fused_moe_noalloc writes it once it exists).  This reads that word with
+ * a host load: no HIP call, no synchronisation, so it may be called after
+ * every op, also under graph capture.  An expiry is seen once its kernel has
+ * run, so a check right after a call reports the expiries of calls that have
+ * finished by then (an asynchronous report, like a device error).  With
+ * clear != 0 a set word is cleared.  No counterpart in the reference, whose
+ * fused kernel exits the process on error (src/fused_moe.cu:9-15). */
+WR_API int wr_fused_moe_expired(int clear);
+
 /* The two launches of wr_fused_moe, for callers that issue them separately
  * (to overlap the router with other work on the stream's timeline, or to time
  * the expert FFN alone).  wr_fused_moe_route computes the router logits into
@@ -270,9 +284,10 @@ WR_API int wr_fused_moe_ffn(const wr_moe_args *args, void *stream);
  * it needs), so calls that overlap on one GPU -- on different streams, or
  * from different threads -- race and must be serialised by the caller.  The
  * call may be recorded into a HIP graph once a first call on the GPU has
- * looked up the array.  A hand-off expiry shows only as
- * NaN output rows: the timeout word lives in the library's array, which
- * wr_fused_moe_status cannot be given.  Otherwise identical to wr_fused_moe,
+ * looked up the array.  A hand-off expiry shows as NaN
+ * output rows, and through wr_fused_moe_expired once another single-token
+ * call has allocated its word: the timeout word lives in the library's
+ * array, which wr_fused_moe_status cannot be given.  Otherwise identical to wr_fused_moe,
  * with the same kernels and results. */
 WR_API int wr_fused_moe_noalloc(const wr_moe_args *args, void *stream);
 

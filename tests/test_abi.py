@@ -25,7 +25,16 @@ def test_header_declares_the_expected_entry_points():
         "wr_status_str", "wr_layout", "wr_total_weight_bytes", "wr_layout_dtype",
         "wr_weight_bytes", "wr_workspace_bytes", "wr_gate_topk", "wr_fused_moe",
         "wr_fused_moe_route", "wr_fused_moe_ffn", "wr_batched_fused_moe", "wr_naive_moe",
-        "wr_fused_moe_opts", "wr_fused_moe_status", "wr_fused_moe_noalloc"])
+        "wr_fused_moe_opts", "wr_fused_moe_status", "wr_fused_moe_noalloc",
+        "wr_fused_moe_expired"])
+
+
+def test_expiry_query_needs_no_gpu():
+    """wr_fused_moe_expired is a host read of a word that only a
+    single-token call allocates: before any such call it reports 0, with or
+    without clearing, and makes no HIP call (none succeeds without a GPU)."""
+    assert capi.lib().wr_fused_moe_expired(0) == 0
+    assert capi.lib().wr_fused_moe_expired(1) == 0
 
 
 def test_library_exports_every_declared_symbol():

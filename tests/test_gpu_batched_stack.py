@@ -306,9 +306,12 @@ def test_fused_handoff_expiry_is_reported(cuda, shape):
     what the gate/up blocks can reach, and spin_limit = 4 ends each down
     block's wait after 4 polls, so every kernel still exits normally.  Every
     down block must then write NaN to its rows, and wr_fused_moe_status must
-    report WR_ETIMEOUT.  The next default call on the same workspace clears
-    the word and is correct again; the torch op with the check switched on
-    does not raise for it."""
+    report WR_ETIMEOUT; the library's host-visible expiry word is set too
+    (wr_fused_moe_expired, no synchronisation).  The next default call on the
+    same workspace clears the timeout word and is correct again; the torch
+    op's next call raises once for the earlier expiry (read from the
+    host-visible word), the one after it does not, nor with the check
+    switched on."""
     E, h, I, k, wd = shape
     x, gw, buf = make_layer(E, h, I, wd, router_std=h ** -0.5, seed=2, device=cuda,
                             gen_device=cuda)
@@ -326,6 +329,8 @@ def test_fused_handoff_expiry_is_reported(cuda, shape):
                                         ctypes.c_void_p(stream))
     assert st == capi.WR_ETIMEOUT, capi.status_str(st)
     assert torch.isnan(out).all(), "a down block that gave up wrote a number"
+    assert capi.lib().wr_fused_moe_expired(0) == 1  # set, and not cleared by reading
+    assert capi.lib().wr_fused_moe_expired(0) == 1
 
     # default options again, same workspace: cleared and correct
     st = capi.lib().wr_fused_moe_opts(ctypes.byref(a), None, ctypes.c_void_p(stream))
@@ -335,6 +340,9 @@ def test_fused_handoff_expiry_is_reported(cuda, shape):
     assert st == capi.WR_OK, capi.status_str(st)
     ref = oracle_token(x, gw, buf, E, h, I, k, False)
     np.testing.assert_allclose(f64(out), ref["out"], rtol=1e-2, atol=1e-2)
+    with pytest.raises(RuntimeError, match="hand-off wait expired"):
+        F.fused_moe(x, gw, buf, E, h, I, k)
+    assert capi.lib().wr_fused_moe_expired(0) == 0  # reported once, then cleared
     want = F.fused_moe(x, gw, buf, E, h, I, k)
     torch.cuda.synchronize()
     assert torch.equal(out, want)
@@ -345,6 +353,7 @@ def test_fused_handoff_expiry_is_reported(cuda, shape):
     finally:
         F.set_handoff_check(False)
     assert torch.equal(again, want)
+    assert capi.lib().wr_fused_moe_expired(0) == 0
     del buf
     torch.cuda.empty_cache()
 

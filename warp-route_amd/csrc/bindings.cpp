@@ -144,6 +144,16 @@ void check_status(int st, const char* op) {
   TORCH_CHECK(st == WR_OK, op, " failed: ", wr_status_str(st), " (status ", st, ")");
 }
 
+// Expiries of single-token hand-off waits, read from the library's
+// host-visible word without a synchronisation: this reports the expiries of
+// every single-token call whose kernel has run by now (this one or an
+// earlier one), once each.
+void check_expired(const char* op) {
+  TORCH_CHECK(wr_fused_moe_expired(1) == 0, op,
+              " failed: a single-token fused call's hand-off wait expired (that call's output "
+              "rows are NaN); seen after its kernel ran, so it may have been an earlier call");
+}
+
 torch::Tensor single_token_op(int kind, torch::Tensor hidden, torch::Tensor gate_w,
                               torch::Tensor weight_buf, int num_experts, int hidden_dim,
                               int intermediate_dim, int top_k, bool renormalize,
@@ -168,9 +178,12 @@ torch::Tensor single_token_op(int kind, torch::Tensor hidden, torch::Tensor gate
   void* stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(dev.index()).stream();
   if (kind == WR_KIND_FUSED) {
     check_status(wr_fused_moe(&a, stream), "fused_moe_forward");
-    if (g_check_handoff.load(std::memory_order_relaxed))
-      check_status(wr_fused_moe_status(a.workspace, a.workspace_bytes, stream),
-                   "fused_moe_forward");
+    if (g_check_handoff.load(std::memory_order_relaxed)) {
+      const int st = wr_fused_moe_status(a.workspace, a.workspace_bytes, stream);
+      if (st == WR_ETIMEOUT) (void)wr_fused_moe_expired(1);  // reported here, not again
+      check_status(st, "fused_moe_forward");
+    }
+    check_expired("fused_moe_forward");
   } else
     check_status(wr_naive_moe(&a, stream), "naive_moe_forward");
   return out;

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 #include <mutex>
 
@@ -194,6 +195,45 @@ void* scratch_ptr() {
   return g_scratch_ptr[dev];
 }
 
+// The host-visible expiry word of every single-token call: 4 bytes of
+// pinned, coherent host memory mapped for every GPU, allocated once by the
+// first call that takes a caller workspace outside stream capture, and held
+// until the process ends.  A kernel whose hand-off wait expires stores 1 to
+// it; wr_fused_moe_expired reads it with a host load.
+std::once_flag g_expired_once;
+std::atomic<unsigned*> g_expired{nullptr};
+
+// The word's device address; allocates it when `alloc` (and the stream is
+// not being captured).  nullptr: not available (the call then does not
+// write it; its timeout word still records an expiry).
+unsigned* expired_word(bool alloc, hipStream_t s) {
+  unsigned* w = g_expired.load(std::memory_order_acquire);
+  if (w != nullptr || !alloc) return w;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+    return nullptr;
+  std::call_once(g_expired_once, [] {
+    void* h = nullptr;
+    if (hipHostMalloc(&h, sizeof(unsigned),
+                      hipHostMallocMapped | hipHostMallocPortable | hipHostMallocCoherent) !=
+            hipSuccess ||
+        h == nullptr) {
+      (void)hipGetLastError();
+      return;
+    }
+    *static_cast<volatile unsigned*>(h) = 0u;
+    void* d = nullptr;
+    if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess || d != h) {
+      // Only a word whose host and device addresses agree is used, so that
+      // the host reads what the kernels write.
+      (void)hipGetLastError();
+      return;
+    }
+    g_expired.store(static_cast<unsigned*>(h), std::memory_order_release);
+  });
+  return g_expired.load(std::memory_order_acquire);
+}
+
 }  // namespace
 
 extern "C" {
@@ -280,6 +320,7 @@ WR_API int wr_fused_moe(const wr_moe_args* args, void* stream) {
   Problem p{};
   const int st = validate(args, WR_KIND_FUSED, &p);
   if (st != WR_OK) return st;
+  p.expired_host = expired_word(true, static_cast<hipStream_t>(stream));
   return hip_status(wr::launch_fused(p, static_cast<hipStream_t>(stream)));
 }
 
@@ -292,6 +333,7 @@ WR_API int wr_fused_moe_opts(const wr_moe_args* args, const wr_fused_opts* opts,
     p.wait_extra = opts->wait_extra;
     p.gu_blocks = (int)(opts->gu_blocks & 0x7fffffe0u);  // a multiple of 32, or 0
   }
+  p.expired_host = expired_word(true, static_cast<hipStream_t>(stream));
   return hip_status(wr::launch_fused(p, static_cast<hipStream_t>(stream)));
 }
 
@@ -310,6 +352,7 @@ WR_API int wr_fused_moe_noalloc(const wr_moe_args* args, void* stream) {
   if (ws == nullptr) return WR_EHIP;
   p.ws = static_cast<char*>(ws);
   p.ws_bytes = WR_NOALLOC_SCRATCH_BYTES;
+  p.expired_host = expired_word(false, nullptr);  // written once an earlier call made it
   return hip_status(wr::launch_fused(p, static_cast<hipStream_t>(stream)));
 }
 
@@ -325,6 +368,14 @@ WR_API int wr_fused_moe_status(const void* workspace, size_t workspace_bytes, vo
   return v != 0 ? WR_ETIMEOUT : WR_OK;
 }
 
+WR_API int wr_fused_moe_expired(int clear) {
+  unsigned* w = g_expired.load(std::memory_order_acquire);
+  if (w == nullptr) return 0;
+  const unsigned v = __atomic_load_n(w, __ATOMIC_ACQUIRE);
+  if (v != 0 && clear != 0) __atomic_store_n(w, 0u, __ATOMIC_RELEASE);
+  return v != 0 ? 1 : 0;
+}
+
 WR_API int wr_fused_moe_route(const wr_moe_args* args, void* stream) {
   Problem p{};
   const int st = validate(args, WR_KIND_FUSED, &p);
@@ -336,6 +387,7 @@ WR_API int wr_fused_moe_ffn(const wr_moe_args* args, void* stream) {
   Problem p{};
   const int st = validate(args, WR_KIND_FUSED, &p);
   if (st != WR_OK) return st;
+  p.expired_host = expired_word(true, static_cast<hipStream_t>(stream));
   return hip_status(wr::launch_fused_ffn(p, static_cast<hipStream_t>(stream)));
 }
 

@@ -45,6 +45,10 @@ struct Problem {
   // (the rest of the gate/up chunks are claimed by the blocks that finish
   // first), else this many (tests).
   int gu_blocks;
+  // Host-visible word (pinned host memory) that a single-token call's kernel
+  // also sets when a hand-off wait expires, so that an expiry can be seen
+  // without synchronising; nullptr: not written.
+  unsigned* expired_host;
 };
 
 // Polls of the single-token hand-off wait before it expires (about 0.2 s).

@@ -601,6 +601,7 @@ struct Handoff {
   int rvec;             // router rows and x in 128-bit loads (else scalar)
   unsigned* cnt;        // FusedWs::kCounters counters, FusedWs::kCounterStride words apart
   unsigned* timeout;    // set to 1 if a wait expired (that block's rows are then NaN)
+  unsigned* host_flag;  // host-visible word also set to 1 then, or nullptr
   unsigned* rot;        // FusedWs::kCounters rotation masks, FusedWs::kCounterStride words apart
   unsigned* claim;      // FusedWs::kClasses claim counters, FusedWs::kCounterStride words apart
   int n1;               // gate/up chunk slots, a multiple of 8 LB: one arrival each
@@ -613,6 +614,15 @@ struct Handoff {
   uint64_t* tl;         // per-block records (include/wr_timeline.h)
 #endif
 };
+
+// A hand-off wait expired: the workspace's timeout word (read by
+// wr_fused_moe_status) and the host-visible word (read by
+// wr_fused_moe_expired without a synchronisation), both plain stores of 1.
+__device__ __forceinline__ void set_expired(const Handoff& hs) {
+  __hip_atomic_store(hs.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (hs.host_flag != nullptr)
+    __hip_atomic_store(hs.host_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 
 // WR_TIMELINE builds: thread 0 stores the wall clock as record `ev` of its
 // workgroup (include/wr_timeline.h), a plain store that nothing waits for.
@@ -718,8 +728,7 @@ __device__ __forceinline__ bool route_and_select(const XT* __restrict__ x,
       if (__ballot(!ok) == 0) break;
       if (++spins > hs.spin_limit) {
         ok_all = 0;
-        if (lane == 0)
-          __hip_atomic_store(hs.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) set_expired(hs);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -1345,8 +1354,7 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
                     target) != 0) {
       if (++spins > hs.spin_limit) {
         gave_up = 1;
-        if (lane == 0)
-          __hip_atomic_store(hs.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) set_expired(hs);
         break;
       }
       __builtin_amdgcn_s_sleep(8);
@@ -1592,6 +1600,7 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
   hs.rvec = router_vec4(p) ? 1 : 0;
   hs.cnt = w.ctrl;
   hs.timeout = w.ctrl + FusedWs::kTimeoutWord;
+  hs.host_flag = p.expired_host;
   hs.rot = w.ctrl + FusedWs::kRotWord;
   hs.claim = w.ctrl + FusedWs::kClaimWord;
   hs.n1 = fused_n1(p.I, p.k, RPW);

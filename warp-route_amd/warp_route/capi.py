@@ -113,6 +113,8 @@ def lib() -> ctypes.CDLL:
         l.wr_fused_moe_opts.restype = ctypes.c_int
         l.wr_fused_moe_status.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         l.wr_fused_moe_status.restype = ctypes.c_int
+        l.wr_fused_moe_expired.argtypes = [ctypes.c_int]
+        l.wr_fused_moe_expired.restype = ctypes.c_int
         # include/wr_timeline.h (measurement hook)
         l.wr_timeline_read.argtypes = [ctypes.POINTER(ctypes.c_uint64), ctypes.c_int64,
                                        ctypes.c_void_p]

@@ -355,9 +355,13 @@ def set_handoff_check(enabled: bool) -> None:
 
     The single-token kernel hands act from its gate/up blocks to its down
     blocks through arrival counters, with a bounded wait (about 0.2 s).  A
-    wait that expires makes that block write NaN rows and sets a status word.
-    With the check on, ``fused_moe`` reads that word after the call (a
-    stream synchronisation, so not under graph capture) and raises
+    wait that expires makes that block write NaN rows and sets a status word
+    and a host-visible word of the library.  Every ``fused_moe`` call reads
+    the host-visible word after its launch, without a synchronisation, and
+    raises ``RuntimeError`` if it is set: that reports the expiries of the
+    calls whose kernels have run by then, so possibly one call late.  With
+    the check on, ``fused_moe`` also reads this call's status word after the
+    call (a stream synchronisation, so not under graph capture) and raises
     ``RuntimeError`` if it is set.  ``WARP_ROUTE_CHECK_HANDOFF=1`` in the
     environment turns it on at import.  The reference has no such wait: its
     fused kernel is a single warp (src/fused_moe.cu:76-227)."""
