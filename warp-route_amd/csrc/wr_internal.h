@@ -20,14 +20,6 @@
 #define WR_ROUTER_IN_FFN 0
 #endif
 
-// 1: a single-token gate/up block that finishes after the last gate/up block
-// has started takes one of the down blocks' row units itself (claimed from a
-// counter that the launched down blocks also claim from), so that its down
-// loads start without a block dispatch and an expert selection.
-#ifndef WR_FU_DUAL
-#define WR_FU_DUAL 0
-#endif
-
 namespace wr {
 
 struct Problem {
@@ -80,14 +72,7 @@ struct FusedWs {
   static constexpr int kTimeoutWord = kCounters * kCounterStride;
   static constexpr int kRotWord = kTimeoutWord + 2 * kCounterStride;
   static constexpr int kClaimWord = kRotWord + kCounters * kCounterStride;
-  // WR_FU_DUAL: the word after the timeout word is set by the last launched
-  // gate/up block when it starts, and kCounters more words after the claim
-  // counters count the down row units claimed (counter c hands out units c,
-  // c + kCounters, ...).
-  static constexpr int kStartWord = kTimeoutWord + kCounterStride;
-  static constexpr int kDownWord = kClaimWord + kClasses * kCounterStride;
-  static constexpr int kCtrlWords =
-      2 * kCounters + 2 + kClasses + (WR_FU_DUAL ? kCounters : 0);  // zeroed words, kCounterStride apart
+  static constexpr int kCtrlWords = 2 * kCounters + 2 + kClasses;  // zeroed words, kCounterStride apart
   // WR_ROUTER_IN_FFN: router slots after the zeroed words, 16 bytes per
   // expert: two 64-bit words {logit bits, tag half} carrying the tag of the
   // call that wrote them (never zeroed: a slot counts only when it carries

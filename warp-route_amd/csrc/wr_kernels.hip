@@ -604,9 +604,6 @@ struct Handoff {
   unsigned* host_flag;  // host-visible word also set to 1 then, or nullptr
   unsigned* rot;        // FusedWs::kCounters rotation masks, FusedWs::kCounterStride words apart
   unsigned* claim;      // FusedWs::kClasses claim counters, FusedWs::kCounterStride words apart
-  unsigned* started;    // WR_FU_DUAL: set to 1 by gate/up block n1b - 1 when it starts
-  unsigned* dclaim;     // WR_FU_DUAL: FusedWs::kCounters down-unit claim counters, a line each
-  int n2;               // down row units (RPD output rows each)
   int n1;               // gate/up chunk slots, a multiple of 8 LB: one arrival each
   int n1b;              // gate/up blocks launched (the first n1b block ids), a multiple of
                         // 8 LB, at most n1; slots n1b .. n1 - 1 are claimed by them
@@ -752,16 +749,11 @@ __host__ __device__ __forceinline__ int chunk_of_block(int b) {
 }
 
 // Rows [r0, r0 + RPW) of selected expert kk's gate/up matrices; the results go
-// to a[0 .. RPW) with agent-scope stores.  pre() runs after the last weights
-// have been used and before the stores.
-struct NoHook {
-  __device__ void operator()() const {}
-};
-template <typename WT, typename XT, int VEC, int RPW, int U, typename Hook = NoHook>
+// to a[0 .. RPW) with agent-scope stores.
+template <typename WT, typename XT, int VEC, int RPW, int U>
 __device__ __forceinline__ void gateup_item(const WT* __restrict__ wbuf, const XT* __restrict__ xb,
                                             float* a, const Geom& g, const TopK& t, int kk,
-                                            int r0, int lane, const Handoff* hsp = nullptr,
-                                            Hook pre = Hook{}) {
+                                            int r0, int lane, const Handoff* hsp = nullptr) {
   (void)hsp;  // WR_TIMELINE builds of k_fused_ffn record a mark
   typedef typename WVec<WT, VEC>::type V;
   constexpr int CH = kWave * VEC;
@@ -811,7 +803,6 @@ __device__ __forceinline__ void gateup_item(const WT* __restrict__ wbuf, const X
 #if WR_TIMELINE
   if (hsp != nullptr) WR_TL_MARK(*hsp, 7);
 #endif
-  pre();
   const float wk = topk_w(t, kk);
 #pragma unroll
   for (int j = 0; j < RPW; ++j) {
@@ -914,12 +905,12 @@ __device__ __forceinline__ void stage_bytes_lds(const uint8_t* src, unsigned cha
 // global-to-LDS loads (no registers), issued before the first round of
 // weight loads; one wait covers both, so the weights are the only
 // long-lived registers and the copy costs no extra round trip.
-template <typename WT, typename XT, int VEC, int RPW, int U, bool STG, typename Hook = NoHook>
+template <typename WT, typename XT, int VEC, int RPW, int U, bool STG>
 __device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
                                                const XT* __restrict__ xb, float* a,
                                                const Geom& g, int eid, float wk, int r0,
                                                int nrows, int lane, unsigned char* xs_raw,
-                                               const Handoff& hs, Hook pre = Hook{}) {
+                                               const Handoff& hs) {
   (void)hs;  // WR_TIMELINE builds record two marks
   typedef typename WVec<WT, VEC>::type V;
   typedef XlLayout<XT, VEC> L;
@@ -1018,7 +1009,6 @@ __device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
     }
   }
   WR_TL_MARK(hs, 7);
-  pre();
 #pragma unroll
   for (int j = 0; j < RPW; ++j) {
     const float gs = wave_sum(ag[j]);
@@ -1163,45 +1153,17 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
   const int lane = threadIdx.x & (kWave - 1);
   // With XL, readfirstlane keeps the (wave-uniform) wave index, and the item
   // indices derived from it, in SGPRs.
-  const int wave = (XL || (WR_FU_DUAL && CLAIM))
-                       ? __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave)
-                       : (int)threadIdx.x / kWave;
+  const int wave = XL ? __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave)
+                      : (int)threadIdx.x / kWave;
   const int64_t act_row = FusedWs::act_row(g.I, COLS);
 
   WR_TL_MARK(hs, 0);
-#if WR_FU_DUAL
-  // Down row units: launched down blocks claim theirs here (the answer is
-  // read after the selection); gate/up blocks may claim one after their
-  // gate/up work, once gate/up block n1b - 1 has started (its flag below).
-  // Under in-order dispatch every gate/up block is then running or done, so a
-  // block that waits for the hand-off waits only for blocks that never wait.
-  __shared__ int s_unit;
-  unsigned my_unit = (unsigned)hs.n2;
-  if (threadIdx.x == 0) {
-    if ((int)blockIdx.x == hs.n1b - 1)
-      __hip_atomic_store(hs.started, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((int)blockIdx.x >= hs.n1b) {
-      // Launched down block j = id - n1b claims from counter j mod kCounters,
-      // which hands out exactly as many units as there are such blocks, so
-      // every unit is claimed even if no gate/up block takes one.
-      const unsigned c = ((unsigned)blockIdx.x - (unsigned)hs.n1b) % FusedWs::kCounters;
-      my_unit = c + FusedWs::kCounters *
-                        __hip_atomic_fetch_add(hs.dclaim + c * FusedWs::kCounterStride, 1u,
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    else
-      s_unit = hs.n2;  // none, unless the gate/up work below claims one
-  }
-#endif
   TopK t;
 #if WR_ROUTER_IN_FFN
   const bool routed = route_and_select<XT>(x, logits, g, hs, t);
 #else
   block_select_topk(logits, g.E, g.k, g.renorm, t);
   constexpr bool routed = true;
-#endif
-#if WR_FU_DUAL
-  if (threadIdx.x == 0 && (int)blockIdx.x >= hs.n1b) s_unit = (int)min(my_unit, (unsigned)hs.n2);
 #endif
   WR_TL_MARK(hs, 1);
 #if WR_TIMELINE
@@ -1239,34 +1201,7 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
     // gate/up role.
     __shared__ int s_claim;
     const int cls = (int)blockIdx.x % FusedWs::kClasses;
-#if WR_FU_DUAL
-    // The started flag, read into LDS with an agent-coherent (sc1) load that
-    // holds no register; it lands before this wave's weights (loads complete
-    // in order), so thread 0 reads it after its first item's arithmetic.
-    __shared__ unsigned s_flag[1];
-    if (threadIdx.x == 0)
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(hs.started),
-                                       (__attribute__((address_space(3))) void*)s_flag, 4, 0, 16);
-#endif
     for (int v = blockIdx.x;;) {
-      // Thread 0, first item: the down unit claimed once the gate/up work is
-      // computed (its answer arrives during the wait for the act stores), or
-      // n2 for none.
-      unsigned dn_claim;
-      auto pre = [&]() {
-#if WR_FU_DUAL
-        dn_claim = (unsigned)hs.n2;
-        if (threadIdx.x == 0 && v == (int)blockIdx.x) {
-          asm volatile("" ::: "memory");
-          if (s_flag[0] != 0u)
-            dn_claim = blockIdx.x % FusedWs::kCounters +
-                       FusedWs::kCounters *
-                           __hip_atomic_fetch_add(hs.dclaim + (blockIdx.x % FusedWs::kCounters) *
-                                                                  FusedWs::kCounterStride,
-                                                  1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-#endif
-      };
       const int G = chunk_of_block<LB>(v);
       if constexpr (XL) {
         // Wave-uniform by construction; readfirstlane keeps them in SGPRs (the
@@ -1277,27 +1212,19 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
         gateup_item_xl<WT, XT, VEC, RPW, U1, STG>(wbuf, x, act + kk * act_row + it * RPW, g,
                                                   topk_id(t, kk), topk_w(t, kk),
                                                   nrows > 0 ? it * RPW : 0, nrows, lane, lds_raw,
-                                                  hs, pre);
-      } else {
+                                                  hs);
+      } else if (G < hs.chunks) {
         const int kk = G / bpk;
         const int it = (G - kk * bpk) * kWavesPerBlock + wave;
-        if (G < hs.chunks && it < items)
+        if (it < items)
           gateup_item<WT, XT, VEC, RPW, U1>(wbuf, x, act + kk * act_row + it * RPW, g, t, kk,
-                                            it * RPW, lane, &hs, pre);
-        else
-          pre();
+                                            it * RPW, lane, &hs);
       }
-      if (threadIdx.x == 0 && v == (int)blockIdx.x) {
+      if (threadIdx.x == 0 && v == (int)blockIdx.x)
         __hip_atomic_fetch_or(hs.rot + (blockIdx.x % FusedWs::kCounters) * FusedWs::kCounterStride,
                               1u << ((xcc_id() - blockIdx.x) & 7u), __ATOMIC_RELAXED,
                               __HIP_MEMORY_SCOPE_AGENT);
-      }
       __builtin_amdgcn_s_waitcnt(0);  // this wave's act stores have completed
-#if WR_FU_DUAL
-      if (threadIdx.x == 0 && v == (int)blockIdx.x) s_unit = (int)min(dn_claim, (unsigned)hs.n2);
-#else
-      (void)dn_claim;
-#endif
       __syncthreads();
       if (threadIdx.x == 0) {
         __hip_atomic_fetch_add(hs.cnt + (v % FusedWs::kCounters) * FusedWs::kCounterStride, 1u,
@@ -1317,26 +1244,15 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
       }
     }
     WR_TL_MARK(hs, 3);
-#if !WR_FU_DUAL
     return;
-#endif
   }
 
   // ---- down block ----
-#if WR_FU_DUAL
-  // This block's down row unit: a gate/up block's claim (made above), or a
-  // launched down block's (made before the selection).  None left: done.
-  __syncthreads();
-  const int unit = s_unit;
-  if (unit >= hs.n2) return;
-#else
-  const int unit = (int)blockIdx.x - hs.n1b;
-#endif
   constexpr bool kFp8 = std::is_same<WT, fp8w>::value;
   __shared__ float part[kWavesPerBlock][RPD];
   __shared__ float sdn[kFp8 ? WR_MAX_TOPK * RPD : 1];  // fp8 row scales [kk][j]
   __shared__ int expired;  // this block's wait gave up
-  const int r0 = unit * RPD;
+  const int r0 = ((int)blockIdx.x - hs.n1b) * RPD;
   const int nrows = min(RPD, g.h - r0);
   const int nch = (g.I + kWave * VEC - 1) / (kWave * VEC);
   const int C = g.k * nch;
@@ -1687,8 +1603,6 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
   hs.host_flag = p.expired_host;
   hs.rot = w.ctrl + FusedWs::kRotWord;
   hs.claim = w.ctrl + FusedWs::kClaimWord;
-  hs.started = w.ctrl + FusedWs::kStartWord;
-  hs.dclaim = w.ctrl + FusedWs::kDownWord;
   hs.n1 = fused_n1(p.I, p.k, RPW);
   hs.n1b = hs.n1;
   hs.chunks = fused_chunks(p.I, p.k, RPW);
@@ -1702,7 +1616,6 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
   constexpr int RPD = kFp4 ? WR_F4_RPD : (kFp8 ? WR_F8_RPD : WR_FU_RPD);
   constexpr int U2 = kFp4 ? WR_F4_U2 : (kFp8 ? WR_F8_U2 : WR_FU_U);
   const int n2 = (p.h + RPD - 1) / RPD;
-  hs.n2 = n2;
   // Gate/up blocks read x from an LDS copy for small enough h (and, except
   // for MXFP4, few enough gate/up blocks).
   constexpr int kXlMax = xl_max_h<WT>();
