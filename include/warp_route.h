@@ -247,7 +247,8 @@ WR_API int wr_fused_moe_status(const void *workspace, size_t workspace_bytes, vo
  * call with clear != 0: 1 or 0.  A down block whose wait expires also stores
  * 1 to a host-visible word of the library (4 bytes of pinned host memory,
  * allocated by the first wr_fused_moe, wr_fused_moe_opts or wr_fused_moe_ffn
- * call made outside stream capture, held until the process ends;
+ * call, or wr_batched_fused_moe call with one token (which runs the same
+ * kernel), made outside stream capture, held until the process ends;
  * wr_fused_moe_noalloc writes it once it exists).  This reads that word with
  * a host load: no HIP call, no synchronisation, so it may be called after
  * every op, also under graph capture.  An expiry is seen once its kernel has

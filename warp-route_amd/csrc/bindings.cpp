@@ -239,6 +239,7 @@ torch::Tensor batched_fused_moe_forward(torch::Tensor hidden_batch, torch::Tenso
   a.workspace_bytes = (size_t)ws.numel();
   void* stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(dev.index()).stream();
   check_status(wr_batched_fused_moe(&a, stream), "batched_fused_moe_forward");
+  check_expired("batched_fused_moe_forward");
   return out;
 }
 

@@ -371,8 +371,10 @@ WR_API int wr_fused_moe_status(const void* workspace, size_t workspace_bytes, vo
 WR_API int wr_fused_moe_expired(int clear) {
   unsigned* w = g_expired.load(std::memory_order_acquire);
   if (w == nullptr) return 0;
-  const unsigned v = __atomic_load_n(w, __ATOMIC_ACQUIRE);
-  if (v != 0 && clear != 0) __atomic_store_n(w, 0u, __ATOMIC_RELEASE);
+  // Clearing swaps in 0, so that an expiry stored between a read and a
+  // separate clear could not be lost.
+  const unsigned v = clear != 0 ? __atomic_exchange_n(w, 0u, __ATOMIC_ACQ_REL)
+                                : __atomic_load_n(w, __ATOMIC_ACQUIRE);
   return v != 0 ? 1 : 0;
 }
 
@@ -395,6 +397,9 @@ WR_API int wr_batched_fused_moe(const wr_moe_args* args, void* stream) {
   Problem p{};
   const int st = validate(args, WR_KIND_BATCHED, &p);
   if (st != WR_OK || p.B == 0) return st;
+  // One token runs the single-token kernel, whose hand-off expiry is reported
+  // through the host-visible word.
+  if (p.B == 1) p.expired_host = expired_word(true, static_cast<hipStream_t>(stream));
   return hip_status(wr::launch_batched(p, static_cast<hipStream_t>(stream)));
 }
 
