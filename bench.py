@@ -415,6 +415,10 @@ def probe_lib():
                                   ctypes.POINTER(ctypes.c_int64), ctypes.c_int, ctypes.c_int,
                                   ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     lib.wr_probe_read.restype = ctypes.c_int
+    lib.wr_probe_gateup.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int,
+                                    ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_void_p, ctypes.c_void_p]
+    lib.wr_probe_gateup.restype = ctypes.c_int
     return lib
 
 
@@ -503,6 +507,61 @@ def read_probe_bench(args) -> int:
     return 0
 
 
+def gateup_probe_bench(args) -> int:
+    """The gate/up phase's read order against the streaming ceiling: over the
+    gate and up matrices of the selected experts of the rotated layers (16-bit
+    weights), the read-only probe in the single-token kernel's slot order
+    (one workgroup per 8-row slot, as that kernel launches them, and the same
+    slots looped over by 4 workgroups per CU), in a workgroup-level grid
+    stride over 4-row groups, and the grid-stride streaming ceiling
+    (wr_probe_read) over the same bytes."""
+    import ctypes
+    import torch
+    from warp_route import functional as F
+    from warp_route.synthetic import CONFIGS, make_config_layer
+    cfg = CONFIGS[args.config].with_weights(weight_dtype(args.weights))
+    if cfg.weight_dtype not in (torch.float16, torch.bfloat16):
+        raise SystemExit("--gateup-probe takes 16-bit weights")
+    E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
+    row_bytes = 2 * h
+    dev = torch.device("cuda:0")
+    layers = [make_config_layer(cfg, seed=s, device=dev, gen_device=dev)
+              for s in range(args.layers)]
+    stride = F.weight_layout(E, h, I, cfg.weight_dtype)["expert_stride"]
+    bases = []
+    for x, gw, buf in layers:
+        ids, _ = F.gate_topk(x, gw, E, h, k, cfg.renormalize)
+        bases.append([buf.data_ptr() + int(e) * stride for e in ids.tolist()])
+    nbytes = k * 2 * I * row_bytes
+    lib = probe_lib()
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    arrs = [(ctypes.c_void_p * k)(*b) for b in bases]
+    rows = []
+    for name, pattern, blocks in [("kernel slots, one workgroup per slot", 0, k * I // 8),
+                                  ("kernel slots, 4 workgroups per CU looping", 0, 4 * cus),
+                                  ("4-row groups, workgroup grid stride", 1, 4 * cus),
+                                  ("4-row groups, workgroup grid stride", 1, 3 * cus)]:
+        def step(i, pattern=pattern, blocks=blocks):
+            if lib.wr_probe_gateup(arrs[i % len(arrs)], k, row_bytes, I, pattern, blocks,
+                                   ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream)) != 0:
+                raise RuntimeError("wr_probe_gateup failed")
+        us = _timed(step, args.steps, 10)
+        rows.append({"order": name, "workgroups": blocks, "us": round(us, 2),
+                     "GBps": round(nbytes / us / 1e3, 1)})
+    ceil = read_ceiling([[(b, 2 * I * row_bytes) for b in bs] for bs in bases], args.steps)
+    print(json.dumps({
+        "metric": "read-only rate of gate/up read orders (GB/s)", "unit": "GB/s",
+        "config": {"workload": f"{cfg.name} gate and up matrices of the selected experts "
+                               f"({args.weights}), {args.layers} layers rotated",
+                   "bytes_per_call": nbytes, "steps": args.steps},
+        "orders": rows,
+        "grid_stride_ceiling": {k2: ceil[k2] for k2 in ("GBps", "us", "shape")},
+    }), flush=True)
+    return 0
+
+
 def naive_bench(args) -> int:
     """The naive multi-kernel path (warp_route.functional.naive_moe: router,
     host softmax / top-K after one stream synchronisation, then per selected
@@ -580,6 +639,9 @@ def main() -> int:
     ap.add_argument("--copy-probe", action="store_true")
     ap.add_argument("--read-probe", action="store_true",
                     help="time the read-only streaming ceiling over the selected experts")
+    ap.add_argument("--gateup-probe", action="store_true",
+                    help="time the single-token gate/up read order against the streaming "
+                         "ceiling over the same bytes (16-bit weights)")
     ap.add_argument("--probe-sweep", action="store_true",
                     help="with --read-probe: sweep PROBE_SWEEP instead of PROBE_SHAPES")
     ap.add_argument("--op", default="fused", choices=["fused", "naive"],
@@ -620,6 +682,8 @@ def main() -> int:
         return 0
     if args.read_probe:
         return read_probe_bench(args)
+    if args.gateup_probe:
+        return gateup_probe_bench(args)
     if args.op == "naive":
         return naive_bench(args)
     if args.throughput:
