@@ -419,6 +419,8 @@ def probe_lib():
                                     ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_void_p, ctypes.c_void_p]
     lib.wr_probe_gateup.restype = ctypes.c_int
+    lib.wr_probe_down.argtypes = lib.wr_probe_gateup.argtypes
+    lib.wr_probe_down.restype = ctypes.c_int
     return lib
 
 
@@ -551,6 +553,24 @@ def gateup_probe_bench(args) -> int:
         rows.append({"order": name, "workgroups": blocks, "us": round(us, 2),
                      "GBps": round(nbytes / us / 1e3, 1)})
     ceil = read_ceiling([[(b, 2 * I * row_bytes) for b in bs] for bs in bases], args.steps)
+    # The down matrices (h rows of I weights each, after gate and up), in the
+    # kernel's down order (4-row groups, one workgroup per group as launched)
+    # and row-contiguous, against the ceiling over the same bytes.
+    dn_row = 2 * I
+    dn_bases = [[b + 2 * I * row_bytes for b in bs] for bs in bases]
+    dn_arrs = [(ctypes.c_void_p * k)(*b) for b in dn_bases]
+    dn_bytes = k * h * dn_row
+    dn_rows = []
+    for name, pattern, blocks in [("kernel down order, one workgroup per 4 rows", 0, h // 4),
+                                  ("row-contiguous, one workgroup per 4 rows", 1, h // 4)]:
+        def dstep(i, pattern=pattern, blocks=blocks):
+            if lib.wr_probe_down(dn_arrs[i % len(dn_arrs)], k, dn_row, h, pattern, blocks,
+                                 ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream)) != 0:
+                raise RuntimeError("wr_probe_down failed")
+        us = _timed(dstep, args.steps, 10)
+        dn_rows.append({"order": name, "workgroups": blocks, "us": round(us, 2),
+                        "GBps": round(dn_bytes / us / 1e3, 1)})
+    dn_ceil = read_ceiling([[(b, h * dn_row) for b in bs] for bs in dn_bases], args.steps)
     print(json.dumps({
         "metric": "read-only rate of gate/up read orders (GB/s)", "unit": "GB/s",
         "config": {"workload": f"{cfg.name} gate and up matrices of the selected experts "
@@ -558,6 +578,8 @@ def gateup_probe_bench(args) -> int:
                    "bytes_per_call": nbytes, "steps": args.steps},
         "orders": rows,
         "grid_stride_ceiling": {k2: ceil[k2] for k2 in ("GBps", "us", "shape")},
+        "down": {"bytes_per_call": dn_bytes, "orders": dn_rows,
+                 "grid_stride_ceiling": {k2: dn_ceil[k2] for k2 in ("GBps", "us", "shape")}},
     }), flush=True)
     return 0
 

@@ -57,6 +57,21 @@ WR_PROBE_API int wr_probe_read(const void *const *ptrs, const int64_t *bytes, in
 WR_PROBE_API int wr_probe_gateup(const void *const *experts, int n_experts, int64_t row_bytes,
                                  int I, int pattern, int blocks, uint32_t *sink, void *stream);
 
+/* Reads the down matrices of n_experts experts (down[i]: h rows of row_bytes,
+ * the intermediate dimension of 16-bit weights) in groups of 4 rows, workgroup
+ * b taking groups b, b + blocks, ...:
+ *   pattern 0: the single-token kernel's down order -- the group's 1 KB column
+ *              chunks of all experts (the last of a row partial),
+ *              wave w taking q = w, w + 4, ..., four chunks of all 4 rows per
+ *              round (16 loads per lane), rounds one after another;
+ *   pattern 1: row-contiguous -- wave w reads row w of the group, expert after
+ *              expert, 16 consecutive 1 KB loads per round.
+ * row_bytes must be a multiple of 16 and at most 65536, h a positive
+ * multiple of 4; rows must start 16-byte aligned.  Returns 0, -1 for invalid arguments (checked before any HIP
+ * call) or -2 if the launch failed; *sink as for wr_probe_read. */
+WR_PROBE_API int wr_probe_down(const void *const *down, int n_experts, int64_t row_bytes, int h,
+                               int pattern, int blocks, uint32_t *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

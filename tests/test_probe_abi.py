@@ -24,12 +24,13 @@ def lib():
     lib.wr_probe_gateup.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int,
                                     ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_void_p, ctypes.c_void_p]
+    lib.wr_probe_down.argtypes = lib.wr_probe_gateup.argtypes
     return lib
 
 
 def test_exports_every_declared_entry_point(lib):
     names = re.findall(r"WR_PROBE_API\s+[\w\s\*]+?\b(wr_probe_\w+)\s*\(", open(HEADER).read())
-    assert sorted(names) == ["wr_probe_gateup", "wr_probe_read"]
+    assert sorted(names) == ["wr_probe_down", "wr_probe_gateup", "wr_probe_read"]
     for n in names:
         assert hasattr(lib, n), n
 
@@ -56,6 +57,19 @@ def test_gateup_rejects_null_and_unaligned_pointers(lib):
     for bad in ((FAKE, 0), (FAKE, FAKE + 8)):
         p = (ctypes.c_void_p * 2)(*bad)
         assert lib.wr_probe_gateup(p, 2, 8192, 14336, 0, 1, ctypes.c_void_p(FAKE), None) == -1
+
+
+@pytest.mark.parametrize("n_experts,row_bytes,h,pattern,blocks", [
+    (0, 28672, 4096, 0, 1), (9, 28672, 4096, 0, 1),       # expert count
+    (2, 8, 4096, 0, 1), (2, 28670, 4096, 0, 1),           # row length: >= 16, whole 16 B
+    (2, 65552, 4096, 0, 1),                               # row length: at most 64 KB
+    (2, 28672, 4094, 0, 1), (2, 28672, 0, 0, 1),          # h not a positive multiple of 4
+    (2, 28672, 4096, 2, 1), (2, 28672, 4096, 0, 0),       # pattern, grid
+])
+def test_down_rejects_invalid_arguments(lib, n_experts, row_bytes, h, pattern, blocks):
+    ptrs = (ctypes.c_void_p * 9)(*([FAKE] * 9))
+    assert lib.wr_probe_down(ptrs, n_experts, row_bytes, h, pattern, blocks,
+                             ctypes.c_void_p(FAKE), None) == -1
 
 
 def test_read_rejects_invalid_arguments(lib):

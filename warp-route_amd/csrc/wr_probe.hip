@@ -123,6 +123,66 @@ __global__ __launch_bounds__(256) void k_probe_rows(Experts ex, int64_t rowb, in
     sink[0] = acc[0] ^ acc[3] ^ (uint32_t)z;
 }
 
+// Down, pattern 0: the single-token kernel's order (see wr_probe_down).
+__global__ __launch_bounds__(256) void k_probe_down_kernel(Experts ex, int nexp, int64_t rowb, int h,
+                                                           uint32_t* sink) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nch = (int)((rowb + 1023) / 1024), C = nexp * nch;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  int z = 0;
+  for (int r0 = blockIdx.x * 4; r0 < h; r0 += gridDim.x * 4) {
+    for (int q0 = wave; q0 < C; q0 += 16) {
+      u32x4 a[16];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int q = q0 + 4 * u;
+        const int e = q < C ? q / nch : 0;
+        const int col = (q - e * nch) * 1024 + lane * 16;  // byte in the row
+        const bool ok = q < C && col < rowb;
+        const unsigned char* D = ex.p[e] + (int64_t)r0 * rowb + col + z;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          a[4 * u + j] = ok ? ld16(D + j * rowb) : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc ^= a[i];
+      z = dep_zero(acc[0]);
+    }
+  }
+  if (acc[0] == 0x9e3779b9u && acc[1] == 0x7f4a7c15u && acc[2] == 0x85ebca6bu &&
+      acc[3] == 0xc2b2ae35u)
+    sink[0] = acc[0] ^ acc[3] ^ (uint32_t)z;
+}
+
+// Down, pattern 1: wave w reads row w of the group, 16 consecutive 1 KB loads
+// per round over the concatenation of the experts' rows.
+__global__ __launch_bounds__(256) void k_probe_down_rows(Experts ex, int nexp, int64_t rowb, int h,
+                                                         uint32_t* sink) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nch = (int)((rowb + 1023) / 1024), C = nexp * nch;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  int z = 0;
+  for (int r0 = blockIdx.x * 4; r0 < h; r0 += gridDim.x * 4) {
+    for (int q0 = 0; q0 < C; q0 += 16) {
+      u32x4 a[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int q = q0 + u;
+        const int e = q < C ? q / nch : 0;
+        const int col = (q - e * nch) * 1024 + lane * 16;
+        a[u] = (q < C && col < rowb) ? ld16(ex.p[e] + (int64_t)(r0 + wave) * rowb + col + z)
+                                     : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc ^= a[i];
+      z = dep_zero(acc[0]);
+    }
+  }
+  if (acc[0] == 0x9e3779b9u && acc[1] == 0x7f4a7c15u && acc[2] == 0x85ebca6bu &&
+      acc[3] == 0xc2b2ae35u)
+    sink[0] = acc[0] ^ acc[3] ^ (uint32_t)z;
+}
+
 int cu_count() {
   int dev = 0, n = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 256;
@@ -187,5 +247,27 @@ extern "C" WR_PROBE_API int wr_probe_gateup(const void* const* experts, int n_ex
     else
       hipLaunchKernelGGL(k_probe_rows<2>, grid, block, 0, s, ex, row_bytes, I, nrows, sink);
   }
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+extern "C" WR_PROBE_API int wr_probe_down(const void* const* down, int n_experts, int64_t row_bytes,
+                                          int h, int pattern, int blocks, uint32_t* sink,
+                                          void* stream) {
+  if (down == nullptr || sink == nullptr) return -1;
+  if (n_experts < 1 || n_experts > WR_PROBE_MAX_EXPERTS) return -1;
+  if (row_bytes < 16 || row_bytes > 65536 || row_bytes % 16 != 0) return -1;
+  if (h < 4 || h % 4 != 0 || (pattern != 0 && pattern != 1) || blocks < 1) return -1;
+  Experts ex{};
+  for (int i = 0; i < n_experts; ++i) {
+    if (down[i] == nullptr || reinterpret_cast<uintptr_t>(down[i]) % 16 != 0) return -1;
+    ex.p[i] = static_cast<const unsigned char*>(down[i]);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pattern == 0)
+    hipLaunchKernelGGL(k_probe_down_kernel, dim3(blocks), dim3(256), 0, s, ex, n_experts, row_bytes,
+                       h, sink);
+  else
+    hipLaunchKernelGGL(k_probe_down_rows, dim3(blocks), dim3(256), 0, s, ex, n_experts, row_bytes,
+                       h, sink);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
