@@ -234,7 +234,19 @@ def timeline_summary(step, n_calls: int) -> dict:
             "kernel_end": float(max(t[gu, 3].max() if gu.any() else 0.0,
                                     t[dn, 4].max() if dn.any() else 0.0)),
         })
-    out = {k: round(float(np.nanmedian([r[k] for r in rows])), 2) for k in rows[0]}
+        # Down workgroups by start: per fifth of them in start order, the
+        # median start and end relative to the call's median release.
+        if dn.sum() >= 5:
+            rel = np.median(t[dn, 3])
+            order = np.argsort(t[dn, 0])
+            for f in range(5):
+                sel = order[f * len(order) // 5:(f + 1) * len(order) // 5]
+                rows[-1][f"dn_fifth{f}_start_rel_release"] = q(t[dn, 0][sel] - rel, 50)
+                rows[-1][f"dn_fifth{f}_end_after_release"] = q(t[dn, 4][sel] - rel, 50)
+    import warnings
+    with warnings.catch_warnings():  # a phase this kernel variant does not mark is all NaN
+        warnings.simplefilter("ignore", RuntimeWarning)
+        out = {k: round(float(np.nanmedian([r[k] for r in rows])), 2) for k in rows[0]}
     out = {k: v for k, v in out.items() if v == v}  # phases this kernel variant does not mark
     out["calls"] = n_calls
     out["clock_khz"] = int(khz)
