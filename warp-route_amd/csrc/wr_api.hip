@@ -82,12 +82,12 @@ wr_layout_info layout_of(int64_t E, int64_t h, int64_t I, int wdt) {
 size_t ws_bytes(int kind, int E, int h, int I, int k, int B) {
   switch (kind) {
     case WR_KIND_FUSED:
-      return wr::FusedWs::bytes(E, h, I, k, 1);
+      return wr::FusedWs::bytes(E, I, k, 1);
     case WR_KIND_BATCHED:
       // B > 1 runs either the grouped MFMA path or the per-token kernels,
       // depending on dtype and alignment: size for both.
-      return B > 1 ? std::max(wr::FusedWs::bytes(E, h, I, k, B), wr::BatchWs::bytes(E, h, I, k, B))
-                   : wr::FusedWs::bytes(E, h, I, k, 1);
+      return B > 1 ? std::max(wr::FusedWs::bytes(E, I, k, B), wr::BatchWs::bytes(E, h, I, k, B))
+                   : wr::FusedWs::bytes(E, I, k, 1);
     case WR_KIND_NAIVE:
       return wr::NaiveWs::bytes(E, h, I);
     default:

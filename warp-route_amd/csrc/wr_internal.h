@@ -9,19 +9,6 @@
 
 #include "warp_route.h"
 
-// 1: the single-token down blocks of 16-bit and fp32 weights split the last
-// WR_FU_PAIR_PCT percent of their row units: the last round of each is
-// computed by one of the first down blocks, and the second of the unit's two
-// parts to finish adds them and writes the rows.
-#ifndef WR_FU_TAILQ
-#define WR_FU_TAILQ 0
-#endif
-// Percent of the down units whose last round an early down block computes.
-#ifndef WR_FU_PAIR_PCT
-#define WR_FU_PAIR_PCT 20
-#endif
-static_assert(WR_FU_PAIR_PCT >= 0 && WR_FU_PAIR_PCT <= 50, "a unit is split at most once");
-
 // 1: the single-token kernel computes the router rows itself and publishes
 // them to its other blocks (wr_kernels.hip, route_and_select): one launch per
 // layer.  0 (the default): a router launch ahead of it, whose first block
@@ -103,16 +90,10 @@ struct FusedWs {
   // columns one gate/up block computes (4 waves x rows per wave: 8 or 16).
   static constexpr int kMaxActCols = 16;
 
-  // WR_FU_TAILQ, one token: per down row unit of kTailRows rows, an arrival
-  // word (zeroed by the router launch) and the fp32 sums of its two parts.
-  static constexpr int kTailRows = 4;
-
   unsigned* ctrl;  // kCtrlBytes
   float* logits;   // [B][WR_MAX_EXPERTS]: token b's E logits, padded to 64
   float* act;      // B == 1: [k][act_row(I, cols)]; B > 1: [B][k][I].
                    // Values are already scaled by the gate weight.
-  unsigned* ucnt;  // WR_FU_TAILQ, B == 1: [tail_units(h)], else nullptr
-  float* upart;    // WR_FU_TAILQ, B == 1: [tail_units(h)][2][kTailRows]
 
   __host__ __device__ static int64_t act_row(int I, int cols) {
     return (int64_t)((I + cols - 1) / cols) * cols;
@@ -120,32 +101,19 @@ struct FusedWs {
   static size_t act_floats(int I, int k, int B) {
     return B == 1 ? (size_t)k * act_row(I, kMaxActCols) : (size_t)B * k * I;
   }
-  static int tail_units(int h) { return (h + kTailRows - 1) / kTailRows; }
-  static size_t tail_bytes(int h, int B) {
-    return (WR_FU_TAILQ && B == 1)
-               ? align_up((size_t)tail_units(h) * 4, kWsAlign) +
-                     align_up((size_t)tail_units(h) * 2 * kTailRows * 4, kWsAlign)
-               : 0;
-  }
-  static size_t bytes(int E, int h, int I, int k, int B) {
+  static size_t bytes(int E, int I, int k, int B) {
     (void)E;
     return kCtrlBytes + (size_t)B * WR_MAX_EXPERTS * 4 +
-           align_up(act_floats(I, k, B) * 4, kWsAlign) + tail_bytes(h, B);
+           align_up(act_floats(I, k, B) * 4, kWsAlign);
   }
-  static FusedWs carve(char* ws, int E, int h, int I, int k, int B) {
+  static FusedWs carve(char* ws, int E, int I, int k, int B) {
     FusedWs w;
     w.ctrl = reinterpret_cast<unsigned*>(ws);
     w.logits = reinterpret_cast<float*>(ws + kCtrlBytes);
     w.act = reinterpret_cast<float*>(ws + kCtrlBytes + (size_t)B * WR_MAX_EXPERTS * 4);
-    w.ucnt = nullptr;
-    w.upart = nullptr;
-    if (tail_bytes(h, B) > 0) {
-      char* t = ws + kCtrlBytes + (size_t)B * WR_MAX_EXPERTS * 4 +
-                align_up(act_floats(I, k, B) * 4, kWsAlign);
-      w.ucnt = reinterpret_cast<unsigned*>(t);
-      w.upart = reinterpret_cast<float*>(t + align_up((size_t)tail_units(h) * 4, kWsAlign));
-    }
     (void)E;
+    (void)I;
+    (void)k;
     return w;
   }
 };

@@ -210,9 +210,7 @@ struct XSplit {
 // so that consumers can read all 64 with scalar loads).  Block (0, 0) also
 // zeroes the words zero[i * zstride], i < nzero <= kBlock (the single-token
 // kernel's arrival counters, timeout flag, rotation masks and claim
-// counters), which the next kernel on the stream reads, and the nzero2
-// consecutive words at zero2 (the down units' arrival words of the shared
-// last rounds), if any.  With xs.hi != NULL,
+// counters), which the next kernel on the stream reads.  With xs.hi != NULL,
 // block (e, b) also writes its 1/E
 // share of token b's split x (XSplit); every block of the token derives the
 // same exponent from the whole row.
@@ -221,9 +219,7 @@ __global__ __launch_bounds__(kBlock) void k_router_logits(const float* __restric
                                                           const XT* __restrict__ x,
                                                           float* __restrict__ logits, int E,
                                                           int h, unsigned* __restrict__ zero,
-                                                          int nzero, int zstride, XSplit xs,
-                                                          unsigned* __restrict__ zero2,
-                                                          int nzero2) {
+                                                          int nzero, int zstride, XSplit xs) {
   __shared__ float part[4];
   __shared__ float pmax[4];
   const int q = threadIdx.x / kWave;
@@ -238,8 +234,6 @@ __global__ __launch_bounds__(kBlock) void k_router_logits(const float* __restric
   }
   if (zero != nullptr && e == 0 && b == 0 && (int)threadIdx.x < nzero)
     zero[(int64_t)threadIdx.x * zstride] = 0u;
-  if (zero2 != nullptr && e == 0 && b == 0)
-    for (int i = threadIdx.x; i < nzero2; i += kBlock) zero2[i] = 0u;
   __syncthreads();
   if (threadIdx.x == 0) logits[(int64_t)b * WR_MAX_EXPERTS + e] = router_combine(part);
   if (xs.hi != nullptr) {
@@ -610,9 +604,6 @@ struct Handoff {
   unsigned* host_flag;  // host-visible word also set to 1 then, or nullptr
   unsigned* rot;        // FusedWs::kCounters rotation masks, FusedWs::kCounterStride words apart
   unsigned* claim;      // FusedWs::kClasses claim counters, FusedWs::kCounterStride words apart
-  unsigned* ucnt;       // WR_FU_TAILQ: per down unit, parts finished (zeroed by the router launch)
-  float* upart;         // WR_FU_TAILQ: per down unit, [2][RPD] part sums
-  int n2;               // down row units (RPD rows each)
   int n1;               // gate/up chunk slots, a multiple of 8 LB: one arrival each
   int n1b;              // gate/up blocks launched (the first n1b block ids), a multiple of
                         // 8 LB, at most n1; slots n1b .. n1 - 1 are claimed by them
@@ -1261,11 +1252,7 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
   __shared__ float part[kWavesPerBlock][RPD];
   __shared__ float sdn[kFp8 ? WR_MAX_TOPK * RPD : 1];  // fp8 row scales [kk][j]
   __shared__ int expired;  // this block's wait gave up
-#if WR_FU_TAILQ
-  static_assert(!WR_ROUTER_IN_FFN, "the router launch zeroes the shared rounds' words");
-#endif
-  const int unit = (int)blockIdx.x - hs.n1b;  // this block's row unit
-  const int r0 = unit * RPD;
+  const int r0 = ((int)blockIdx.x - hs.n1b) * RPD;
   const int nrows = min(RPD, g.h - r0);
   const int nch = (g.I + kWave * VEC - 1) / (kWave * VEC);
   const int C = g.k * nch;
@@ -1432,100 +1419,22 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
       down_tile_fma<WT, V, VEC, RPD, 1>(acc, lw, act, g, act_row, q, nch, lane, sdn);
     }
   }
-  // Rounds of the block after the prefetched chunks: U2 chunks per wave.
-  // WR_FU_TAILQ (16-bit and fp32 weights): the last round of every unit is
-  // shared -- this block computes its unit up to it, and then the last
-  // rounds of any units, claimed one at a time.
-#if WR_FU_TAILQ
-  constexpr bool kTail = !XL && !kFp8 && RPD == FusedWs::kTailRows;
-#else
-  constexpr bool kTail = false;
-#endif
-  constexpr int kRound = kWavesPerBlock * U2;
-  if constexpr (!kTail) {
-    for (int q0 = wave + kWavesPerBlock * (U2 + PRE + spre); q0 < C; q0 += kRound) {
-      V wv[U2][RPD];
-      down_tile_load<WT, VEC, RPD, U2, STG>(wv, wbuf, g, t, r0, nrows, q0, nch, lane);
-      if constexpr (STG) down_tile_scales<WT, VEC, RPD, U2>(wv, lds_raw, g, nrows, q0, nch, lane);
-      down_tile_fma<WT, V, VEC, RPD, U2>(acc, wv, act, g, act_row, q0, nch, lane, sdn);
-    }
-#pragma unroll
-    for (int j = 0; j < RPD; ++j) {
-      const float s = wave_sum(acc[j]);
-      if (lane == 0) part[wave][j] = s;
-    }
-    __syncthreads();
-    if (wave == 0 && lane < nrows)
-      out[r0 + lane] = to_out<XT>(expired ? __builtin_nanf("")
-                                          : (part[0][lane] + part[1][lane]) +
-                                                (part[2][lane] + part[3][lane]));
-  } else {
-    // Down blocks are dispatched in index order as gate/up blocks leave, and
-    // the last ones get their prefetched data last: they set the kernel's end.
-    // So the last round of each of the m = n2 WR_FU_PAIR_PCT / 100 last units
-    // is computed by one of the first m blocks, which end earliest: block e
-    // takes unit n2 - 1 - e's last round after its own unit.  Such a unit's two
-    // parts -- the owner's rounds (part 0) and that last round (part 1) --
-    // store their row sums, each then counts itself on the unit's word, and
-    // the one that counts second writes out = part 0 + part 1 (the same sums
-    // whichever block ends first, so the rows are deterministic).  Without a
-    // round after the prefetch there is nothing to move.
-    const int qpost = kWavesPerBlock * (U2 + PRE + spre);
-    const int nround = C > qpost ? (C - qpost + kRound - 1) / kRound : 0;
-    const int qlast = nround > 0 ? qpost + kRound * (nround - 1) : C;
-    const int m = nround > 0 ? (int)((int64_t)hs.n2 * WR_FU_PAIR_PCT / 100) : 0;
-    const bool late = unit >= hs.n2 - m;   // its last round is done by block n2 - 1 - unit
-    const bool early = unit < m && !late;  // it does the last round of unit n2 - 1 - unit
-    int cu = unit, cr0 = r0, cnr = nrows;  // the unit whose rounds are computed
-    int qb = qpost, qstop = late ? qlast : C;
-    int pidx = late ? 0 : -1;  // the part computed: 0 or 1 of a split unit, -1 a whole unit
-    for (;;) {
-      for (; qb < qstop; qb += kRound) {
-        V wv[U2][RPD];
-        down_tile_load<WT, VEC, RPD, U2, STG>(wv, wbuf, g, t, cr0, cnr, qb + wave, nch, lane);
-        down_tile_fma<WT, V, VEC, RPD, U2>(acc, wv, act, g, act_row, qb + wave, nch, lane, sdn);
-      }
-#pragma unroll
-      for (int j = 0; j < RPD; ++j) {
-        const float sj = wave_sum(acc[j]);
-        if (lane == 0) part[wave][j] = sj;
-        acc[j] = 0.0f;
-      }
-      __syncthreads();
-      if (wave == 0) {
-        const float sum = expired ? __builtin_nanf("")
-                                  : (part[0][lane & (RPD - 1)] + part[1][lane & (RPD - 1)]) +
-                                        (part[2][lane & (RPD - 1)] + part[3][lane & (RPD - 1)]);
-        if (pidx < 0) {
-          if (lane < cnr) out[cr0 + lane] = to_out<XT>(sum);
-        } else {
-          float* up = hs.upart + (int64_t)cu * 2 * RPD;
-          if (lane < cnr)
-            __hip_atomic_store(up + pidx * RPD + lane, sum, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-          __builtin_amdgcn_s_waitcnt(0);  // the part's sums have completed
-          unsigned old = 0;
-          if (lane == 0)
-            old = __hip_atomic_fetch_add(hs.ucnt + cu, 1u, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-          old = __shfl(old, 0);
-          if (old == 1u && lane < cnr) {
-            const float other = __hip_atomic_load(up + (1 - pidx) * RPD + lane, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-            out[cr0 + lane] = to_out<XT>(pidx == 0 ? sum + other : other + sum);
-          }
-        }
-      }
-      if (!early || pidx == 1) break;
-      __syncthreads();  // part free
-      cu = hs.n2 - 1 - unit;
-      cr0 = cu * RPD;
-      cnr = min(RPD, g.h - cr0);
-      qb = qlast;
-      qstop = C;
-      pidx = 1;
-    }
+  for (int q0 = wave + kWavesPerBlock * (U2 + PRE + spre); q0 < C; q0 += kWavesPerBlock * U2) {
+    V wv[U2][RPD];
+    down_tile_load<WT, VEC, RPD, U2, STG>(wv, wbuf, g, t, r0, nrows, q0, nch, lane);
+    if constexpr (STG) down_tile_scales<WT, VEC, RPD, U2>(wv, lds_raw, g, nrows, q0, nch, lane);
+    down_tile_fma<WT, V, VEC, RPD, U2>(acc, wv, act, g, act_row, q0, nch, lane, sdn);
   }
+#pragma unroll
+  for (int j = 0; j < RPD; ++j) {
+    const float s = wave_sum(acc[j]);
+    if (lane == 0) part[wave][j] = s;
+  }
+  __syncthreads();
+  if (wave == 0 && lane < nrows)
+    out[r0 + lane] = to_out<XT>(expired ? __builtin_nanf("")
+                                        : (part[0][lane] + part[1][lane]) +
+                                              (part[2][lane] + part[3][lane]));
   WR_TL_MARK(hs, 4);
 }
 
@@ -1587,16 +1496,15 @@ bool router_vec4(const Problem& p) {
 
 template <typename XT>
 hipError_t logits_t(const Problem& p, float* logits, unsigned* zero, int nzero, int zstride,
-                    hipStream_t s, XSplit xs = XSplit{nullptr, nullptr, nullptr, nullptr, 0, 0},
-                    unsigned* zero2 = nullptr, int nzero2 = 0) {
+                    hipStream_t s, XSplit xs = XSplit{nullptr, nullptr, nullptr, nullptr, 0, 0}) {
   const dim3 grid(p.E, p.B);
   const XT* x = static_cast<const XT*>(p.x);
   if (router_vec4(p))
     hipLaunchKernelGGL((k_router_logits<XT, 4>), grid, dim3(kBlock), 0, s, p.gate_w, x, logits,
-                       p.E, p.h, zero, nzero, zstride, xs, zero2, nzero2);
+                       p.E, p.h, zero, nzero, zstride, xs);
   else
     hipLaunchKernelGGL((k_router_logits<XT, 1>), grid, dim3(kBlock), 0, s, p.gate_w, x, logits,
-                       p.E, p.h, zero, nzero, zstride, xs, zero2, nzero2);
+                       p.E, p.h, zero, nzero, zstride, xs);
   return hipGetLastError();
 }
 
@@ -1695,8 +1603,6 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
   hs.host_flag = p.expired_host;
   hs.rot = w.ctrl + FusedWs::kRotWord;
   hs.claim = w.ctrl + FusedWs::kClaimWord;
-  hs.ucnt = w.ucnt;
-  hs.upart = w.upart;
   hs.n1 = fused_n1(p.I, p.k, RPW);
   hs.n1b = hs.n1;
   hs.chunks = fused_chunks(p.I, p.k, RPW);
@@ -1710,7 +1616,6 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
   constexpr int RPD = kFp4 ? WR_F4_RPD : (kFp8 ? WR_F8_RPD : WR_FU_RPD);
   constexpr int U2 = kFp4 ? WR_F4_U2 : (kFp8 ? WR_F8_U2 : WR_FU_U);
   const int n2 = (p.h + RPD - 1) / RPD;
-  hs.n2 = n2;
   // Gate/up blocks read x from an LDS copy for small enough h (and, except
   // for MXFP4, few enough gate/up blocks).
   constexpr int kXlMax = xl_max_h<WT>();
@@ -1831,20 +1736,18 @@ hipError_t ffn_x(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
 // Router logits into the workspace; for one token also the reset of the
 // single-token kernel's control words, which start each call at zero.
 hipError_t run_route(const Problem& p, hipStream_t s) {
-  const FusedWs w = FusedWs::carve(p.ws, p.E, p.h, p.I, p.k, p.B);
+  const FusedWs w = FusedWs::carve(p.ws, p.E, p.I, p.k, p.B);
   static_assert(FusedWs::kCtrlWords <= kBlock, "one router thread zeroes each control word");
   unsigned* zero = p.B == 1 ? w.ctrl : nullptr;
   const int nz = FusedWs::kCtrlWords, zs = FusedWs::kCounterStride;
-  const XSplit none{nullptr, nullptr, nullptr, nullptr, 0, 0};
-  const int nz2 = w.ucnt != nullptr ? FusedWs::tail_units(p.h) : 0;
-  return p.adt == WR_F16 ? logits_t<f16>(p, w.logits, zero, nz, zs, s, none, w.ucnt, nz2)
-                         : logits_t<float>(p, w.logits, zero, nz, zs, s, none, w.ucnt, nz2);
+  return p.adt == WR_F16 ? logits_t<f16>(p, w.logits, zero, nz, zs, s)
+                         : logits_t<float>(p, w.logits, zero, nz, zs, s);
 }
 
 // The expert FFN from the logits run_route left in the workspace (fold =
 // false), or for one token with the router inside the FFN kernel.
 hipError_t run_ffn_only(const Problem& p, bool fold, hipStream_t s) {
-  const FusedWs w = FusedWs::carve(p.ws, p.E, p.h, p.I, p.k, p.B);
+  const FusedWs w = FusedWs::carve(p.ws, p.E, p.I, p.k, p.B);
   return p.adt == WR_F16 ? ffn_x<f16>(p, w, fold, s) : ffn_x<float>(p, w, fold, s);
 }
 
