@@ -81,3 +81,33 @@ def test_read_rejects_invalid_arguments(lib):
     assert lib.wr_probe_read(p, n, 1, 1, 3, sink, None) == -1          # unroll
     n_bad = (ctypes.c_int64 * 1)(1000)                                   # not whole 16 B
     assert lib.wr_probe_read(p, n_bad, 1, 1, 1, sink, None) == -1
+
+
+@pytest.mark.gpu
+def test_probe_patterns_run_on_small_experts(cuda, lib):
+    """Every pattern of wr_probe_gateup and wr_probe_down, and wr_probe_read,
+    over two small packed experts (h = 2048 and 4096 fp16 rows, I = 64):
+    each returns 0, and none writes the sink (random bytes never fold to the
+    value that would)."""
+    import torch
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for h in (2048, 4096):
+        I, row = 64, 2 * h
+        expert = 3 * I * row  # gate, up [I][h] and down [h][I], fp16
+        buf = torch.randint(0, 255, (2 * expert,), dtype=torch.uint8, device=cuda)
+        sink = torch.zeros(4, dtype=torch.int32, device=cuda)
+        gu = (ctypes.c_void_p * 2)(buf.data_ptr(), buf.data_ptr() + expert)
+        dn = (ctypes.c_void_p * 2)(buf.data_ptr() + 2 * I * row,
+                                   buf.data_ptr() + expert + 2 * I * row)
+        print(f"[gpu] probe patterns h={h}", flush=True)
+        for pattern in (0, 1):
+            for blocks in (1, 7, 64):
+                assert lib.wr_probe_gateup(gu, 2, row, I, pattern, blocks,
+                                           ctypes.c_void_p(sink.data_ptr()), stream) == 0
+                assert lib.wr_probe_down(dn, 2, 2 * I, h, pattern, blocks,
+                                         ctypes.c_void_p(sink.data_ptr()), stream) == 0
+        n = (ctypes.c_int64 * 1)(2 * expert)
+        p = (ctypes.c_void_p * 1)(buf.data_ptr())
+        assert lib.wr_probe_read(p, n, 1, 2, 4, ctypes.c_void_p(sink.data_ptr()), stream) == 0
+        torch.cuda.synchronize()
+        assert int(sink.abs().sum()) == 0
