@@ -416,6 +416,26 @@ def stack_bench(args) -> int:
     return 0
 
 
+def bench_config(args):
+    """The layer shape of this run: --config with --weights, and with
+    --tp-shard G one GPU's share of a G-way split over I (the same packed
+    layout with I' = I / G; the router is replicated, so every shard routes
+    as the whole layer does).  Exits with status 2 if G does not divide I
+    into whole rows of the format."""
+    from warp_route.synthetic import CONFIGS
+    cfg = CONFIGS[args.config].with_weights(weight_dtype(args.weights))
+    G = args.tp_shard
+    if G > 1:
+        if cfg.intermediate_dim % G or (args.weights == "mxfp4"
+                                        and (cfg.intermediate_dim // G) % 32):
+            print(f"--tp-shard {G} does not divide I = {cfg.intermediate_dim} "
+                  f"into whole rows for {args.weights}", file=sys.stderr)
+            raise SystemExit(2)
+        cfg = dataclasses.replace(cfg, intermediate_dim=cfg.intermediate_dim // G,
+                                  name=f"{cfg.name}_tp{G}")
+    return cfg
+
+
 def probe_lib():
     """ctypes handle of libwr_probe.so (include/wr_probe.h)."""
     import ctypes
@@ -499,8 +519,8 @@ def read_probe_bench(args) -> int:
     bytes of the rotated layers (what one MoE call must read), and over one
     contiguous 1 GiB buffer."""
     import torch
-    from warp_route.synthetic import CONFIGS, make_config_layer
-    cfg = CONFIGS[args.config].with_weights(weight_dtype(args.weights))
+    from warp_route.synthetic import make_config_layer
+    cfg = bench_config(args)
     dev = torch.device("cuda:0")
     layers = [make_config_layer(cfg, seed=s, device=dev, gen_device=dev)
               for s in range(args.layers)]
@@ -532,8 +552,8 @@ def gateup_probe_bench(args) -> int:
     import ctypes
     import torch
     from warp_route import functional as F
-    from warp_route.synthetic import CONFIGS, make_config_layer
-    cfg = CONFIGS[args.config].with_weights(weight_dtype(args.weights))
+    from warp_route.synthetic import make_config_layer
+    cfg = bench_config(args)
     if cfg.weight_dtype not in (torch.float16, torch.bfloat16):
         raise SystemExit("--gateup-probe takes 16-bit weights")
     E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
@@ -604,8 +624,8 @@ def naive_bench(args) -> int:
     the comparison of benchmarks/bench_latency.cu:83-122 in the reference."""
     import torch
     from warp_route import functional as F
-    from warp_route.synthetic import CONFIGS, make_config_layer
-    cfg = CONFIGS[args.config].with_weights(weight_dtype(args.weights))
+    from warp_route.synthetic import make_config_layer
+    cfg = bench_config(args)
     E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
     dev = torch.device("cuda:0")
     layers = [make_config_layer(cfg, seed=s, device=dev, gen_device=dev)
@@ -728,20 +748,10 @@ def main() -> int:
         return stack_bench(args)
 
     from warp_route import functional as F
-    from warp_route.synthetic import CONFIGS, make_config_layer
+    from warp_route.synthetic import make_config_layer
 
-    cfg = CONFIGS[args.config].with_weights(weight_dtype(args.weights))
+    cfg = bench_config(args)
     G = args.tp_shard
-    if G > 1:
-        # The shard is the same packed layout with I' = I / G; the router is
-        # replicated, so every shard routes as the whole layer does.
-        if cfg.intermediate_dim % G or (args.weights == "mxfp4"
-                                        and (cfg.intermediate_dim // G) % 32):
-            print(f"--tp-shard {G} does not divide I = {cfg.intermediate_dim} "
-                  f"into whole rows for {args.weights}", file=sys.stderr)
-            return 2
-        cfg = dataclasses.replace(cfg, intermediate_dim=cfg.intermediate_dim // G,
-                                  name=f"{cfg.name}_tp{G}")
     E, h, I, k = cfg.num_experts, cfg.hidden_dim, cfg.intermediate_dim, cfg.top_k
     dev = torch.device("cuda:0")
     log(f"[bench] generating {args.layers} {cfg.name} {args.weights} layers on the GPU")
