@@ -135,19 +135,6 @@
 #ifndef WR_F4_STG_RAW
 #define WR_F4_STG_RAW 39936
 #endif
-// MXFP4 gate/up as a software-pipelined stream of persistent gate/up blocks
-// (gateup_stream_xl), and its ring of register rounds per wave.
-#ifndef WR_F4_PGU
-#define WR_F4_PGU 0
-#endif
-#ifndef WR_F4_PGU_D
-#define WR_F4_PGU_D 3
-#endif
-// 1: the streaming gate/up blocks take every resident slot (the down blocks
-// are dispatched as they finish); 0: they leave a slot for every down block.
-#ifndef WR_F4_PGU_ALL
-#define WR_F4_PGU_ALL 0
-#endif
 
 namespace wr {
 
@@ -1048,143 +1035,6 @@ __device__ __forceinline__ void gateup_item_xl(const WT* __restrict__ wbuf,
   }
 }
 
-// MXFP4 gate/up as one software-pipelined stream per wave (PGU).  Gate/up
-// block b of n1b takes the slots v = b, b + n1b, ... below n1 (n1b is a
-// multiple of 8, so every slot keeps its block's XCD class and each act line
-// still has writers on one XCD only).  The block selects the experts and
-// copies x into LDS once.  Each wave then runs through its rows of all of
-// those slots as rounds of RPW rows x 2 matrices x one 64 VEC column chunk,
-// with a ring of D register buffers: round t + D is issued as soon as round t
-// has been summed, so D - 1 rounds stay in flight while one is summed.  The
-// block's loads thus keep a steady few KB per wave in flight, instead of one
-// burst per slot followed by selection, sums and stores with nothing in
-// flight.  Every load is issued (rows past nrows, chunks past h and the
-// padding rounds after the last slot read the expert's first 16 bytes, whose
-// products are dropped or meet zero x values), so the compiler's load counts
-// stay exact.  The act values wait in lanes (lane i RPW + j: row j of the
-// wave's slot i; ns RPW <= 64) and are stored once, after the last round, so
-// no store sits between a round's loads and their use.  The caller counts the
-// slots' arrivals when the block's stores have completed.
-template <typename WT, typename XT, int VEC, int RPW, int D>
-__device__ __forceinline__ void gateup_stream_xl(const WT* __restrict__ wbuf,
-                                                 const XT* __restrict__ xb, float* act,
-                                                 int64_t act_row, const Geom& g, const TopK& t,
-                                                 const Handoff& hs, int ns, int lane,
-                                                 unsigned char* xs_raw) {
-  typedef typename WVec<WT, VEC>::type V;
-  constexpr int CH = kWave * VEC;
-  constexpr int LB = 32 / (kWavesPerBlock * RPW);
-  static_assert(std::is_same<WT, fp4x2>::value && VEC == 32, "the stream is the MXFP4 path");
-  static_assert(D >= 2, "a ring of at least two rounds");
-  (void)hs;  // WR_TIMELINE builds record two marks
-  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
-  const int items = (g.I + RPW - 1) / RPW;
-  const int bpk = (items + kWavesPerBlock - 1) / kWavesPerBlock;
-  const int nc = (g.h + CH - 1) / CH;  // rounds per slot
-
-  // Slot i of this block, for this wave: selected-expert index kk and rows
-  // [r0, r0 + nrows) (nrows = 0 for an empty slot and for i >= ns).
-  auto slot = [&](int i, int& kk, int& r0, int& nrows) {
-    const int v = (int)blockIdx.x + i * hs.n1b;
-    const int G = chunk_of_block<LB>(v);
-    const bool ok = i < ns && G < hs.chunks;
-    kk = ok ? G / bpk : 0;
-    const int it = (G - kk * bpk) * kWavesPerBlock + wave;
-    nrows = (ok && it < items) ? min(RPW, g.I - it * RPW) : 0;
-    r0 = nrows > 0 ? it * RPW : 0;
-  };
-  auto issue = [&](V (&wgd)[RPW], V (&wud)[RPW], int i, int c) {
-    int kk, r0, nrows;
-    slot(i, kk, r0, nrows);
-    const WT* blk = wbuf + (int64_t)topk_id(t, kk) * g.stride;
-    const int col = c * CH + lane * VEC;
-#pragma unroll
-    for (int j = 0; j < RPW; ++j) {
-      const bool ok = col < g.h && j < nrows;
-      const int64_t r = ok ? r0 + j : 0;
-      const int cc = ok ? col : 0;
-      wgd[j] = load_wq<WT, VEC>(blk + eoff<WT>(r * g.h + cc), mx_at<WT>(mx_row(blk, g, 0, r), cc));
-      wud[j] = load_wq<WT, VEC>(blk + g.off_up + eoff<WT>(r * g.h + cc),
-                                mx_at<WT>(mx_row(blk, g, 1, r), cc));
-    }
-  };
-
-  V wg[D][RPW], wu[D][RPW];
-  int ii = 0, ic = 0;  // the next round to issue: slot ii, chunk ic
-#pragma unroll
-  for (int d = 0; d < D; ++d) {
-    issue(wg[d], wu[d], ii, ic);
-    if (++ic == nc) {
-      ic = 0;
-      ++ii;
-    }
-  }
-  xl_copy<XT, VEC>(xb, xs_raw, g.h, wave, lane);
-  __builtin_amdgcn_s_waitcnt(0);  // the copy's loads (and the first rounds) have landed
-  __syncthreads();
-  WR_TL_MARK(hs, 2);
-
-  float ag[RPW], au[RPW], actv = 0.0f;
-#pragma unroll
-  for (int j = 0; j < RPW; ++j) ag[j] = au[j] = 0.0f;
-  // Rounds [0, Tp) with Tp = ns nc rounded up to whole rings: the loop sums
-  // Tp - D of them and issues the next ring behind each; the last ring is
-  // summed after it with nothing more issued (padding rounds, at most D - 1,
-  // are issued only to fill the last ring).
-  const int Tp = (ns * nc + D - 1) / D * D;
-  int si = 0, sc = 0;  // the round being summed
-  auto sum_round = [&](const V (&wgd)[RPW], const V (&wud)[RPW]) {
-    float xv[VEC];
-    xl_read<XT, VEC>(xs_raw, sc * CH + lane * VEC, g.h, xv);
-#pragma unroll
-    for (int j = 0; j < RPW; ++j)
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        ag[j] = fmaf(wdec<WT>(wgd[j], i), xv[i], ag[j]);
-        au[j] = fmaf(wdec<WT>(wud[j], i), xv[i], au[j]);
-      }
-    if (sc == nc - 1) {  // slot si's rows are complete (wave-uniform)
-      int kk, r0, nrows;
-      slot(si, kk, r0, nrows);
-      RowScales<WT, RPW> rs;
-      load_row_scales<WT, RPW>(rs, wbuf, g, r0, nrows);  // unit scales: no loads
-      const float wk = topk_w(t, kk);
-#pragma unroll
-      for (int j = 0; j < RPW; ++j) {
-        const float v = act_value<WT, RPW>(rs, j, wk, wave_sum(ag[j]), wave_sum(au[j]));
-        actv = lane == si * RPW + j ? v : actv;
-        ag[j] = au[j] = 0.0f;
-      }
-    }
-    if (++sc == nc) {
-      sc = 0;
-      ++si;
-    }
-  };
-  for (int t0 = 0; t0 < Tp - D; t0 += D) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      sum_round(wg[d], wu[d]);
-      issue(wg[d], wu[d], ii, ic);
-      if (++ic == nc) {
-        ic = 0;
-        ++ii;
-      }
-    }
-  }
-#pragma unroll
-  for (int d = 0; d < D; ++d) sum_round(wg[d], wu[d]);
-  WR_TL_MARK(hs, 7);
-  {
-    int kk, r0, nrows;
-    const int i = lane / RPW, j = lane % RPW;
-    slot(i, kk, r0, nrows);
-    if (j < nrows)
-      __hip_atomic_store(act + kk * act_row + r0 + j, actv, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
 // Down tile of a fused down block: U column chunks q = q0 + 4 u (chunk q is
 // columns [(q mod nch) * 64 VEC, +64 VEC) of selected expert q / nch), RPD rows
 // from r0.
@@ -1307,7 +1157,7 @@ constexpr size_t fused_raw_bytes() {
 #define WR_FUSED_BOUNDS __launch_bounds__(kBlock)
 #endif
 template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2, bool XL,
-          bool STG, bool CLAIM = false, bool PGU = false>
+          bool STG, bool CLAIM = false>
 __global__ WR_FUSED_BOUNDS void k_fused_ffn(
     const WT* __restrict__ wbuf, const XT* __restrict__ x, const float* __restrict__ logits,
     float* act, XT* __restrict__ out, int32_t* __restrict__ ids_out, float* __restrict__ w_out,
@@ -1356,27 +1206,6 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
           if (w_out != nullptr) w_out[kk] = t.w[kk];
         }
       }
-    }
-    if constexpr (PGU) {
-      // Streaming variant: this block's ns slots v = b + i n1b, then one
-      // arrival per slot once the block's act stores have completed.
-      static_assert(XL && !CLAIM, "the stream reads x from the x-in-LDS copy");
-      const int ns = (hs.n1 - (int)blockIdx.x + hs.n1b - 1) / hs.n1b;
-      gateup_stream_xl<WT, XT, VEC, RPW, WR_F4_PGU_D>(wbuf, x, act, act_row, g, t, hs, ns, lane,
-                                                      lds_raw);
-      if (threadIdx.x == 0)
-        __hip_atomic_fetch_or(hs.rot + (blockIdx.x % FusedWs::kCounters) * FusedWs::kCounterStride,
-                              1u << ((xcc_id() - blockIdx.x) & 7u), __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
-      __builtin_amdgcn_s_waitcnt(0);  // this wave's act stores have completed
-      __syncthreads();
-      if ((int)threadIdx.x < ns)
-        __hip_atomic_fetch_add(
-            hs.cnt + (((int)blockIdx.x + (int)threadIdx.x * hs.n1b) % FusedWs::kCounters) *
-                         FusedWs::kCounterStride,
-            1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      WR_TL_MARK(hs, 3);
-      return;
     }
     const int items = (g.I + RPW - 1) / RPW;
     const int bpk = (items + kWavesPerBlock - 1) / kWavesPerBlock;  // chunks per expert
@@ -1695,20 +1524,17 @@ hipError_t logits_t(const Problem& p, float* logits, unsigned* zero, int nzero, 
   return hipGetLastError();
 }
 
-bool fused_pgu(const Problem& p);
-
 // Rows per gate/up wave of the single-token kernel: 4 (two column chunks in
 // flight) when those two chunks cover a whole weight row (at most 2 KB), else
 // 2 (four chunks in flight).  Either way a wave reads about 16-32 KB per
 // iteration, and a row of at most 4 chunks takes one load round per wave
 // instead of two dependent ones (DeepSeek's 4 KB rows: 31.3 -> 28.0 us).
 // fp8 rows always take 4: four chunks of 16 fp32 x values per lane would
-// cost 64 VGPRs and a wave per SIMD.  MXFP4 takes 2 in the streaming gate/up
-// (fused_pgu), else 4.
+// cost 64 VGPRs and a wave per SIMD.
 int fused_rpw(const Problem& p) {
   const int64_t row_bytes = (int64_t)p.h * weight_es(p.wdt);
   if (p.wdt == WR_FP8_E4M3) return p.vec > 1 ? WR_F8_RPW : 2;
-  if (p.wdt == WR_MXFP4) return (p.vec == 32 && !fused_pgu(p)) ? 4 : 2;
+  if (p.wdt == WR_MXFP4) return p.vec == 32 ? 4 : 2;
   return (p.vec > 1 && row_bytes <= 2048) ? 4 : 2;
 }
 
@@ -1721,27 +1547,6 @@ int fused_chunks(int I, int k, int rpw) {
 int fused_n1(int I, int k, int rpw) {
   const int group = 8 * (32 / (kWavesPerBlock * rpw));
   return (fused_chunks(I, k, rpw) + group - 1) / group * group;
-}
-
-// Gate/up blocks of the streaming MXFP4 variant for n1 slots beside n2 down
-// blocks, with cap blocks resident at once: the fewest (a multiple of 8) that
-// leave every down block a place among the resident blocks from the start,
-// with the slots spread evenly (ns = ceil(n1 / n1b) per block, and ns rpw <=
-// 64 act values per wave).  0 when the shape does not fit.
-int pgu_blocks(int n1, int n2, int cap, int rpw) {
-  const int room = (cap - n2) / 8 * 8;
-  if (room < 8) return 0;
-  const int ns = (n1 + room - 1) / room;
-  if (ns * rpw > kWave) return 0;
-  return std::min(room, ((n1 + ns - 1) / ns + 7) / 8 * 8);
-}
-
-// MXFP4 with 16-byte loads takes the streaming gate/up (2 rows per wave) when
-// the shape fits it at 4 resident blocks per CU (the kernel's occupancy).
-bool fused_pgu(const Problem& p) {
-  if (!WR_F4_PGU || p.wdt != WR_MXFP4 || p.vec != 32 || p.h > WR_XL_FP4_MAXH) return false;
-  const int n2 = (p.h + WR_F4_RPD - 1) / WR_F4_RPD;
-  return pgu_blocks(fused_n1(p.I, p.k, 2), n2, 4 * cu_count(), 2) > 0;
 }
 
 // Blocks of `kernel` resident per CU (occupancy query, cached per kernel).
@@ -1839,35 +1644,6 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
       // (k RPD I / 32 bytes), and the down rows are long enough for the copy
       // to pay (I >= WR_F4_STG_MIN_I).  Measured: Mixtral 57.5 -> 55.7 us,
       // DBRX 105.0 -> 102.0 us; DeepSeek (I = 1408) 18.7 -> 19.0 us.
-      // MXFP4 streaming gate/up (fused_pgu chose 2 rows per wave): n1b
-      // persistent gate/up blocks, and the down role as below (staged scales
-      // under the same conditions).
-      if constexpr (kFp4 && RPW == 2 && VEC == 32 && WR_F4_PGU) {
-        constexpr size_t kRaw = fused_raw_bytes<WT, XT, VEC, RPW, true, true>();
-        const bool stg = p.h % 128 == 0 && p.I % 128 == 0 && p.I >= WR_F4_STG_MIN_I &&
-                         (size_t)p.k * RPD * (p.I / 32) <= kRaw;
-        auto ks = k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, true, false, true>;
-        auto kn = k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, false, false, true>;
-        const int bpc = blocks_per_cu(stg ? reinterpret_cast<const void*>(ks)
-                                          : reinterpret_cast<const void*>(kn));
-        const int n1b = pgu_blocks(hs.n1, WR_F4_PGU_ALL ? 0 : n2, bpc * cu_count(), RPW);
-        if (n1b > 0) {
-          hs.n1b = n1b;
-          hs.nb = n1b + n2;
-          WR_TL_GRID(hs.nb);
-          if (stg)
-            hipLaunchKernelGGL(ks, dim3(hs.nb), dim3(kBlock), 0, s,
-                               static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x),
-                               w.logits, w.act, static_cast<XT*>(p.out), p.topk_ids, p.topk_w, g,
-                               hs);
-          else
-            hipLaunchKernelGGL(kn, dim3(hs.nb), dim3(kBlock), 0, s,
-                               static_cast<const WT*>(p.wbuf), static_cast<const XT*>(p.x),
-                               w.logits, w.act, static_cast<XT*>(p.out), p.topk_ids, p.topk_w, g,
-                               hs);
-          return hipGetLastError();
-        }
-      }
       if constexpr (kFp4 && RPW == 4) {
         constexpr size_t kRaw = fused_raw_bytes<WT, XT, VEC, RPW, true, true>();
         if (p.h % 128 == 0 && p.I % 128 == 0 && p.I >= WR_F4_STG_MIN_I &&
