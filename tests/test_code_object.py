@@ -210,9 +210,11 @@ def test_no_kernel_uses_scratch_memory_or_spills(kernels):
 def test_single_token_kernels_keep_four_waves_per_simd(kernels):
     # k_fused_ffn<WT, XT, VEC, ...> with 16-byte vectors: f16 / bf16 (VEC 8)
     # and MXFP4 (VEC 32).  fp8 keeps 3 waves by design (16 fp32 x values
-    # per chunk and lane on the register path).
+    # per chunk and lane on the register path), and so do the MXFP4 kernels
+    # with whole rows in flight (U1 = 2, below).
     fused = {k: v["vgpr_alloc"] for k, v in kernels.items() if re.search(
-        r"k_fused_ffnI(DF16_|NS_5bf16wE)(DF16_|f)Li8E|k_fused_ffnINS_5fp4x2E(DF16_|f)Li32E", k)}
+        r"k_fused_ffnI(DF16_|NS_5bf16wE)(DF16_|f)Li8E|k_fused_ffnINS_5fp4x2E(DF16_|f)Li32E", k)
+        and not re.search(WHOLE_ROWS, k)}
     # 3 weight types x 2 x types x 2 RPW x 2 x paths, plus the MXFP4 kernels
     # with staged block scales (x in LDS, 4 rows per wave) for the 2 x types,
     # plus the claiming register-path variants of f16 and bf16 (2 x 2 x 2)
@@ -220,6 +222,22 @@ def test_single_token_kernels_keep_four_waves_per_simd(kernels):
     assert all(n > 0 for n in fused.values()), "kernel descriptors not found"
     over = {k: n for k, n in fused.items() if n > 128}
     assert not over, f"single-token kernels allocating more than 128 VGPRs: {over}"
+
+
+# MXFP4 single-token kernels with both column chunks of a row in flight
+# (VEC 32, 4 rows per wave, U1 = 2), x in LDS with and without staged scales.
+WHOLE_ROWS = r"k_fused_ffnINS_5fp4x2E(DF16_|f)Li32ELi4ELi2E"
+
+
+def test_whole_row_mxfp4_kernels_keep_two_waves_per_simd(kernels):
+    # They run only where every gate/up block of the layer is resident at once
+    # at their own occupancy (queried at launch), which needs at least 2
+    # blocks of 4 waves per CU.
+    whole = {k: v["vgpr_alloc"] for k, v in kernels.items() if re.search(WHOLE_ROWS, k)}
+    assert len(whole) == 4, sorted(whole)
+    assert all(re.search(r"ELb1ELb[01]ELb0EEEv", k) for k in whole), "x-in-LDS variants only"
+    over = {k: n for k, n in whole.items() if n > 256}
+    assert not over, f"whole-row MXFP4 kernels allocating more than 256 VGPRs: {over}"
 
 
 def test_register_path_kernels_hold_no_per_thread_arrays_in_lds(kernels):

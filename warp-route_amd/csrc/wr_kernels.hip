@@ -1549,6 +1549,15 @@ int fused_n1(int I, int k, int rpw) {
   return (fused_chunks(I, k, rpw) + group - 1) / group * group;
 }
 
+// MXFP4 block scales staged in LDS (x-in-LDS variant): rows hold whole
+// dwords of them (h and I multiples of 128), the down role's copy fits the
+// buffer (k RPD I / 32 bytes) and the down rows are long enough for the copy
+// to pay (I >= WR_F4_STG_MIN_I).
+bool f4_stg(const Problem& p) {
+  return p.h % 128 == 0 && p.I % 128 == 0 && p.I >= WR_F4_STG_MIN_I &&
+         (size_t)p.k * WR_F4_RPD * (p.I / 32) <= (size_t)WR_F4_STG_RAW;
+}
+
 // Blocks of `kernel` resident per CU (occupancy query, cached per kernel).
 int blocks_per_cu(const void* kernel) {
   static std::mutex mu;
@@ -1639,15 +1648,14 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
   if constexpr (kXl) {
     constexpr int kBpc = kFp8 ? WR_XL_FP8_BPC : WR_XL_F16_BPC;  // MXFP4: no bound
     if (p.h <= kXlMax && (kFp4 || hs.n1 <= kBpc * cu_count())) {
-      // MXFP4: block-scale bytes staged in LDS when rows hold whole dwords of
-      // them (h and I multiples of 128), the down role's copy fits the buffer
-      // (k RPD I / 32 bytes), and the down rows are long enough for the copy
-      // to pay (I >= WR_F4_STG_MIN_I).  Measured: Mixtral 57.5 -> 55.7 us,
-      // DBRX 105.0 -> 102.0 us; DeepSeek (I = 1408) 18.7 -> 19.0 us.
+      // MXFP4: block-scale bytes staged in LDS under f4_stg's conditions.
+      // Measured: Mixtral 57.5 -> 55.7 us, DBRX 105.0 -> 102.0 us; DeepSeek
+      // (I = 1408) 18.7 -> 19.0 us.
       if constexpr (kFp4 && RPW == 4) {
-        constexpr size_t kRaw = fused_raw_bytes<WT, XT, VEC, RPW, true, true>();
-        if (p.h % 128 == 0 && p.I % 128 == 0 && p.I >= WR_F4_STG_MIN_I &&
-            (size_t)p.k * RPD * (p.I / 32) <= kRaw) {
+        static_assert(fused_raw_bytes<WT, XT, VEC, RPW, true, true>() == WR_F4_STG_RAW &&
+                          RPD == WR_F4_RPD,
+                      "f4_stg sizes the down role's scale copy with these");
+        if (f4_stg(p)) {
           hs.nb = hs.n1 + n2;
           WR_TL_GRID(hs.nb);
           hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, true, true>),
@@ -1684,13 +1692,19 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
       return hipGetLastError();
     }
   }
-  hs.nb = hs.n1 + n2;
-  WR_TL_GRID(hs.nb);
-  hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, false, false>),
-                     dim3(hs.n1 + n2), dim3(kBlock), 0, s, static_cast<const WT*>(p.wbuf),
-                     static_cast<const XT*>(p.x), w.logits, w.act, static_cast<XT*>(p.out),
-                     p.topk_ids, p.topk_w, g, hs);
-  return hipGetLastError();
+  if constexpr (kFp4 && U1 == 2) {
+    // Whole MXFP4 rows in flight are chosen (f4_whole_rows) only for shapes
+    // whose x the LDS copy holds, which returned above.
+    return hipErrorInvalidValue;
+  } else {
+    hs.nb = hs.n1 + n2;
+    WR_TL_GRID(hs.nb);
+    hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, false, false>),
+                       dim3(hs.n1 + n2), dim3(kBlock), 0, s, static_cast<const WT*>(p.wbuf),
+                       static_cast<const XT*>(p.x), w.logits, w.act, static_cast<XT*>(p.out),
+                       p.topk_ids, p.topk_w, g, hs);
+    return hipGetLastError();
+  }
 }
 
 // Column chunks in flight per gate/up row: fp8 WR_F8_U1, MXFP4 one (32 x
@@ -1702,9 +1716,39 @@ constexpr int fused_u1() {
   return RPW == 4 ? WR_GU_U / 2 : WR_GU_U;
 }
 
+// MXFP4 rows of two column chunks (2048 < h <= 4096) take both chunks of a
+// row in one load round (U1 = 2) when every gate/up block of the layer is
+// resident at once at that variant's occupancy (168-208 VGPRs: 2 or 3 blocks
+// per CU): each block then ends after one round trip instead of two.  With a
+// second round of blocks the lower occupancy costs more than it saves.
+// Measured (fp32 x): Mixtral tp4 / tp8 shards 22.4 / 17.6 -> 21.1 / 17.4 us;
+// full Mixtral 54.6 -> 57.4, tp2 shard 33.5 -> 33.7, DBRX 102.6 -> 122.0,
+// DeepSeek 19.2 -> 23.7 us with U1 = 2 throughout.
+template <typename WT, typename XT, int VEC>
+bool f4_whole_rows(const Problem& p) {
+  if constexpr (std::is_same<WT, fp4x2>::value && VEC == 32) {
+    if (p.h <= kWave * VEC || p.h > 2 * kWave * VEC || p.h > WR_XL_FP4_MAXH) return false;
+    constexpr int RPD = WR_F4_RPD, U2 = WR_F4_U2;
+    const void* k = f4_stg(p)
+                        ? reinterpret_cast<const void*>(
+                              k_fused_ffn<WT, XT, VEC, 4, 2, RPD, U2, true, true>)
+                        : reinterpret_cast<const void*>(
+                              k_fused_ffn<WT, XT, VEC, 4, 2, RPD, U2, true, false>);
+    return fused_n1(p.I, p.k, 4) <= blocks_per_cu(k) * cu_count();
+  } else {
+    (void)p;
+    return false;
+  }
+}
+
 template <typename WT, typename XT, int VEC>
 hipError_t fused_t(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
-  if (fused_rpw(p) == 4) return fused_rpw_t<WT, XT, VEC, 4, fused_u1<WT, 4>()>(p, w, fold, s);
+  if (fused_rpw(p) == 4) {
+    if constexpr (std::is_same<WT, fp4x2>::value && VEC == 32) {
+      if (f4_whole_rows<WT, XT, VEC>(p)) return fused_rpw_t<WT, XT, VEC, 4, 2>(p, w, fold, s);
+    }
+    return fused_rpw_t<WT, XT, VEC, 4, fused_u1<WT, 4>()>(p, w, fold, s);
+  }
   return fused_rpw_t<WT, XT, VEC, 2, fused_u1<WT, 2>()>(p, w, fold, s);
 }
 
