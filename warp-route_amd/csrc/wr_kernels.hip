@@ -135,6 +135,11 @@
 #ifndef WR_F4_STG_RAW
 #define WR_F4_STG_RAW 39936
 #endif
+// MXFP4 x-in-LDS kernels without staged scales: their down blocks also stage
+// one more weight chunk per wave in the x copy's bytes before the hand-off.
+#ifndef WR_F4_XL_DN_STAGE
+#define WR_F4_XL_DN_STAGE 1
+#endif
 
 namespace wr {
 
@@ -1319,14 +1324,21 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
       }
     }
   }
-  // STG: the down role does not use the x copy's bytes of lds_raw, so after
-  // the scale copy they hold one more 8-row chunk for each wave there is room
-  // for (spre = 1): chunk wave + 4 U2, codes only, staged the same way.
+  // MXFP4 x-in-LDS variants: the down role does not use the x copy's bytes
+  // of lds_raw, so (after the STG scale copy) they hold one more 8-row chunk
+  // for each wave there is room for (spre = 1): chunk wave + 4 U2, codes
+  // only, staged the same way.  Without STG the chunk's block-scale bytes go
+  // to registers (sscale), loaded with it.
+  constexpr bool kStage =
+      STG || (XL && std::is_same<WT, fp4x2>::value && VEC == 32 && WR_F4_XL_DN_STAGE);
   int spre = 0;
   const unsigned char* sp = lds_raw;
-  if constexpr (STG) {
+  uint32_t sscale[RPD];
+#pragma unroll
+  for (int j = 0; j < RPD; ++j) sscale[j] = 127u;
+  if constexpr (kStage) {
     constexpr int kChunk = RPD * kWave * 16;
-    const int sbytes = (g.k * RPD * (g.I / 32) + 255) & ~255;
+    const int sbytes = STG ? (g.k * RPD * (g.I / 32) + 255) & ~255 : 0;
     const int npre = ((int)sizeof(lds_raw) - sbytes) / kChunk;
     const int q = wu + kWavesPerBlock * U2;
     if (wu < npre && q < C) {  // wave-uniform
@@ -1334,16 +1346,18 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
       sp = lds_raw + sbytes + wu * kChunk;
       const int kk = q / nch;
       const int c = (q - kk * nch) * kWave * VEC + lane * VEC;
-      const WT* D = wbuf + (int64_t)topk_id(t, kk) * g.stride + g.off_down +
-                    eoff<WT>((int64_t)r0 * g.I + c);
+      const WT* blk = wbuf + (int64_t)topk_id(t, kk) * g.stride;
+      const WT* D = blk + g.off_down + eoff<WT>((int64_t)r0 * g.I + c);
 #pragma unroll
       for (int j = 0; j < RPD; ++j) {
-        if (j < nrows && c < g.I)
+        if (j < nrows && c < g.I) {
           __builtin_amdgcn_global_load_lds(
               static_cast<const void*>(D + eoff<WT>((int64_t)j * g.I)),
               (__attribute__((address_space(3))) void*)(lds_raw + sbytes + wu * kChunk +
                                                         j * kWave * 16),
               16, 0, 0);
+          if constexpr (!STG) sscale[j] = *mx_at<WT>(mx_row(blk, g, 2, r0 + j), c);
+        }
       }
     }
   }
@@ -1389,7 +1403,7 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
     else
       invalidate_l1();
   }
-  if constexpr (STG) __builtin_amdgcn_s_waitcnt(0);  // this wave's scale copies have landed
+  if constexpr (kStage) __builtin_amdgcn_s_waitcnt(0);  // this wave's staged bytes have landed
   __syncthreads();
   WR_TL_MARK(hs, 3);
 
@@ -1418,7 +1432,7 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
       }
     }
   }
-  if constexpr (STG) {
+  if constexpr (kStage) {
     // The staged chunk landed before the barrier after the wait (the wave
     // waited for all of its loads there).
     if (spre) {
@@ -1429,9 +1443,10 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
 #pragma unroll
       for (int j = 0; j < RPD; ++j)
         lw[0][j] = (j < nrows && c < g.I)
-                       ? V{*reinterpret_cast<const u32x4*>(sp + j * kWave * 16 + lane * 16), 127u}
+                       ? V{*reinterpret_cast<const u32x4*>(sp + j * kWave * 16 + lane * 16),
+                           sscale[j]}
                        : vzero<V>();
-      down_tile_scales<WT, VEC, RPD, 1>(lw, lds_raw, g, nrows, q, nch, lane);
+      if constexpr (STG) down_tile_scales<WT, VEC, RPD, 1>(lw, lds_raw, g, nrows, q, nch, lane);
       down_tile_fma<WT, V, VEC, RPD, 1>(acc, lw, act, g, act_row, q, nch, lane, sdn);
     }
   }
