@@ -142,12 +142,12 @@ def test_layout_rejects_bad_arguments():
 
 def test_workspace_bytes():
     lib = capi.lib()
-    # fused: control block (64 arrival counters, a timeout flag, an unused
-    # word, 64 XCD-rotation masks and 8 gate/up claim counters, one 256-byte
-    # line each) + 64 fp32 logits per token (E padded to 64) + act: single
+    # fused: control block (64 arrival words, a timeout flag, an unused word
+    # and 8 gate/up claim counters, one 256-byte line each) + 64 fp32 logits
+    # per token (E padded to 64) + act: single
     # token k rows of I rounded up to 16 columns, B > 1 B*k*I; fp32, rounded up
     # to 256 bytes.
-    ctrl = 138 * 256
+    ctrl = 74 * 256
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 4096, 14336, 2, 1) == (
         ctrl + 256 + 2 * 14336 * 4)
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 64, 100, 3, 1) == (
@@ -275,8 +275,8 @@ def test_noalloc_validates_before_hip():
 def test_fused_status_checks_its_workspace_before_hip():
     lib = capi.lib()
     assert lib.wr_fused_moe_status(None, 1 << 20, None) == capi.WR_EINVAL_NULL
-    # smaller than the control block (138 lines of 256 bytes)
-    assert lib.wr_fused_moe_status(FAKE, 138 * 256 - 1, None) == capi.WR_EINVAL_WORKSPACE
+    # smaller than the control block (74 lines of 256 bytes)
+    assert lib.wr_fused_moe_status(FAKE, 74 * 256 - 1, None) == capi.WR_EINVAL_WORKSPACE
     assert "NaN" in capi.status_str(capi.WR_ETIMEOUT)
 
 

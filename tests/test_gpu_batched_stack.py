@@ -359,9 +359,8 @@ def test_fused_handoff_expiry_is_reported(cuda, shape):
 
 
 # Byte offset of the single-token workspace's 8 claim counters (one 256-byte
-# line each): after 64 arrival counters, the timeout word, one unused word
-# and 64 rotation masks.
-CLAIM_OFFSET = (2 * 64 + 2) * 256
+# line each): after 64 arrival words, the timeout word and one unused word.
+CLAIM_OFFSET = (64 + 2) * 256
 
 
 @pytest.mark.parametrize("shape,gu", [((8, 512, 8192, 2, F16), 64), ((8, 512, 8192, 2, F16), 992),

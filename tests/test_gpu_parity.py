@@ -514,18 +514,17 @@ def _fused_args(x, gw, buf, E, h, I, k, out, work, renorm=0):
                          ids=["small", "mixtral", "deepseek", "ragged", "mixtral-fp8",
                               "dbrx-fp8", "mixtral-mxfp4", "dbrx-mxfp4"])
 def test_fused_handoff_never_times_out(cuda, shape):
-    """Single-token fused kernel: every gate/up block incremented its arrival
-    counter (64 counters, 256 bytes apart) and no down block's bounded wait
-    expired (timeout word after the counters).  Gate/up blocks = act chunks
-    k * ceil(ceil(I / rpw) / 4), rounded up to a multiple of 8 * 32 / (4 rpw),
-    with rpw = 4 rows per wave for fp16 rows of at most 2 KB (h <= 1024, 16-byte
-    vectors) and for all 16-byte-vector fp8 rows, else 2.  The workspace starts as junk: the router kernel must
-    zero the control block on every call.  The 64 rotation masks (after the
-    timeout word and one unused word) each hold one bit per XCD rotation
-    (XCD - block) mod 8 that gate/up blocks b with b mod 64 equal to the
-    mask's index ran with; masks of indices with no blocks stay zero.  Any set
-    of bits gives correct results (more than one rotation switches the down
-    blocks to a full acquire)."""
+    """Single-token fused kernel: every gate/up block added its arrival to
+    its arrival word (64 words of 64 bits, 256 bytes apart) and no down
+    block's bounded wait expired (timeout word after them).  Gate/up blocks =
+    act chunks k * ceil(ceil(I / rpw) / 4), rounded up to a multiple of
+    8 * 32 / (4 rpw), with rpw = 4 rows per wave for fp16 rows of at most 2 KB
+    (h <= 1024, 16-byte vectors) and for all 16-byte-vector fp8 rows, else 2.
+    The workspace starts as junk: the router kernel must zero the control
+    block on every call.  Word c holds {arrivals of the blocks b with b mod 64
+    = c in bits 0-15, the sum of their XCD rotations r = (XCD - b) mod 8 in
+    bits 16-31, the sum of r^2 in bits 32-63}.  Any rotations give correct
+    results (more than one switches the down blocks to a full acquire)."""
     E, h, I, k, wd = shape
     x, gw, buf = make_layer(E, h, I, wd, router_std=h ** -0.5, seed=2, device=cuda,
                             gen_device=cuda)
@@ -544,17 +543,19 @@ def test_fused_handoff_never_times_out(cuda, shape):
     for _ in range(3):
         assert capi.call("wr_fused_moe", a, torch.cuda.current_stream().cuda_stream) == 0
         torch.cuda.synchronize()
-        words = work[:130 * 256].view(torch.int32).cpu()
-        counters = words[0:64 * 64:64]
-        assert int(words[64 * 64]) == 0, "a down block's wait expired"
-        rot = words[66 * 64:130 * 64:64].tolist()
-        for c, m in enumerate(rot):
-            assert 0 <= m < 256 and (m != 0) == (c < n1), (c, m)
-        assert counters.tolist() == [(n1 - c + 63) // 64 for c in range(64)]
-    seen = 0
-    for m in rot:
-        seen |= m
-    print(f"[gpu] handoff {shape}: gate/up blocks {n1}, rotations {bin(seen)}")
+        ctrl = work[:66 * 256].cpu()
+        assert int(ctrl[64 * 256:64 * 256 + 4].view(torch.int32)[0]) == 0, \
+            "a down block's wait expired"
+        arr = [int(v) for v in ctrl[:64 * 256].view(torch.int64)[0::32]]
+        counts = [a & 0xFFFF for a in arr]
+        assert counts == [(n1 - c + 63) // 64 for c in range(64)]
+        rots = set()
+        for n, word in zip(counts, arr):
+            sr, sq = (word >> 16) & 0xFFFF, word >> 32
+            assert sr <= 7 * n and sq <= 49 * n and sr * sr <= n * sq, (n, sr, sq)
+            if n and sr * sr == n * sq:
+                rots.add(sr // n)  # one rotation among this word's arrivals
+    print(f"[gpu] handoff {shape}: gate/up blocks {n1}, rotations {sorted(rots)}")
     ref = oracle_token(x, gw, buf, E, h, I, k, False)
     np.testing.assert_allclose(f64(out), ref["out"], rtol=1e-2, atol=1e-2)
     del buf

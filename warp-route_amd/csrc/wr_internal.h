@@ -59,20 +59,20 @@ constexpr size_t kWsAlign = 256;
 
 // Workspace carving.  Every region starts on a 256-byte boundary.
 struct FusedWs {
-  // Single-token hand-off, one 256-byte line per word: kCounters arrival
-  // counters, the wait-timeout flag, an unused word, kCounters XCD-rotation
-  // masks (gate/up block b ORs bit (its XCD - b) mod 8 into mask
-  // b mod kCounters), then kClasses claim counters of the gate/up chunks
+  // Single-token hand-off, one 256-byte line per word: kCounters 64-bit
+  // arrival words (each gate/up slot adds its arrival and its XCD rotation,
+  // (its XCD - block) mod 8, to word slot mod kCounters), the wait-timeout
+  // flag, an unused word, then kClasses claim counters of the gate/up chunks
   // beyond the launched blocks (class b mod 8).  The router launch of each
-  // single-token call zeroes them (with WR_ROUTER_IN_FFN, block 0 of the
-  // call's kernel, before it publishes its router slot).
+  // single-token call zeroes the first 8 bytes of each line (with
+  // WR_ROUTER_IN_FFN, block 0 of the call's kernel, before it publishes its
+  // router slot).
   static constexpr int kCounters = 64;
   static constexpr int kClasses = 8;
   static constexpr int kCounterStride = 64;  // words (256 bytes)
   static constexpr int kTimeoutWord = kCounters * kCounterStride;
-  static constexpr int kRotWord = kTimeoutWord + 2 * kCounterStride;
-  static constexpr int kClaimWord = kRotWord + kCounters * kCounterStride;
-  static constexpr int kCtrlWords = 2 * kCounters + 2 + kClasses;  // zeroed words, kCounterStride apart
+  static constexpr int kClaimWord = kTimeoutWord + 2 * kCounterStride;
+  static constexpr int kCtrlWords = kCounters + 2 + kClasses;  // zeroed lines, kCounterStride apart
   // WR_ROUTER_IN_FFN: router slots after the zeroed words, 16 bytes per
   // expert: two 64-bit words {logit bits, tag half} carrying the tag of the
   // call that wrote them (never zeroed: a slot counts only when it carries

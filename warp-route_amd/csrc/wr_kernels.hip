@@ -213,9 +213,9 @@ struct XSplit {
 
 // grid (E, B), block 256.  Token b's logits go to logits[b * 64 + e] (padded
 // so that consumers can read all 64 with scalar loads).  Block (0, 0) also
-// zeroes the words zero[i * zstride], i < nzero <= kBlock (the single-token
-// kernel's arrival counters, timeout flag, rotation masks and claim
-// counters), which the next kernel on the stream reads.  With xs.hi != NULL,
+// zeroes the 8-byte words at zero + i * zstride, i < nzero <= kBlock (the
+// single-token kernel's arrival words, timeout flag and claim counters),
+// which the next kernel on the stream reads.  With xs.hi != NULL,
 // block (e, b) also writes its 1/E
 // share of token b's split x (XSplit); every block of the token derives the
 // same exponent from the whole row.
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(kBlock) void k_router_logits(const float* __restric
     pmax[q] = m;
   }
   if (zero != nullptr && e == 0 && b == 0 && (int)threadIdx.x < nzero)
-    zero[(int64_t)threadIdx.x * zstride] = 0u;
+    *reinterpret_cast<uint64_t*>(zero + (int64_t)threadIdx.x * zstride) = 0ull;
   __syncthreads();
   if (threadIdx.x == 0) logits[(int64_t)b * WR_MAX_EXPERTS + e] = router_combine(part);
   if (xs.hi != nullptr) {
@@ -559,11 +559,11 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 // computes rows COLS j + RPW w .. + RPW of expert kk's gate and up matrices and
 // stores w_kk * silu(gate . x) * (up . x) with agent-scope stores, which are
 // written through to memory.  When all of them have completed, the block
-// increments arrival counter b mod 64 (the counters sit 256 bytes apart so
+// adds its arrival to arrival word b mod 64 (the words sit 256 bytes apart so
 // that their atomics do not serialise on one address).
 //
 // Down block: owns RPD output rows.  It issues the loads of its first tile of
-// down weights (they do not depend on act), then wave 0 polls the 64 counters
+// down weights (they do not depend on act), then wave 0 polls the 64 words
 // until all n1 gate/up blocks have arrived, then the 4 waves stream strided
 // column chunks of every selected down matrix and combine in LDS.  Every
 // output row is written once.
@@ -588,26 +588,27 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 // acquire invalidates them), and no wave reads act before every gate/up block
 // has arrived.  Hence an XCD's L2 holds an act line only if its own writers
 // put it there (all of the line's writers go through that L2) or if a reader
-// fetched it from memory after it was complete.  Each gate/up block records
-// the rotation it actually ran with, (HW_REG_XCC_ID - b) mod 8, as a bit in
-// one of 64 masks; a down block ORs the 64 masks and, unless exactly one bit
-// is set (one rotation for the whole grid), falls back to a full agent-scope
-// acquire (L2 and L1 invalidate).  Otherwise it only invalidates its CU's L1,
+// fetched it from memory after it was complete.  Each gate/up block adds
+// the rotation it actually ran with, r = (HW_REG_XCC_ID - b) mod 8, and r^2
+// to its arrival word (arrival_word); a down block sums the 64 words it
+// waited on and, unless (sum r)^2 = n sum r^2 (one rotation for the whole
+// grid), falls back to a full agent-scope acquire (L2 and L1 invalidate).
+// Otherwise it only invalidates its CU's L1,
 // in case a writer on the same CU left a partial line there.  This saves the L2
 // invalidate per down block (about 6 us per layer at the Mixtral shape) and
 // keeps act dense, so the readers' loads stay fully coalesced.
 // ---------------------------------------------------------------------------
 struct Handoff {
-  unsigned* ctrl;       // the control block: FusedWs::kCtrlWords words zeroed at the start of
-                        // each call, FusedWs::kCounterStride words apart
+  unsigned* ctrl;       // the control block: FusedWs::kCtrlWords 8-byte words zeroed at the
+                        // start of each call, FusedWs::kCounterStride words apart
   uint64_t* slot;       // WR_ROUTER_IN_FFN: router slots, 2 words per expert (FusedWs::kSlotWord)
   const float* gate_w;  // router matrix [E][h]; nullptr: the logits are read from `logits`
   int nb;               // blocks in the grid
   int rvec;             // router rows and x in 128-bit loads (else scalar)
-  unsigned* cnt;        // FusedWs::kCounters counters, FusedWs::kCounterStride words apart
+  unsigned* cnt;        // FusedWs::kCounters 64-bit arrival words, FusedWs::kCounterStride
+                        // words apart (arrival_word)
   unsigned* timeout;    // set to 1 if a wait expired (that block's rows are then NaN)
   unsigned* host_flag;  // host-visible word also set to 1 then, or nullptr
-  unsigned* rot;        // FusedWs::kCounters rotation masks, FusedWs::kCounterStride words apart
   unsigned* claim;      // FusedWs::kClasses claim counters, FusedWs::kCounterStride words apart
   int n1;               // gate/up chunk slots, a multiple of 8 LB: one arrival each
   int n1b;              // gate/up blocks launched (the first n1b block ids), a multiple of
@@ -619,6 +620,23 @@ struct Handoff {
   uint64_t* tl;         // per-block records (include/wr_timeline.h)
 #endif
 };
+
+// Arrival word of counter (slot mod 64): 64 bits, {arrivals in bits 0-15, the
+// sum of their XCD rotations r = (HW_REG_XCC_ID - block) mod 8 in bits 16-31,
+// the sum of r^2 in bits 32-63}, so that one atomic add per gate/up slot
+// counts it and records its rotation, and one load per lane gives a down
+// block both.  The fields hold ceil(n1 / 64) <= kMaxArrivals arrivals per
+// counter without carrying into the next one.
+constexpr int kMaxArrivals = 9362;  // 7 kMaxArrivals < 2^16
+__device__ __forceinline__ uint64_t* arrival_word(const Handoff& hs, int slot) {
+  return reinterpret_cast<uint64_t*>(hs.cnt + (slot % FusedWs::kCounters) *
+                                                  FusedWs::kCounterStride);
+}
+__device__ __forceinline__ uint64_t arrival_bits() {
+  const uint64_t r = (xcc_id() - blockIdx.x) & 7u;
+  return 1ull | (r << 16) | ((r * r) << 32);
+}
+__device__ __forceinline__ unsigned arrivals(uint64_t w) { return (unsigned)(w & 0xffffu); }
 
 // A hand-off wait expired: the workspace's timeout word (read by
 // wr_fused_moe_status) and the host-visible word (read by
@@ -660,8 +678,8 @@ __device__ __forceinline__ void set_expired(const Handoff& hs) {
 // router launch), and publishes row e as slot e: the 64-bit words
 // {logit, tag lo} and {logit, tag hi}, where the tag is this launch's
 // (launch_tag), in each of FusedWs::kSlotReplicas copies.  Block 0 first
-// zeroes the control words of the hand-off (arrival counters, timeout word,
-// rotation masks, claim counters) and waits for those stores to complete.
+// zeroes the control words of the hand-off (arrival words, timeout word,
+// claim counters) and waits for those stores to complete.
 // Wave 0 of every block then polls the E slots of its copy until each
 // carries this launch's tag in both words, and every wave selects from the
 // logits read (wave_select_topk_reg).
@@ -692,8 +710,9 @@ __device__ __forceinline__ bool route_and_select(const XT* __restrict__ x,
   // Block 0's zero stores go out before its router loads, so that the wait
   // for the loads covers them too.
   if (blockIdx.x == 0 && (int)threadIdx.x < FusedWs::kCtrlWords)
-    __hip_atomic_store(hs.ctrl + threadIdx.x * FusedWs::kCounterStride, 0u, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(
+        reinterpret_cast<uint64_t*>(hs.ctrl + threadIdx.x * FusedWs::kCounterStride), 0ull,
+        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (int e = blockIdx.x; e < g.E; e += hs.nb) {  // block-uniform
     if (hs.gate_w != nullptr) {
       float unused;
@@ -1241,15 +1260,11 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
           gateup_item<WT, XT, VEC, RPW, U1>(wbuf, x, act + kk * act_row + it * RPW, g, t, kk,
                                             it * RPW, lane, &hs);
       }
-      if (threadIdx.x == 0 && v == (int)blockIdx.x)
-        __hip_atomic_fetch_or(hs.rot + (blockIdx.x % FusedWs::kCounters) * FusedWs::kCounterStride,
-                              1u << ((xcc_id() - blockIdx.x) & 7u), __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
       __builtin_amdgcn_s_waitcnt(0);  // this wave's act stores have completed
       __syncthreads();
       if (threadIdx.x == 0) {
-        __hip_atomic_fetch_add(hs.cnt + (v % FusedWs::kCounters) * FusedWs::kCounterStride, 1u,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(arrival_word(hs, v), arrival_bits(), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         if constexpr (CLAIM)
           s_claim = hs.n1b + cls +
                     FusedWs::kClasses *
@@ -1377,11 +1392,13 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
     const unsigned target =
         (c < hs.n1 ? (unsigned)((hs.n1 - c + FusedWs::kCounters - 1) / FusedWs::kCounters)
                    : 0u) + hs.wait_extra;
-    const unsigned* ctr = hs.cnt + c * FusedWs::kCounterStride;
+    const uint64_t* ctr = arrival_word(hs, c);
     unsigned spins = 0;
     int gave_up = 0;
-    while (__ballot(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-                    target) != 0) {
+    uint64_t w;
+    for (;;) {
+      w = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__ballot(arrivals(w) < target) == 0) break;
       if (++spins > hs.spin_limit) {
         gave_up = 1;
         if (lane == 0) set_expired(hs);
@@ -1390,15 +1407,12 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
       __builtin_amdgcn_s_sleep(8);
     }
     if (lane == 0) expired = gave_up;
-    // One rotation for every gate/up block <=> exactly one bit in the OR of
-    // the masks.
-    const unsigned m = __hip_atomic_load(hs.rot + c * FusedWs::kCounterStride, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-    unsigned all = 0;
-#pragma unroll
-    for (int bit = 0; bit < 8; ++bit)
-      if (__ballot((m >> bit) & 1u) != 0) all |= 1u << bit;
-    if (__popc(all) != 1)
+    // One rotation r for every arrival <=> (sum r)^2 = n sum r^2 over all n
+    // of them (Cauchy-Schwarz); the sums are small integers, exact in fp32.
+    const float n = wave_sum((float)arrivals(w));
+    const float sr = wave_sum((float)(unsigned)((w >> 16) & 0xffffu));
+    const float sq = wave_sum((float)(unsigned)(w >> 32));
+    if ((double)sr * sr != (double)n * sq)
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     else
       invalidate_l1();
@@ -1641,9 +1655,9 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
   hs.cnt = w.ctrl;
   hs.timeout = w.ctrl + FusedWs::kTimeoutWord;
   hs.host_flag = p.expired_host;
-  hs.rot = w.ctrl + FusedWs::kRotWord;
   hs.claim = w.ctrl + FusedWs::kClaimWord;
   hs.n1 = fused_n1(p.I, p.k, RPW);
+  if (hs.n1 > FusedWs::kCounters * kMaxArrivals) return hipErrorInvalidValue;
   hs.n1b = hs.n1;
   hs.chunks = fused_chunks(p.I, p.k, RPW);
   hs.spin_limit = p.spin_limit;
