@@ -135,6 +135,11 @@
 #ifndef WR_F4_STG_RAW
 #define WR_F4_STG_RAW 39936
 #endif
+// 1: down blocks poll the last gate/up slot's arrival word alone until it is
+// complete, then all 64 words; 0: all 64 words from the start.
+#ifndef WR_POLL_ONE
+#define WR_POLL_ONE 1
+#endif
 // MXFP4 x-in-LDS kernels without staged scales: their down blocks also stage
 // one more weight chunk per wave in the x copy's bytes before the hand-off.
 #ifndef WR_F4_XL_DN_STAGE
@@ -563,8 +568,9 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 // that their atomics do not serialise on one address).
 //
 // Down block: owns RPD output rows.  It issues the loads of its first tile of
-// down weights (they do not depend on act), then wave 0 polls the 64 words
-// until all n1 gate/up blocks have arrived, then the 4 waves stream strided
+// down weights (they do not depend on act), then wave 0 polls the last
+// slot's arrival word (lane 0 alone) and then the 64 words until all n1
+// gate/up blocks have arrived, then the 4 waves stream strided
 // column chunks of every selected down matrix and combine in LDS.  Every
 // output row is written once.
 //
@@ -1396,6 +1402,27 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
     unsigned spins = 0;
     int gave_up = 0;
     uint64_t w;
+#if WR_POLL_ONE
+    {
+      // Until the word of the last gate/up slot (dispatched last, or claimed
+      // last) is complete, poll that word alone: one request per poll
+      // instead of 64 from every waiting down block, which the memory side
+      // otherwise serves beside the weight stream.  Any order of completion
+      // stays correct: the loop below then checks all 64.
+      const int cl = (hs.n1 - 1) % FusedWs::kCounters;
+      const unsigned tl =
+          (unsigned)((hs.n1 - cl + FusedWs::kCounters - 1) / FusedWs::kCounters) + hs.wait_extra;
+      const uint64_t* last = arrival_word(hs, cl);
+      for (;;) {
+        unsigned a = 0;
+        if (lane == 0)
+          a = arrivals(__hip_atomic_load(last, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if (__builtin_amdgcn_readfirstlane(a) >= tl) break;
+        if (++spins > hs.spin_limit) break;  // the loop below then expires at once
+        __builtin_amdgcn_s_sleep(8);
+      }
+    }
+#endif
     for (;;) {
       w = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (__ballot(arrivals(w) < target) == 0) break;
