@@ -218,8 +218,10 @@ WR_API size_t wr_workspace_bytes(int kind, int num_experts, int hidden_dim,
  * (src/gate.cu:103-116, declared at src/gate.cuh:21-27). */
 WR_API int wr_gate_topk(const wr_moe_args *args, void *stream);
 
-/* Single-token fused MoE (batch_size must be 1): a router launch, then one
- * kernel for the selection and the whole expert FFN.  The workspace needs no
+/* Single-token fused MoE (batch_size must be 1): one kernel for the
+ * selection and the whole expert FFN, which also computes the router rows
+ * for layers of at least 2 gate/up block slots per CU on its register path
+ * (one launch per layer), else a router launch ahead of it.  The workspace needs no
  * initialisation (each call resets the control words it uses) and may be
  * reused by later calls on the same stream.  Replaces fused_moe_forward
  * (src/fused_moe.cu:233-263, declared at src/fused_moe.cuh:29-32). */

@@ -143,11 +143,12 @@ def test_layout_rejects_bad_arguments():
 def test_workspace_bytes():
     lib = capi.lib()
     # fused: control block (64 arrival words, a timeout flag, an unused word
-    # and 8 gate/up claim counters, one 256-byte line each) + 64 fp32 logits
-    # per token (E padded to 64) + act: single
+    # and 8 gate/up claim counters, one 256-byte line each, then 16 copies of
+    # the router slots of a kernel with the router inside, 1152 bytes each)
+    # + 64 fp32 logits per token (E padded to 64) + act: single
     # token k rows of I rounded up to 16 columns, B > 1 B*k*I; fp32, rounded up
     # to 256 bytes.
-    ctrl = 74 * 256
+    ctrl = 74 * 256 + 16 * 1152
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 4096, 14336, 2, 1) == (
         ctrl + 256 + 2 * 14336 * 4)
     assert lib.wr_workspace_bytes(capi.WR_KIND_FUSED, 8, 64, 100, 3, 1) == (

@@ -14,8 +14,9 @@ travels with the source tree.  Run ``python warp-route_amd/build.py``.
 
 WR_HIPCC_FLAGS in the environment adds hipcc options to every HIP compile:
 the kernels' tuning macros (#ifndef WR_... in csrc/) are set that way, e.g.
-``WR_HIPCC_FLAGS=-DWR_ROUTER_IN_FFN=1 python warp-route_amd/build.py`` builds
-the single-token kernel with its router inside.  Tests assume the defaults.
+``WR_HIPCC_FLAGS=-DWR_POLL_ONE=0 python warp-route_amd/build.py`` builds the
+single-token kernel's down blocks polling all 64 arrival words from the start.
+Tests assume the defaults.
 """
 from __future__ import annotations
 

@@ -9,17 +9,6 @@
 
 #include "warp_route.h"
 
-// 1: the single-token kernel computes the router rows itself and publishes
-// them to its other blocks (wr_kernels.hip, route_and_select): one launch per
-// layer.  0 (the default): a router launch ahead of it, whose first block
-// also zeroes the hand-off's control words.  Measured on one box (layer us,
-// fp16 unless noted): DeepSeek 26.5 -> 27.3, DeepSeek MXFP4 19.1 -> 21.2, a
-// Mixtral tp8 shard 29.9 -> 30.9, Mixtral 115.7 -> 115.6: the in-kernel
-// publish and poll cost about what the kernel boundary does.
-#ifndef WR_ROUTER_IN_FFN
-#define WR_ROUTER_IN_FFN 0
-#endif
-
 namespace wr {
 
 struct Problem {
@@ -64,16 +53,16 @@ struct FusedWs {
   // (its XCD - block) mod 8, to word slot mod kCounters), the wait-timeout
   // flag, an unused word, then kClasses claim counters of the gate/up chunks
   // beyond the launched blocks (class b mod 8).  The router launch of each
-  // single-token call zeroes the first 8 bytes of each line (with
-  // WR_ROUTER_IN_FFN, block 0 of the call's kernel, before it publishes its
-  // router slot).
+  // single-token call zeroes the first 8 bytes of each line (when the router
+  // runs inside the single-token kernel, that kernel's block 0 does, before
+  // it publishes its router slot).
   static constexpr int kCounters = 64;
   static constexpr int kClasses = 8;
   static constexpr int kCounterStride = 64;  // words (256 bytes)
   static constexpr int kTimeoutWord = kCounters * kCounterStride;
   static constexpr int kClaimWord = kTimeoutWord + 2 * kCounterStride;
   static constexpr int kCtrlWords = kCounters + 2 + kClasses;  // zeroed lines, kCounterStride apart
-  // WR_ROUTER_IN_FFN: router slots after the zeroed words, 16 bytes per
+  // Router slots (a kernel with the router inside) after the zeroed words, 16 bytes per
   // expert: two 64-bit words {logit bits, tag half} carrying the tag of the
   // call that wrote them (never zeroed: a slot counts only when it carries
   // the reader's own call tag).  kSlotReplicas copies, kReplicaBytes apart (9
@@ -84,8 +73,7 @@ struct FusedWs {
   static constexpr int kSlotReplicas = 16;
   static constexpr int kReplicaBytes = 1152;
   static_assert(WR_MAX_EXPERTS * kSlotBytes <= kReplicaBytes, "a copy holds every slot");
-  static constexpr size_t kCtrlBytes =
-      (size_t)kSlotWord * 4 + (WR_ROUTER_IN_FFN ? (size_t)kSlotReplicas * kReplicaBytes : 0);
+  static constexpr size_t kCtrlBytes = (size_t)kSlotWord * 4 + (size_t)kSlotReplicas * kReplicaBytes;
   // Single-token act rows: I rounded up to whole chunks of `cols` columns, the
   // columns one gate/up block computes (4 waves x rows per wave: 8 or 16).
   static constexpr int kMaxActCols = 16;

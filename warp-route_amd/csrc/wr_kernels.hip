@@ -4,8 +4,8 @@
 // token) computes the router dot product (src/fused_moe.cu:100-112); each
 // wave covers a quarter of the row, so one memory round trip covers it.
 // Every consumer then derives the top-K selection from the logits itself
-// (wave_select_topk: DPP max/sum and a 64-bit ballot).  Built with
-// WR_ROUTER_IN_FFN=1, the single-token kernel computes the router rows itself
+// (wave_select_topk: DPP max/sum and a 64-bit ballot).  For layers of many
+// gate/up blocks the single-token kernel computes the router rows itself
 // instead (route_and_select), one launch per layer as in the reference.
 //
 // Single token (the decode hot path): k_fused_ffn, ONE launch whose first
@@ -607,7 +607,7 @@ __global__ __launch_bounds__(kBlock) void k_down(const WT* __restrict__ wbuf,
 struct Handoff {
   unsigned* ctrl;       // the control block: FusedWs::kCtrlWords 8-byte words zeroed at the
                         // start of each call, FusedWs::kCounterStride words apart
-  uint64_t* slot;       // WR_ROUTER_IN_FFN: router slots, 2 words per expert (FusedWs::kSlotWord)
+  uint64_t* slot;       // router slots (ROUTE), 2 words per expert (FusedWs::kSlotWord)
   const float* gate_w;  // router matrix [E][h]; nullptr: the logits are read from `logits`
   int nb;               // blocks in the grid
   int rvec;             // router rows and x in 128-bit loads (else scalar)
@@ -1187,7 +1187,7 @@ constexpr size_t fused_raw_bytes() {
 #define WR_FUSED_BOUNDS __launch_bounds__(kBlock)
 #endif
 template <typename WT, typename XT, int VEC, int RPW, int U1, int RPD, int U2, bool XL,
-          bool STG, bool CLAIM = false>
+          bool STG, bool CLAIM = false, bool ROUTE = false>
 __global__ WR_FUSED_BOUNDS void k_fused_ffn(
     const WT* __restrict__ wbuf, const XT* __restrict__ x, const float* __restrict__ logits,
     float* act, XT* __restrict__ out, int32_t* __restrict__ ids_out, float* __restrict__ w_out,
@@ -1205,12 +1205,11 @@ __global__ WR_FUSED_BOUNDS void k_fused_ffn(
 
   WR_TL_MARK(hs, 0);
   TopK t;
-#if WR_ROUTER_IN_FFN
-  const bool routed = route_and_select<XT>(x, logits, g, hs, t);
-#else
-  block_select_topk(logits, g.E, g.k, g.renorm, t);
-  constexpr bool routed = true;
-#endif
+  bool routed = true;  // false: the router slots' wait expired (ROUTE)
+  if constexpr (ROUTE)
+    routed = route_and_select<XT>(x, logits, g, hs, t);
+  else
+    block_select_topk(logits, g.E, g.k, g.renorm, t);
   WR_TL_MARK(hs, 1);
 #if WR_TIMELINE
   {
@@ -1665,10 +1664,16 @@ uint64_t* tl_ptr() {
 }
 #endif
 
-// fold: the kernel computes the router rows (one launch per layer); else it
-// reads the logits an earlier router launch left in the workspace.
+// Gate/up slots per CU from which the register-path kernel takes the router
+// inside (one launch per layer).
+constexpr int kFoldSlotsPerCu = 2;
+
+// fold == nullptr: the kernel reads the logits an earlier router launch left
+// in the workspace.  Otherwise a request to compute the router rows inside
+// the kernel (one launch per layer): *fold tells whether this shape's variant
+// did, and if not nothing was launched.
 template <typename WT, typename XT, int VEC, int RPW, int U1>
-hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
+hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool* fold, hipStream_t s) {
   const Geom g = make_geom(p);
   Handoff hs;
 #if WR_TIMELINE
@@ -1677,7 +1682,7 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
 #endif
   hs.ctrl = w.ctrl;
   hs.slot = reinterpret_cast<uint64_t*>(w.ctrl + FusedWs::kSlotWord);
-  hs.gate_w = fold ? p.gate_w : nullptr;
+  hs.gate_w = fold != nullptr ? p.gate_w : nullptr;
   hs.rvec = router_vec4(p) ? 1 : 0;
   hs.cnt = w.ctrl;
   hs.timeout = w.ctrl + FusedWs::kTimeoutWord;
@@ -1704,6 +1709,10 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
   if constexpr (kXl) {
     constexpr int kBpc = kFp8 ? WR_XL_FP8_BPC : WR_XL_F16_BPC;  // MXFP4: no bound
     if (p.h <= kXlMax && (kFp4 || hs.n1 <= kBpc * cu_count())) {
+      if (fold != nullptr) {  // the x-in-LDS variants keep the router launch
+        *fold = false;
+        return hipSuccess;
+      }
       // MXFP4: block-scale bytes staged in LDS under f4_stg's conditions.
       // Measured: Mixtral 57.5 -> 55.7 us, DBRX 105.0 -> 102.0 us; DeepSeek
       // (I = 1408) 18.7 -> 19.0 us.
@@ -1739,6 +1748,10 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
     auto kc = k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, false, false, true>;
     const int n1b = gu_launch_blocks(p, hs.n1, reinterpret_cast<const void*>(kc));
     if (n1b < hs.n1) {
+      if (fold != nullptr) {  // so does the claiming variant
+        *fold = false;
+        return hipSuccess;
+      }
       hs.n1b = n1b;
       hs.nb = hs.n1b + n2;
       WR_TL_GRID(hs.nb);
@@ -1755,6 +1768,21 @@ hipError_t fused_rpw_t(const Problem& p, const FusedWs& w, bool fold, hipStream_
   } else {
     hs.nb = hs.n1 + n2;
     WR_TL_GRID(hs.nb);
+    if (fold != nullptr) {
+      // The router inside the kernel (route_and_select) pays for layers of
+      // at least kFoldSlotsPerCu gate/up slots per CU, whose gate/up phase
+      // spans rounds of resident blocks; smaller layers keep the router
+      // launch.  Measured (layer us): Mixtral 114.50 -> 113.54, DBRX 240.5 ->
+      // 239.4, Mixtral tp4 shard 42.96 -> 42.53 folded; tp8 shard 27.03 ->
+      // 27.74 and DeepSeek (claiming variant) 25.51 -> 26.37 would lose.
+      *fold = hs.n1 >= kFoldSlotsPerCu * cu_count();
+      if (!*fold) return hipSuccess;
+      hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, false, false, false, true>),
+                         dim3(hs.n1 + n2), dim3(kBlock), 0, s, static_cast<const WT*>(p.wbuf),
+                         static_cast<const XT*>(p.x), w.logits, w.act, static_cast<XT*>(p.out),
+                         p.topk_ids, p.topk_w, g, hs);
+      return hipGetLastError();
+    }
     hipLaunchKernelGGL((k_fused_ffn<WT, XT, VEC, RPW, U1, RPD, U2, false, false>),
                        dim3(hs.n1 + n2), dim3(kBlock), 0, s, static_cast<const WT*>(p.wbuf),
                        static_cast<const XT*>(p.x), w.logits, w.act, static_cast<XT*>(p.out),
@@ -1798,7 +1826,7 @@ bool f4_whole_rows(const Problem& p) {
 }
 
 template <typename WT, typename XT, int VEC>
-hipError_t fused_t(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
+hipError_t fused_t(const Problem& p, const FusedWs& w, bool* fold, hipStream_t s) {
   if (fused_rpw(p) == 4) {
     if constexpr (std::is_same<WT, fp4x2>::value && VEC == 32) {
       if (f4_whole_rows<WT, XT, VEC>(p)) return fused_rpw_t<WT, XT, VEC, 4, 2>(p, w, fold, s);
@@ -1809,7 +1837,7 @@ hipError_t fused_t(const Problem& p, const FusedWs& w, bool fold, hipStream_t s)
 }
 
 template <typename WT, typename XT, int VEC>
-hipError_t ffn_t(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
+hipError_t ffn_t(const Problem& p, const FusedWs& w, bool* fold, hipStream_t s) {
   constexpr int RPW = WR_GU_RPW, RPD = WR_DN_RPD;
   // fp8: half the chunks in flight (16 fp32 x values per chunk and lane);
   // MXFP4: one chunk (32 values), and one chunk per down tile.
@@ -1817,6 +1845,10 @@ hipError_t ffn_t(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
   constexpr int U1 = kFp4 ? 1 : (std::is_same<WT, fp8w>::value ? WR_GU_U / 2 : WR_GU_U);
   constexpr int UD = kFp4 ? 1 : WR_DN_U;
   if (p.B == 1) return fused_t<WT, XT, VEC>(p, w, fold, s);
+  if (fold != nullptr) {  // several tokens: the router runs in its own launch
+    *fold = false;
+    return hipSuccess;
+  }
   const Geom g = make_geom(p);
   const WT* wb = static_cast<const WT*>(p.wbuf);
   const int nw1 = waves_for(p.k * ((p.I + RPW - 1) / RPW), p.B);
@@ -1833,13 +1865,13 @@ hipError_t ffn_t(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
 }
 
 template <typename WT, typename XT>
-hipError_t ffn_w(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
+hipError_t ffn_w(const Problem& p, const FusedWs& w, bool* fold, hipStream_t s) {
   constexpr int V = wvec_width<WT>(), V1 = wvec_scalar<WT>();
   return p.vec == V ? ffn_t<WT, XT, V>(p, w, fold, s) : ffn_t<WT, XT, V1>(p, w, fold, s);
 }
 
 template <typename XT>
-hipError_t ffn_x(const Problem& p, const FusedWs& w, bool fold, hipStream_t s) {
+hipError_t ffn_x(const Problem& p, const FusedWs& w, bool* fold, hipStream_t s) {
   switch (p.wdt) {
     case WR_F16: return ffn_w<f16, XT>(p, w, fold, s);
     case WR_BF16: return ffn_w<bf16w, XT>(p, w, fold, s);
@@ -1861,19 +1893,25 @@ hipError_t run_route(const Problem& p, hipStream_t s) {
 }
 
 // The expert FFN from the logits run_route left in the workspace (fold =
-// false), or for one token with the router inside the FFN kernel.
-hipError_t run_ffn_only(const Problem& p, bool fold, hipStream_t s) {
+// nullptr).  With fold != nullptr, one token's FFN kernel with the router
+// inside when its variant takes it (*fold = true), else nothing (*fold =
+// false).
+hipError_t run_ffn_only(const Problem& p, bool* fold, hipStream_t s) {
   const FusedWs w = FusedWs::carve(p.ws, p.E, p.I, p.k, p.B);
   return p.adt == WR_F16 ? ffn_x<f16>(p, w, fold, s) : ffn_x<float>(p, w, fold, s);
 }
 
-// With WR_ROUTER_IN_FFN, one token takes one launch.  Otherwise the router
-// launch, then the FFN kernel(s).
+// One token whose single-token kernel takes the router inside: one launch.
+// Otherwise the router launch, then the FFN kernel(s).
 hipError_t run_ffn(const Problem& p, hipStream_t s) {
-  if (WR_ROUTER_IN_FFN && p.B == 1) return run_ffn_only(p, true, s);
+  if (p.B == 1) {
+    bool folded = false;
+    const hipError_t err = run_ffn_only(p, &folded, s);
+    if (err != hipSuccess || folded) return err;
+  }
   const hipError_t err = run_route(p, s);
   if (err != hipSuccess) return err;
-  return run_ffn_only(p, false, s);
+  return run_ffn_only(p, nullptr, s);
 }
 
 template <typename XT>
@@ -1903,7 +1941,7 @@ hipError_t launch_fused(const Problem& p, hipStream_t s) { return run_ffn(p, s);
 
 hipError_t launch_fused_route(const Problem& p, hipStream_t s) { return run_route(p, s); }
 
-hipError_t launch_fused_ffn(const Problem& p, hipStream_t s) { return run_ffn_only(p, false, s); }
+hipError_t launch_fused_ffn(const Problem& p, hipStream_t s) { return run_ffn_only(p, nullptr, s); }
 
 hipError_t launch_logits_split(const Problem& p, float* logits, f16* x_hi, f16* x_lo,
                                int32_t* x_exp, unsigned* amax, int split_bf16, hipStream_t s) {
