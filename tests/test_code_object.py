@@ -218,11 +218,31 @@ def test_single_token_kernels_keep_four_waves_per_simd(kernels):
     # 3 weight types x 2 x types x 2 RPW x 2 x paths, plus the MXFP4 kernels
     # with staged block scales (x in LDS, 4 rows per wave) for the 2 x types,
     # plus the claiming register-path variants of f16 and bf16 (2 x 2 x 2),
-    # plus the register-path variants with the router inside (3 x 2 x 2)
-    assert len(fused) == 46, sorted(fused)
+    # plus the register-path variants with the router inside (3 x 2 x 2),
+    # plus the all-resident x-in-LDS variants of f16 and bf16 (2 x 2 x 2)
+    assert len(fused) == 54, sorted(fused)
     assert all(n > 0 for n in fused.values()), "kernel descriptors not found"
     over = {k: n for k, n in fused.items() if n > 128}
     assert not over, f"single-token kernels allocating more than 128 VGPRs: {over}"
+
+
+# f16 / bf16 single-token kernels with x in LDS and half the column chunks in
+# flight (2 per down tile): the variant taken when every gate/up and down
+# block of the layer can be resident at once.
+ALL_RESIDENT = r"k_fused_ffnI(DF16_|NS_5bf16wE)(DF16_|f)Li8ELi[24]ELi[12]ELi4ELi2ELb1ELb0ELb0ELb0EEEv"
+
+
+def test_all_resident_kernels_fit_six_blocks_per_cu(kernels):
+    # x-in-LDS f16 / bf16 layers have h <= 4096 (at most 1024 down blocks of
+    # 4 rows) and at most 2 gate/up blocks per CU: on 256 CUs all of them are
+    # resident at once when 6 blocks of 4 waves fit a CU (512 VGPRs per SIMD
+    # lane, 160 KB of LDS).
+    ar = {k: (v["vgpr_alloc"], v.get("group_segment_fixed_size", 0))
+          for k, v in kernels.items() if re.search(ALL_RESIDENT, k)}
+    assert len(ar) == 8, sorted(ar)
+    assert all(n > 0 for n, _ in ar.values()), "kernel descriptors not found"
+    over = {k: (n, lds) for k, (n, lds) in ar.items() if 6 * n > 512 or 6 * lds > 160 * 1024}
+    assert not over, f"all-resident kernels fitting fewer than 6 blocks per CU: {over}"
 
 
 # MXFP4 single-token kernels with both column chunks of a row in flight
